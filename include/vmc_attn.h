@@ -1,0 +1,177 @@
+/*
+ * vmc_attn.h -- C ABI of the MI355X (gfx950) attention hot path.
+ *
+ * The drop-in boundary for vm_c's attention kernels: plain pointers, sizes
+ * and enums, no C++ or framework types.  Every entry point is stream-ordered
+ * and asynchronous (no host synchronisation, no device allocation); errors are
+ * returned as negative errno-style codes.  The C++ layer in
+ * vm_c_amd/host/ (namespace vm_c) keeps vm_c's own signatures and calls these.
+ *
+ * All pointers are device pointers unless a comment says otherwise.
+ */
+#ifndef VMC_ATTN_H
+#define VMC_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* vmc_stream_t; /* == hipStream_t */
+
+/* ---- status codes ---- */
+#define VMC_OK 0
+#define VMC_EINVAL (-22) /* bad shape / dtype / format / pointer            */
+#define VMC_ENOMEM (-12) /* caller workspace smaller than the query says    */
+#define VMC_EIO (-5)     /* HIP launch or runtime error                       */
+
+/* ---- element types of Q / K / V / O ---- */
+typedef enum { VMC_DTYPE_F16 = 0, VMC_DTYPE_BF16 = 1 } vmc_dtype;
+
+/* ---- paged KV formats (kv_cache_dtype strings "fp16", "bf16", "q8_0",
+ *      "q4_0"; the TurboQuant packed slot has its own entry points) ---- */
+typedef enum {
+    VMC_KV_F16 = 0,
+    VMC_KV_BF16 = 1,
+    VMC_KV_Q8_0 = 2, /* GGUF block_q8_0: fp16 d + 32 x int8, 34 B / 32 values */
+    VMC_KV_Q4_0 = 3  /* GGUF block_q4_0: fp16 d + 16 B nibbles, 18 B / 32     */
+} vmc_kv_format;
+
+/* "nhd": page [block][token][head][entry]; "hnd": [block][head][token][entry] */
+typedef enum { VMC_LAYOUT_NHD = 0, VMC_LAYOUT_HND = 1 } vmc_kv_layout;
+
+/* bytes of one (token, kv-head) entry of head_dim values, < 0 if invalid */
+int64_t vmc_kv_entry_bytes(int kv_format, int head_dim);
+
+/*
+ * Append K/V rows into the paged cache, quantizing on the way.
+ * Replaces vm_c::reshape_and_cache (include/vm_c/cuda/kernels_cache.h:17-27,
+ * src/cuda/cache_kernels.cu:88-157); kv_cache_dtype becomes kv_format and
+ * q8_0/q4_0 follow ggml's set_rows encoders (ggml-quants.c:234-257, :71-104).
+ *   key, value    [num_tokens][num_kv_heads][head_dim] of src_dtype
+ *   key_cache, value_cache   page pools, cache_stride bytes per block
+ *                 (0 = block_size*num_kv_heads*entry_bytes)
+ *   slot_mapping  int64 [num_tokens]; slot = block*block_size + offset, < 0 skips
+ */
+int vmc_reshape_and_cache(const void* key, const void* value, void* key_cache,
+                          void* value_cache, const int64_t* slot_mapping, int num_tokens,
+                          int num_kv_heads, int head_dim, int64_t block_size,
+                          int64_t cache_stride, int kv_format, int src_dtype, int layout,
+                          vmc_stream_t stream);
+
+/*
+ * Paged decode attention, one query token per sequence, over f16/bf16/q8_0/
+ * q4_0 pages read through the block table, split-KV with an fp32 LSE merge.
+ * Replaces vm_c::paged_attention_v1 / _v2 (include/vm_c/cuda/
+ * kernels_attention.h:30-78); semantics are those of ggml's flash_attn_ext
+ * (ggml-cpu/ops.cpp:8214-8957) on the gathered K/V, GQA head = q_head /
+ * (num_heads / num_kv_heads).
+ *   out, query    [batch][num_heads][head_dim] of q_dtype
+ *   block_tables  int32 [batch][max_num_blocks_per_req]; entries < 0 are holes
+ *   seq_lens      int32 [batch]; 0 writes a zero row
+ *   workspace     >= vmc_paged_decode_workspace_size(...) bytes
+ *   max_num_kv_splits  cap on splits per sequence (<= 0: library default)
+ * Limits: head_dim == 128, num_heads / num_kv_heads <= 16, num_kv_heads <= 16.
+ */
+size_t vmc_paged_decode_workspace_size(int batch_size, int num_heads, int head_dim,
+                                       int max_num_blocks_per_req, int block_size,
+                                       int max_num_kv_splits);
+int vmc_paged_attention_decode(void* out, const void* query, const void* key_cache,
+                               const void* value_cache, const int32_t* block_tables,
+                               const int32_t* seq_lens, int batch_size, int num_heads,
+                               int num_kv_heads, int head_dim, int block_size,
+                               int max_num_blocks_per_req, float scale, int q_dtype,
+                               int kv_format, int layout, int max_num_kv_splits,
+                               void* workspace, size_t workspace_bytes, vmc_stream_t stream);
+
+/* ---- TurboQuant packed KV (src/cuda/turboquant_kernels.cu) ---- */
+
+/* Mirrors vm_c::TQConfig (include/vm_c/cuda/kernels_turboquant.h:10-75). */
+typedef struct vmc_tq_config {
+    int head_dim;
+    int key_quant_bits;
+    int value_quant_bits;
+    int norm_correction;
+    int key_fp8;
+    int fp8_e4b15;
+    int mse_bytes;
+    int key_packed_size;
+    int val_data_bytes;
+    int value_packed_size;
+    int slot_size;
+    int slot_size_aligned;
+    int n_centroids;
+    int max_num_kv_splits;
+} vmc_tq_config;
+
+/* TQConfig::from_method: "turboquant_4bit_nc" (default), "turboquant_3bit_nc",
+ * "turboquant_k3v4_nc".  Returns VMC_EINVAL for an unknown method or for
+ * "turboquant_k8v4" (fp8 keys, not implemented). */
+int vmc_tq_config_from_method(int head_dim, const char* method, vmc_tq_config* out);
+
+/* Host-side constant tables (Lloyd-Max centroids for N(0, 1/d), midpoints),
+ * identical to src/cuda/turboquant_kernels.cu:578-623 / :662-664.  Host
+ * pointers; n_centroids floats and n_centroids-1 floats. */
+int vmc_tq_host_tables(int head_dim, int bits, float* centroids, float* midpoints);
+
+/*
+ * Quantize-on-append of K/V into packed TurboQuant slots.
+ * Replaces vm_c::turboquant_store (kernels_turboquant.h:107-119;
+ * turboquant_kernels.cu:792-860).  key/value [num_tokens][num_kv_heads]
+ * [head_dim] of half_dtype; norm, scale and zero are stored as half_dtype.
+ * One fused kernel, no workspace.
+ */
+int vmc_turboquant_store(const void* key, const void* value, void* kv_cache,
+                         const int64_t* slot_mapping, int num_tokens, int num_kv_heads,
+                         int head_dim, int64_t block_size, const vmc_tq_config* cfg,
+                         int half_dtype, vmc_stream_t stream);
+
+/*
+ * Split-KV paged decode over packed TurboQuant slots.
+ * Replaces vm_c::turboquant_decode_attention (kernels_turboquant.h:121-138;
+ * turboquant_kernels.cu:939-1007): q rotated by the Hadamard transform, K
+ * reconstructed from centroids (norm-corrected, times the stored norm), V =
+ * code*scale + zero, fp32 online softmax, LSE merge.  The caller provides the
+ * workspace (the reference grew it inside the call).
+ */
+size_t vmc_turboquant_decode_workspace_size(int batch_size, int num_heads, int head_dim,
+                                            int64_t max_num_blocks_per_req,
+                                            int64_t block_size, int max_num_kv_splits);
+int vmc_turboquant_decode_attention(void* output, const void* query, const void* kv_cache,
+                                    const int32_t* block_tables, const int32_t* seq_lens,
+                                    int batch_size, int num_heads, int num_kv_heads,
+                                    int head_dim, float scale, int64_t block_size,
+                                    int64_t max_num_blocks_per_req, const vmc_tq_config* cfg,
+                                    int half_dtype, int max_num_kv_splits, void* workspace,
+                                    size_t workspace_bytes, vmc_stream_t stream);
+
+/*
+ * Causal flash-attention prefill over contiguous ("local") K/V, bf16 or fp16,
+ * MFMA for QK^T and PV, fp32 softmax.  Each sequence's tokens are contiguous
+ * with positions 0..n-1, so token t attends tokens [t - pos(t), t].
+ * Replaces vm_c::flash_attention_prefill_local (include/vm_c/cuda/
+ * kernels_flash_attn.h:81-93).
+ *   output, query [num_tokens][num_heads][head_dim]; key, value
+ *   [num_tokens][num_kv_heads][head_dim]; token_positions int32 [num_tokens].
+ * Optional fused quantize-on-append: when key_cache != NULL the same launch
+ * writes every K/V row into the paged cache (kv_format/layout as in
+ * vmc_reshape_and_cache, slot_mapping int64 [num_tokens]).
+ * Limits: head_dim == 128, num_heads % num_kv_heads == 0.
+ */
+int vmc_flash_attention_prefill(void* output, const void* query, const void* key,
+                                const void* value, int num_tokens, int num_heads,
+                                int num_kv_heads, int head_dim, float scale,
+                                const int32_t* token_positions, int dtype, void* key_cache,
+                                void* value_cache, const int64_t* slot_mapping,
+                                int64_t block_size, int kv_format, int layout,
+                                vmc_stream_t stream);
+
+/* Library self-description: "vmc_attn <version> gfx950". */
+const char* vmc_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VMC_ATTN_H */

@@ -1,0 +1,944 @@
+/*
+ * vmc_oracle.c -- CPU restatement of vm_c's attention hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker): loaded by tests/, by
+ * __graft_entry__.smoke() and by bench.py's cpu_baseline leg, never by the
+ * product path.  Built with -ffp-contract=off so every a*b+c below is two
+ * roundings unless written as fmaf(): the CUDA reference was compiled by nvcc
+ * with its default --fmad=true, so the places where nvcc contracted are
+ * written as explicit fmaf() and cited.
+ *
+ * Parity status per function is recorded in vmc_oracle.h and DESIGN.md.
+ */
+#include "vmc_oracle.h"
+
+#include <float.h>
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* scalar conversions                                                       */
+/* ------------------------------------------------------------------------ */
+
+uint16_t orc_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t exp = (x >> 23) & 0xffu;
+    uint32_t mant = x & 0x7fffffu;
+    if (exp == 0xffu) return (uint16_t)(sign | 0x7c00u | (mant ? (0x200u | (mant >> 13)) : 0u));
+    const int e = (int)exp - 127 + 15;
+    if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        mant |= 0x800000u;
+        const int shift = 14 - e;
+        uint32_t hm = mant >> shift;
+        const uint32_t rem = mant & ((1u << shift) - 1u);
+        const uint32_t halfway = 1u << (shift - 1);
+        if (rem > halfway || (rem == halfway && (hm & 1u))) hm++;
+        return (uint16_t)(sign | hm);
+    }
+    uint32_t h = sign | ((uint32_t)e << 10) | (mant >> 13);
+    const uint32_t rem = mant & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+    return (uint16_t)h;
+}
+
+float orc_f16_to_f32(uint16_t h) {
+    const uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    const uint32_t exp = ((uint32_t)h >> 10) & 0x1fu;
+    uint32_t mant = (uint32_t)h & 0x3ffu;
+    uint32_t x;
+    if (exp == 0) {
+        if (mant == 0) {
+            x = sign;
+        } else {
+            int e = -1;
+            do { mant <<= 1; e++; } while (!(mant & 0x400u));
+            mant &= 0x3ffu;
+            x = sign | ((uint32_t)(127 - 15 - e) << 23) | (mant << 13);
+        }
+    } else if (exp == 0x1fu) {
+        x = sign | 0x7f800000u | (mant << 13);
+    } else {
+        x = sign | ((exp + 127u - 15u) << 23) | (mant << 13);
+    }
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
+uint16_t orc_f32_to_bf16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
+    x += 0x7fffu + ((x >> 16) & 1u);
+    return (uint16_t)(x >> 16);
+}
+
+float orc_bf16_to_f32(uint16_t h) {
+    const uint32_t x = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
+void orc_f32_to_f16_n(const float* x, uint16_t* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = orc_f32_to_f16(x[i]);
+}
+
+void orc_f16_to_f32_n(const uint16_t* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = orc_f16_to_f32(x[i]);
+}
+
+static inline float half_to_f32(uint16_t h, int bf16) {
+    return bf16 ? orc_bf16_to_f32(h) : orc_f16_to_f32(h);
+}
+static inline uint16_t f32_to_half(float f, int bf16) {
+    return bf16 ? orc_f32_to_bf16(f) : orc_f32_to_f16(f);
+}
+
+/* ------------------------------------------------------------------------ */
+/* GGUF q8_0 / q4_0                                                         */
+/* ------------------------------------------------------------------------ */
+
+enum { QK = 32, Q8_0_BYTES = 34, Q4_0_BYTES = 18 };
+
+/* ggml/src/ggml-quants.c:234-257 (quantize_row_q8_0_ref): d = amax/127,
+ * id = d ? 1/d : 0, qs = roundf(x*id) (half away from zero), d stored fp16. */
+void orc_quantize_row_q8_0(const float* x, void* yv, int64_t k) {
+    uint8_t* y = (uint8_t*)yv;
+    for (int64_t i = 0; i < k / QK; ++i) {
+        const float* xb = x + i * QK;
+        float amax = 0.0f;
+        for (int j = 0; j < QK; ++j) {
+            const float a = fabsf(xb[j]);
+            amax = amax > a ? amax : a;
+        }
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        const uint16_t dh = orc_f32_to_f16(d);
+        uint8_t* blk = y + i * Q8_0_BYTES;
+        blk[0] = (uint8_t)(dh & 0xff);
+        blk[1] = (uint8_t)(dh >> 8);
+        for (int j = 0; j < QK; ++j) blk[2 + j] = (uint8_t)(int8_t)roundf(xb[j] * id);
+    }
+}
+
+/* ggml/src/ggml-quants.c:491-503 */
+void orc_dequantize_row_q8_0(const void* xv, float* y, int64_t k) {
+    const uint8_t* x = (const uint8_t*)xv;
+    for (int64_t i = 0; i < k / QK; ++i) {
+        const uint8_t* blk = x + i * Q8_0_BYTES;
+        const float d = orc_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+        for (int j = 0; j < QK; ++j) y[i * QK + j] = (float)(int8_t)blk[2 + j] * d;
+    }
+}
+
+/* ggml/src/ggml-quants.c:71-104 (quantize_row_q4_0_ref): max = signed value of
+ * largest |x| (first wins), d = max/-8, q = min(15, (int8_t)(x*id + 8.5f)),
+ * qs[j] = q[j] | q[j+16] << 4.  x*id and +8.5f are separate roundings (the
+ * ggml CPU build has no FMA). */
+void orc_quantize_row_q4_0(const float* x, void* yv, int64_t k) {
+    uint8_t* y = (uint8_t*)yv;
+    for (int64_t i = 0; i < k / QK; ++i) {
+        const float* xb = x + i * QK;
+        float amax = 0.0f, max = 0.0f;
+        for (int j = 0; j < QK; ++j) {
+            const float v = xb[j];
+            if (amax < fabsf(v)) { amax = fabsf(v); max = v; }
+        }
+        const float d = max / -8.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        const uint16_t dh = orc_f32_to_f16(d);
+        uint8_t* blk = y + i * Q4_0_BYTES;
+        blk[0] = (uint8_t)(dh & 0xff);
+        blk[1] = (uint8_t)(dh >> 8);
+        for (int j = 0; j < QK / 2; ++j) {
+            volatile float x0 = xb[j] * id;
+            volatile float x1 = xb[QK / 2 + j] * id;
+            const int8_t t0 = (int8_t)(x0 + 8.5f);
+            const int8_t t1 = (int8_t)(x1 + 8.5f);
+            const uint8_t q0 = (uint8_t)(t0 < 15 ? t0 : 15);
+            const uint8_t q1 = (uint8_t)(t1 < 15 ? t1 : 15);
+            blk[2 + j] = (uint8_t)(q0 | (q1 << 4));
+        }
+    }
+}
+
+/* ggml/src/ggml-quants.c:397-414 */
+void orc_dequantize_row_q4_0(const void* xv, float* y, int64_t k) {
+    const uint8_t* x = (const uint8_t*)xv;
+    for (int64_t i = 0; i < k / QK; ++i) {
+        const uint8_t* blk = x + i * Q4_0_BYTES;
+        const float d = orc_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+        for (int j = 0; j < QK / 2; ++j) {
+            y[i * QK + j] = (float)((blk[2 + j] & 0x0f) - 8) * d;
+            y[i * QK + QK / 2 + j] = (float)((blk[2 + j] >> 4) - 8) * d;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* paged KV (src/cuda/cache_kernels.cu:14-54 addressing; q8_0/q4_0 rows as  */
+/* written by ggml_set_rows, ggml/src/ggml-cpu/ops.cpp:4950-5020)           */
+/* ------------------------------------------------------------------------ */
+
+int64_t orc_kv_entry_bytes(int fmt, int head_dim) {
+    switch (fmt) {
+        case ORC_KV_F16:
+        case ORC_KV_BF16: return (int64_t)head_dim * 2;
+        case ORC_KV_Q8_0: return (int64_t)(head_dim / QK) * Q8_0_BYTES;
+        case ORC_KV_Q4_0: return (int64_t)(head_dim / QK) * Q4_0_BYTES;
+        default: return -1;
+    }
+}
+
+static inline int64_t kv_entry_offset(int64_t slot, int h, int64_t bs, int Hkv,
+                                      int64_t E, int hnd) {
+    const int64_t blk = slot / bs, off = slot % bs;
+    const int64_t stride = bs * Hkv * E;
+    return hnd ? blk * stride + (int64_t)h * bs * E + off * E
+               : blk * stride + off * Hkv * E + (int64_t)h * E;
+}
+
+static void encode_entry(const uint16_t* src, int src_bf16, uint8_t* dst, int fmt,
+                         int D, float* tmp) {
+    if (fmt == ORC_KV_F16 || fmt == ORC_KV_BF16) {
+        uint16_t* d16 = (uint16_t*)dst;
+        for (int d = 0; d < D; ++d) {
+            const float v = half_to_f32(src[d], src_bf16);
+            /* same-type copy is a bit copy (cache_kernels.cu:49-50) */
+            d16[d] = ((fmt == ORC_KV_BF16) == (src_bf16 != 0)) ? src[d]
+                                                               : f32_to_half(v, fmt == ORC_KV_BF16);
+        }
+        return;
+    }
+    for (int d = 0; d < D; ++d) tmp[d] = half_to_f32(src[d], src_bf16);
+    if (fmt == ORC_KV_Q8_0) orc_quantize_row_q8_0(tmp, dst, D);
+    else orc_quantize_row_q4_0(tmp, dst, D);
+}
+
+void orc_kv_append(const uint16_t* key, const uint16_t* value, int src_bf16,
+                   uint8_t* key_cache, uint8_t* value_cache,
+                   const int64_t* slot_mapping, int num_tokens, int num_kv_heads,
+                   int head_dim, int64_t block_size, int fmt, int hnd) {
+    const int64_t E = orc_kv_entry_bytes(fmt, head_dim);
+    float* tmp = (float*)malloc(sizeof(float) * (size_t)head_dim);
+    for (int t = 0; t < num_tokens; ++t) {
+        const int64_t slot = slot_mapping[t];
+        if (slot < 0) continue; /* cache_kernels.cu:26 */
+        for (int h = 0; h < num_kv_heads; ++h) {
+            const int64_t src = ((int64_t)t * num_kv_heads + h) * head_dim;
+            const int64_t off = kv_entry_offset(slot, h, block_size, num_kv_heads, E, hnd);
+            encode_entry(key + src, src_bf16, key_cache + off, fmt, head_dim, tmp);
+            encode_entry(value + src, src_bf16, value_cache + off, fmt, head_dim, tmp);
+        }
+    }
+    free(tmp);
+}
+
+void orc_kv_dequant_entry(const uint8_t* e, int fmt, int D, float* out) {
+    if (fmt == ORC_KV_F16 || fmt == ORC_KV_BF16) {
+        for (int d = 0; d < D; ++d) {
+            const uint16_t h = (uint16_t)(e[2 * d] | (e[2 * d + 1] << 8));
+            out[d] = half_to_f32(h, fmt == ORC_KV_BF16);
+        }
+    } else if (fmt == ORC_KV_Q8_0) {
+        orc_dequantize_row_q8_0(e, out, D);
+    } else {
+        orc_dequantize_row_q4_0(e, out, D);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* TurboQuant                                                               */
+/* ------------------------------------------------------------------------ */
+
+/* include/vm_c/cuda/kernels_turboquant.h:29-74 (compute_layout/from_method);
+ * include/vm_c/memory/kv_cache_manager.hpp:121-162.  Only the codebook
+ * methods are restated here (k8v4 stores fp8 keys). */
+int orc_tq_layout_from_method(int head_dim, const char* method, orc_tq_layout* L) {
+    memset(L, 0, sizeof(*L));
+    L->head_dim = head_dim;
+    L->norm_correction = 1;
+    if (method && strcmp(method, "turboquant_k3v4_nc") == 0) {
+        L->key_quant_bits = 3; L->value_quant_bits = 4;
+    } else if (method && strcmp(method, "turboquant_3bit_nc") == 0) {
+        L->key_quant_bits = 3; L->value_quant_bits = 3;
+    } else if (!method || strcmp(method, "turboquant_4bit_nc") == 0 ||
+               strcmp(method, "") == 0) {
+        L->key_quant_bits = 4; L->value_quant_bits = 4;
+    } else {
+        return -1;
+    }
+    L->n_centroids = 1 << L->key_quant_bits;
+    L->mse_bytes = (head_dim * L->key_quant_bits + 7) / 8;
+    L->key_packed_size = L->mse_bytes + 2;
+    L->val_data_bytes = (head_dim * L->value_quant_bits + 7) / 8;
+    L->value_packed_size = L->val_data_bytes + 4;
+    L->slot_size = L->key_packed_size + L->value_packed_size;
+    L->slot_size_aligned = L->slot_size + (L->slot_size % 2);
+    return 0;
+}
+
+/* src/cuda/turboquant_kernels.cu:551-570 (build_hadamard_on_host): Sylvester
+ * doubling, then every entry times 1.0f/sqrtf(d). */
+void orc_tq_hadamard(float* out, int d) {
+    const float inv_sqrt_d = 1.0f / sqrtf((float)d);
+    for (int i = 0; i < d; ++i)
+        for (int j = 0; j < d; ++j)
+            out[i * d + j] = (__builtin_popcount((unsigned)(i & j)) & 1) ? -inv_sqrt_d : inv_sqrt_d;
+}
+
+/* src/cuda/turboquant_kernels.cu:572-576 */
+static float gaussian_pdf(float x, float sigma2) {
+    return (1.0f / sqrtf(2.0f * 3.14159265358979f * sigma2)) * expf(-x * x / (2.0f * sigma2));
+}
+
+/* src/cuda/turboquant_kernels.cu:578-623 (solve_lloyd_max_centroids): N(0,1/d)
+ * Lloyd-Max, init uniform centres on [-3.5s, 3.5s], outer edges +-10.5s,
+ * 201-point trapezoid per cell, <= 200 iterations, tolerance 1e-10, sorted. */
+void orc_tq_lloyd_max(float* centroids_out, int d, int bits) {
+    const int n = 1 << bits;
+    const float sigma2 = 1.0f / (float)d;
+    const float sigma = sqrtf(sigma2);
+    const float lo = -3.5f * sigma, hi = 3.5f * sigma;
+    float c[256], nc[256], edges[257];
+    for (int i = 0; i < n; ++i) c[i] = lo + (hi - lo) * ((float)i + 0.5f) / (float)n;
+    for (int iter = 0; iter < 200; ++iter) {
+        edges[0] = lo * 3.0f;
+        for (int i = 0; i < n - 1; ++i) edges[i + 1] = (c[i] + c[i + 1]) * 0.5f;
+        edges[n] = hi * 3.0f;
+        int converged = 1;
+        for (int i = 0; i < n; ++i) {
+            const int n_trap = 200;
+            const float a = edges[i], b = edges[i + 1];
+            const float step = (b - a) / (float)n_trap;
+            float num = 0.0f, den = 0.0f;
+            for (int j = 0; j <= n_trap; ++j) {
+                const float x = a + (float)j * step;
+                const float p = gaussian_pdf(x, sigma2);
+                const float w = (j == 0 || j == n_trap) ? 0.5f : 1.0f;
+                den += w * p;
+                num += w * x * p;
+            }
+            num *= step;
+            den *= step;
+            nc[i] = (den > 1e-15f) ? num / den : c[i];
+            if (fabsf(nc[i] - c[i]) > 1e-10f) converged = 0;
+        }
+        memcpy(c, nc, sizeof(float) * (size_t)n);
+        if (converged) break;
+    }
+    /* std::sort ascending (:621) */
+    for (int i = 1; i < n; ++i) {
+        const float v = c[i];
+        int j = i - 1;
+        while (j >= 0 && c[j] > v) { c[j + 1] = c[j]; --j; }
+        c[j + 1] = v;
+    }
+    memcpy(centroids_out, c, sizeof(float) * (size_t)n);
+}
+
+/* src/cuda/turboquant_kernels.cu:662-664 */
+void orc_tq_midpoints(const float* c, int n, float* mid) {
+    for (int i = 0; i < n - 1; ++i) mid[i] = (c[i] + c[i + 1]) * 0.5f;
+}
+
+/* Declared order for y = H x (the reference used cublasSgemm, :841-848, whose
+ * summation order is unspecified): butterflies of half-width 1, 2, ..., d/2
+ * on (a, b) -> (a + b, a - b), then a single multiply by 1.0f/sqrtf(d), the
+ * same fp32 constant build_hadamard_on_host scales H by (:568). */
+void orc_tq_rotate(const float* x, const float* signs, float* y, int d) {
+    for (int i = 0; i < d; ++i) y[i] = signs ? x[i] * signs[i] : x[i];
+    for (int h = 1; h < d; h <<= 1) {
+        for (int i = 0; i < d; i += 2 * h) {
+            for (int j = i; j < i + h; ++j) {
+                const float a = y[j], b = y[j + h];
+                y[j] = a + b;
+                y[j + h] = a - b;
+            }
+        }
+    }
+    const float c = 1.0f / sqrtf((float)d);
+    for (int i = 0; i < d; ++i) y[i] = y[i] * c;
+}
+
+static inline void put_half(uint8_t* p, float v, int bf16) {
+    const uint16_t b = f32_to_half(v, bf16);
+    p[0] = (uint8_t)(b & 0xff);
+    p[1] = (uint8_t)(b >> 8);
+}
+static inline float get_half(const uint8_t* p, int bf16) {
+    return half_to_f32((uint16_t)(p[0] | (p[1] << 8)), bf16);
+}
+
+/* pack codes: 4-bit -> even d low nibble (:278-292); 3-bit -> 8 codes per 3
+ * bytes little-endian, code i at bits 3i (:293-310, :335-347). */
+static void pack_codes(const int* q, int D, int bits, uint8_t* dst) {
+    if (bits == 4) {
+        for (int d = 0; d < D; d += 2) dst[d / 2] = (uint8_t)((q[d] & 0xf) | ((q[d + 1] & 0xf) << 4));
+    } else {
+        for (int g = 0; g < D / 8; ++g) {
+            int packed = 0;
+            for (int i = 0; i < 8; ++i) packed |= (q[g * 8 + i] & 0x7) << (i * 3);
+            dst[g * 3] = (uint8_t)(packed & 0xff);
+            dst[g * 3 + 1] = (uint8_t)((packed >> 8) & 0xff);
+            dst[g * 3 + 2] = (uint8_t)((packed >> 16) & 0xff);
+        }
+    }
+}
+
+static void unpack_codes(const uint8_t* src, int D, int bits, int* q) {
+    if (bits == 4) {
+        for (int d = 0; d < D; d += 2) { q[d] = src[d / 2] & 0xf; q[d + 1] = src[d / 2] >> 4; }
+    } else {
+        for (int g = 0; g < D / 8; ++g) {
+            const int packed = src[g * 3] | (src[g * 3 + 1] << 8) | (src[g * 3 + 2] << 16);
+            for (int i = 0; i < 8; ++i) q[g * 8 + i] = (packed >> (i * 3)) & 0x7;
+        }
+    }
+}
+
+/* src/cuda/turboquant_kernels.cu:792-860 (turboquant_store) ->
+ *   half_to_float_norm_kernel :145-161  norm = sqrtf(sum k*k), the sum a
+ *                                       sequential fmaf chain (nvcc contracts);
+ *   normalize_kernel :163-175           x = k * (1/(norm + 1e-8f));
+ *   cublasSgemm :841-848                y = H x (declared order, orc_tq_rotate);
+ *   tq_store_mse_kernel :247-351        codes = #midpoints <= y (scan :283-304),
+ *                                       norm fp16 at +mse_bytes (:312);
+ *                                       V min/max asymmetric codes (:314-347),
+ *                                       scale, zero at +val_data(+2) (:349-350). */
+void orc_tq_store(const uint16_t* key, const uint16_t* value, uint8_t* kv_cache,
+                  const int64_t* slot_mapping, int num_tokens, int num_kv_heads,
+                  int head_dim, int64_t block_size, const orc_tq_layout* L,
+                  const float* midpoints, int bf16) {
+    const int D = head_dim;
+    float kf[256], xh[256], y[256], vf[256];
+    int q[256];
+    for (int t = 0; t < num_tokens; ++t) {
+        const int64_t slot = slot_mapping[t];
+        if (slot < 0) continue; /* :266-267 */
+        const int64_t blk = slot / block_size, off = slot % block_size;
+        for (int h = 0; h < num_kv_heads; ++h) {
+            const int64_t pid = (int64_t)t * num_kv_heads + h;
+            /* compute_slot_byte_offset :39-45 */
+            uint8_t* sp = kv_cache + blk * block_size * num_kv_heads * L->slot_size_aligned +
+                          off * num_kv_heads * L->slot_size_aligned +
+                          (int64_t)h * L->slot_size_aligned;
+            float norm_sq = 0.0f;
+            for (int d = 0; d < D; ++d) {
+                kf[d] = half_to_f32(key[pid * D + d], bf16);
+                norm_sq = fmaf(kf[d], kf[d], norm_sq);
+            }
+            const float norm = sqrtf(norm_sq);
+            const float inv_norm = 1.0f / (norm + 1e-8f);
+            for (int d = 0; d < D; ++d) xh[d] = kf[d] * inv_norm;
+            orc_tq_rotate(xh, NULL, y, D);
+            const int nc = L->n_centroids;
+            for (int d = 0; d < D; ++d) {
+                int idx = 0;
+                for (int c = nc - 2; c >= 0; --c) {
+                    if (y[d] >= midpoints[c]) { idx = c + 1; break; }
+                }
+                q[d] = idx < nc - 1 ? idx : nc - 1;
+            }
+            pack_codes(q, D, L->key_quant_bits, sp);
+            put_half(sp + L->mse_bytes, norm, bf16);
+
+            float vmin = FLT_MAX, vmax = -FLT_MAX;
+            for (int d = 0; d < D; ++d) {
+                vf[d] = half_to_f32(value[pid * D + d], bf16);
+                vmin = fminf(vmin, vf[d]);
+                vmax = fmaxf(vmax, vf[d]);
+            }
+            const int vmaxq = L->value_quant_bits == 4 ? 15 : 7;
+            float vscale = (vmax - vmin) / (float)vmaxq;
+            vscale = fmaxf(vscale, 1e-8f);
+            for (int d = 0; d < D; ++d) {
+                int qq = (int)roundf((vf[d] - vmin) / vscale);
+                qq = qq < 0 ? 0 : (qq > vmaxq ? vmaxq : qq);
+                q[d] = qq;
+            }
+            uint8_t* vp = sp + L->key_packed_size;
+            pack_codes(q, D, L->value_quant_bits, vp);
+            put_half(vp + L->val_data_bytes, vscale, bf16);
+            put_half(vp + L->val_data_bytes + 2, vmin, bf16);
+        }
+    }
+}
+
+/* Dequantisation of tq_decode_stage1_kernel :416-483. */
+void orc_tq_dequant_slot(const uint8_t* sp, const orc_tq_layout* L, const float* C,
+                         int bf16, float* k_out, float* v_out) {
+    const int D = L->head_dim;
+    int q[256];
+    unpack_codes(sp, D, L->key_quant_bits, q);
+    for (int d = 0; d < D; ++d) k_out[d] = C[q[d]];
+    if (L->norm_correction) {
+        float c_norm_sq = 0.0f;
+        for (int d = 0; d < D; ++d) c_norm_sq = fmaf(k_out[d], k_out[d], c_norm_sq);
+        const float c_inv = 1.0f / sqrtf(c_norm_sq + 1e-16f);
+        for (int d = 0; d < D; ++d) k_out[d] *= c_inv;
+    }
+    const float vec_norm = get_half(sp + L->mse_bytes, bf16);
+    for (int d = 0; d < D; ++d) k_out[d] *= vec_norm;
+    const uint8_t* vp = sp + L->key_packed_size;
+    const float vs = get_half(vp + L->val_data_bytes, bf16);
+    const float vz = get_half(vp + L->val_data_bytes + 2, bf16);
+    unpack_codes(vp, D, L->value_quant_bits, q);
+    for (int d = 0; d < D; ++d) v_out[d] = fmaf((float)q[d], vs, vz);
+}
+
+static inline const uint8_t* tq_slot_ptr(const uint8_t* cache, int64_t blk, int64_t off,
+                                         int h, int64_t bs, int Hkv, int S) {
+    return cache + blk * bs * Hkv * S + off * Hkv * S + (int64_t)h * S;
+}
+
+/* src/cuda/turboquant_kernels.cu:939-1007 (turboquant_decode_attention):
+ * q -> fp32 (:968), q_rot = H q (:975-982, declared order), stage 1 per
+ * (b, h, split) (:353-506) executed once, stage 2 LSE merge (:508-547).
+ * A split with no tokens has zero weight (the reference leaves it unwritten,
+ * :380).  seq_len <= 0 writes zeros (the reference writes nothing, :375).
+ * Tokens whose block-table entry is < 0 contribute nothing (:402). */
+void orc_tq_decode(uint16_t* out, const uint16_t* query, const uint8_t* kv_cache,
+                   const int32_t* block_tables, const int32_t* seq_lens,
+                   int B, int Hq, int Hkv, int D, float scale, int64_t bs,
+                   int64_t max_blocks, const orc_tq_layout* L, const float* C,
+                   int ns, int bf16, int nthreads) {
+    const int kv_group = Hq / Hkv;
+    const int BLOCK_KV = 4;
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel for schedule(dynamic)
+#endif
+    for (int bh = 0; bh < B * Hq; ++bh) {
+        const int b = bh / Hq, h = bh % Hq;
+        const int kv_head = h / kv_group;
+        const int seq_len = seq_lens[b];
+        uint16_t* o = out + (int64_t)bh * D;
+        if (seq_len <= 0) {
+            for (int d = 0; d < D; ++d) o[d] = f32_to_half(0.0f, bf16);
+            continue;
+        }
+        float qf[256], qr[256], acc[256], kr[256], vr[4][256], s[4], merge[256];
+        float* mid = (float*)malloc(sizeof(float) * (size_t)ns * (size_t)(D + 1));
+        int* valid = (int*)malloc(sizeof(int) * (size_t)ns);
+        for (int d = 0; d < D; ++d) qf[d] = half_to_f32(query[(int64_t)bh * D + d], bf16);
+        orc_tq_rotate(qf, NULL, qr, D);
+        const int split_len = (seq_len + ns - 1) / ns;
+        for (int sid = 0; sid < ns; ++sid) {
+            const int start = split_len * sid;
+            const int end = start + split_len < seq_len ? start + split_len : seq_len;
+            valid[sid] = start < end;
+            if (!valid[sid]) continue;
+            for (int d = 0; d < D; ++d) acc[d] = 0.0f;
+            float m_prev = -FLT_MAX, l_prev = 0.0f;
+            for (int sn = start; sn < end; sn += BLOCK_KV) {
+                const int en = sn + BLOCK_KV < end ? sn + BLOCK_KV : end;
+                int cnt = 0;
+                for (int pos = sn; pos < en; ++pos) {
+                    const int32_t blk = block_tables[(int64_t)b * max_blocks + pos / bs];
+                    if (blk < 0) continue;
+                    const uint8_t* sp = tq_slot_ptr(kv_cache, blk, pos % bs, kv_head, bs, Hkv,
+                                                    L->slot_size_aligned);
+                    orc_tq_dequant_slot(sp, L, C, bf16, kr, vr[cnt]);
+                    float dot = 0.0f;
+                    for (int d = 0; d < D; ++d) dot = fmaf(qr[d], kr[d], dot);
+                    s[cnt] = dot * scale;
+                    cnt++;
+                }
+                if (cnt == 0) continue;
+                float bmax = -FLT_MAX;
+                for (int n = 0; n < cnt; ++n) bmax = fmaxf(bmax, s[n]);
+                const float new_max = fmaxf(m_prev, bmax);
+                const float re = expf(m_prev - new_max);
+                for (int d = 0; d < D; ++d) acc[d] *= re;
+                l_prev *= re;
+                for (int n = 0; n < cnt; ++n) {
+                    const float p = expf(s[n] - new_max);
+                    l_prev += p;
+                    for (int d = 0; d < D; ++d) acc[d] = fmaf(p, vr[n][d], acc[d]);
+                }
+                m_prev = new_max;
+            }
+            float* mo = mid + (int64_t)sid * (D + 1);
+            const float safe_l = l_prev > 0.0f ? l_prev : 1.0f;
+            for (int d = 0; d < D; ++d) mo[d] = acc[d] / safe_l;
+            mo[D] = m_prev + logf(safe_l);
+        }
+        float max_lse = -FLT_MAX;
+        for (int sid = 0; sid < ns; ++sid)
+            if (valid[sid]) max_lse = fmaxf(max_lse, mid[(int64_t)sid * (D + 1) + D]);
+        for (int d = 0; d < D; ++d) merge[d] = 0.0f;
+        float sum_exp = 0.0f;
+        for (int sid = 0; sid < ns; ++sid) {
+            if (!valid[sid]) continue;
+            const float* mo = mid + (int64_t)sid * (D + 1);
+            const float w = expf(mo[D] - max_lse);
+            sum_exp += w;
+            for (int d = 0; d < D; ++d) merge[d] = fmaf(w, mo[d], merge[d]);
+        }
+        const float inv_sum = 1.0f / (sum_exp + 1e-8f);
+        for (int d = 0; d < D; ++d) o[d] = f32_to_half(merge[d] * inv_sum, bf16);
+        free(mid);
+        free(valid);
+    }
+}
+
+/* exact fp64 softmax(q k^T * scale) v over rows k[n][D], v[n][D] */
+static void softmax_av_exact(const double* qd, const double* K, const double* V, int n,
+                             int D, double scale, double* out) {
+    double m = -INFINITY;
+    double* s = (double*)malloc(sizeof(double) * (size_t)(n > 0 ? n : 1));
+    for (int i = 0; i < n; ++i) {
+        double dot = 0.0;
+        for (int d = 0; d < D; ++d) dot += qd[d] * K[(int64_t)i * D + d];
+        s[i] = dot * scale;
+        if (s[i] > m) m = s[i];
+    }
+    double l = 0.0;
+    for (int d = 0; d < D; ++d) out[d] = 0.0;
+    for (int i = 0; i < n; ++i) {
+        const double p = exp(s[i] - m);
+        l += p;
+        for (int d = 0; d < D; ++d) out[d] += p * V[(int64_t)i * D + d];
+    }
+    for (int d = 0; d < D; ++d) out[d] = n > 0 ? out[d] / l : 0.0;
+    free(s);
+}
+
+void orc_tq_decode_exact(double* out, const uint16_t* query, const uint8_t* kv_cache,
+                         const int32_t* block_tables, const int32_t* seq_lens,
+                         int B, int Hq, int Hkv, int D, double scale, int64_t bs,
+                         int64_t max_blocks, const orc_tq_layout* L, const float* C,
+                         int bf16, int nthreads) {
+    const int kv_group = Hq / Hkv;
+    const double c = 1.0 / sqrt((double)D);
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel for schedule(dynamic)
+#endif
+    for (int bh = 0; bh < B * Hq; ++bh) {
+        const int b = bh / Hq, h = bh % Hq, kvh = h / kv_group;
+        const int n = seq_lens[b] > 0 ? seq_lens[b] : 0;
+        double* K = (double*)malloc(sizeof(double) * (size_t)(n + 1) * (size_t)D);
+        double* V = (double*)malloc(sizeof(double) * (size_t)(n + 1) * (size_t)D);
+        double qd[256], qr[256];
+        float kr[256], vr[256];
+        int cnt = 0;
+        for (int pos = 0; pos < n; ++pos) {
+            const int32_t blk = block_tables[(int64_t)b * max_blocks + pos / bs];
+            if (blk < 0) continue;
+            const uint8_t* sp = tq_slot_ptr(kv_cache, blk, pos % bs, kvh, bs, Hkv,
+                                            L->slot_size_aligned);
+            /* exact dequant: centroid / ||centroids|| * norm, code*scale + zero */
+            int qc[256];
+            unpack_codes(sp, D, L->key_quant_bits, qc);
+            double cn = 0.0;
+            for (int d = 0; d < D; ++d) cn += (double)C[qc[d]] * (double)C[qc[d]];
+            const double ci = L->norm_correction ? 1.0 / sqrt(cn + 1e-16) : 1.0;
+            const double nrm = get_half(sp + L->mse_bytes, bf16);
+            for (int d = 0; d < D; ++d) K[(int64_t)cnt * D + d] = (double)C[qc[d]] * ci * nrm;
+            const uint8_t* vp = sp + L->key_packed_size;
+            const double vs = get_half(vp + L->val_data_bytes, bf16);
+            const double vz = get_half(vp + L->val_data_bytes + 2, bf16);
+            unpack_codes(vp, D, L->value_quant_bits, qc);
+            for (int d = 0; d < D; ++d) V[(int64_t)cnt * D + d] = qc[d] * vs + vz;
+            cnt++;
+        }
+        (void)kr; (void)vr;
+        for (int d = 0; d < D; ++d) qd[d] = half_to_f32(query[(int64_t)bh * D + d], bf16);
+        for (int i = 0; i < D; ++i) {
+            double acc = 0.0;
+            for (int j = 0; j < D; ++j)
+                acc += ((__builtin_popcount((unsigned)(i & j)) & 1) ? -c : c) * qd[j];
+            qr[i] = acc;
+        }
+        softmax_av_exact(qr, K, V, cnt, D, scale, out + (int64_t)bh * D);
+        free(K);
+        free(V);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* paged decode over f16 / bf16 / q8_0 / q4_0 pages                         */
+/* ------------------------------------------------------------------------ */
+
+/* Gather one sequence's K (or V) entries for kv-head h through the block
+ * table: row i = token i.  Returns the number of tokens gathered (tokens
+ * whose block-table entry is < 0 are dropped). */
+static int gather_entries(const uint8_t* cache, int fmt, int hnd, const int32_t* bt,
+                          int seq_len, int h, int Hkv, int D, int64_t bs,
+                          uint8_t* dst) {
+    const int64_t E = orc_kv_entry_bytes(fmt, D);
+    int cnt = 0;
+    for (int pos = 0; pos < seq_len; ++pos) {
+        const int32_t blk = bt[pos / bs];
+        if (blk < 0) continue;
+        const int64_t off = kv_entry_offset((int64_t)blk * bs + pos % bs, h, bs, Hkv, E, hnd);
+        memcpy(dst + (int64_t)cnt * E, cache + off, (size_t)E);
+        cnt++;
+    }
+    return cnt;
+}
+
+void orc_paged_decode_exact(double* out, const float* q, const uint8_t* kc,
+                            const uint8_t* vc, int fmt, int hnd, const int32_t* bt,
+                            const int32_t* seq_lens, int B, int Hq, int Hkv, int D,
+                            double scale, int64_t bs, int64_t max_blocks, int nthreads) {
+    const int kv_group = Hq / Hkv;
+    const int64_t E = orc_kv_entry_bytes(fmt, D);
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel for schedule(dynamic)
+#endif
+    for (int bh = 0; bh < B * Hq; ++bh) {
+        const int b = bh / Hq, h = bh % Hq, kvh = h / kv_group;
+        const int n = seq_lens[b] > 0 ? seq_lens[b] : 0;
+        uint8_t* kb = (uint8_t*)malloc((size_t)E * (size_t)(n + 1));
+        uint8_t* vb = (uint8_t*)malloc((size_t)E * (size_t)(n + 1));
+        double* K = (double*)malloc(sizeof(double) * (size_t)(n + 1) * (size_t)D);
+        double* V = (double*)malloc(sizeof(double) * (size_t)(n + 1) * (size_t)D);
+        const int cnt = gather_entries(kc, fmt, hnd, bt + (int64_t)b * max_blocks, n, kvh, Hkv, D, bs, kb);
+        gather_entries(vc, fmt, hnd, bt + (int64_t)b * max_blocks, n, kvh, Hkv, D, bs, vb);
+        float tmp[256];
+        double qd[256];
+        for (int i = 0; i < cnt; ++i) {
+            orc_kv_dequant_entry(kb + (int64_t)i * E, fmt, D, tmp);
+            for (int d = 0; d < D; ++d) K[(int64_t)i * D + d] = tmp[d];
+            orc_kv_dequant_entry(vb + (int64_t)i * E, fmt, D, tmp);
+            for (int d = 0; d < D; ++d) V[(int64_t)i * D + d] = tmp[d];
+        }
+        for (int d = 0; d < D; ++d) qd[d] = q[(int64_t)bh * D + d];
+        softmax_av_exact(qd, K, V, cnt, D, scale, out + (int64_t)bh * D);
+        free(kb); free(vb); free(K); free(V);
+    }
+}
+
+/* ggml-cpu vec_dot of K row (fmt) with Q converted to K's vec_dot type:
+ * f16 K: ggml_vec_dot_f16 (vec.cpp) -> double-accumulated fp32 products;
+ * q8_0/q4_0 K: Q quantised to q8_0 (quantize_row_q8_0 -> _ref in vm_c's
+ * SSE-only ggml build), per-block integer dot times d_k*d_q
+ * (ggml-cpu/quants.c ggml_vec_dot_q8_0_q8_0_generic / q4_0_q8_0_generic). */
+static float kq_dot(const uint8_t* k, int fmt, const uint16_t* q16, const uint8_t* q8, int D) {
+    if (fmt == ORC_KV_F16 || fmt == ORC_KV_BF16) {
+        double sum = 0.0;
+        for (int d = 0; d < D; ++d) {
+            const uint16_t kh = (uint16_t)(k[2 * d] | (k[2 * d + 1] << 8));
+            const float kf = half_to_f32(kh, fmt == ORC_KV_BF16);
+            const float qf = half_to_f32(q16[d], fmt == ORC_KV_BF16);
+            sum += (double)(kf * qf);
+        }
+        return (float)sum;
+    }
+    float sumf = 0.0f;
+    const int E = fmt == ORC_KV_Q8_0 ? Q8_0_BYTES : Q4_0_BYTES;
+    for (int ib = 0; ib < D / QK; ++ib) {
+        const uint8_t* kb = k + ib * E;
+        const uint8_t* qb = q8 + ib * Q8_0_BYTES;
+        int sumi = 0;
+        if (fmt == ORC_KV_Q8_0) {
+            for (int j = 0; j < QK; ++j) sumi += (int)(int8_t)kb[2 + j] * (int)(int8_t)qb[2 + j];
+        } else {
+            for (int j = 0; j < QK / 2; ++j) {
+                const int v0 = (kb[2 + j] & 0x0f) - 8;
+                const int v1 = (kb[2 + j] >> 4) - 8;
+                sumi += v0 * (int)(int8_t)qb[2 + j] + v1 * (int)(int8_t)qb[2 + j + QK / 2];
+            }
+        }
+        const float dk = orc_f16_to_f32((uint16_t)(kb[0] | (kb[1] << 8)));
+        const float dq = orc_f16_to_f32((uint16_t)(qb[0] | (qb[1] << 8)));
+        sumf += (float)sumi * (dk * dq);
+    }
+    return sumf;
+}
+
+/* ggml/src/ggml-cpu/ops.cpp:8214-8450 (one_chunk) over [ic0, ic1) for one query
+ * row; writes M, S and the fp32 VKQ accumulator. */
+static void ggml_one_chunk(const float* q, const uint8_t* K, const uint8_t* V, int fmt,
+                           int D, int64_t E, int ic0, int ic1, float scale, float* M_out,
+                           float* S_out, float* vkq32) {
+    uint16_t q16[256], vkq16[256];
+    uint8_t q8[8 * Q8_0_BYTES];
+    float v32[256];
+    const int f16v = (fmt == ORC_KV_F16);
+    if (fmt == ORC_KV_F16 || fmt == ORC_KV_BF16) {
+        for (int d = 0; d < D; ++d) q16[d] = f32_to_half(q[d], fmt == ORC_KV_BF16);
+    } else {
+        orc_quantize_row_q8_0(q, q8, D);
+    }
+    if (f16v) memset(vkq16, 0, sizeof(uint16_t) * (size_t)D);
+    else memset(vkq32, 0, sizeof(float) * (size_t)D);
+    float S = 0.0f, M = -INFINITY;
+    for (int ic = ic0; ic < ic1; ++ic) {
+        float s = kq_dot(K + (int64_t)ic * E, fmt, q16, q8, D);
+        s = s * scale;
+        const float Mold = M;
+        float ms = 1.0f, vs = 1.0f;
+        const uint8_t* vd = V + (int64_t)ic * E;
+        if (f16v) {
+            if (s > M) {
+                M = s;
+                ms = expf(Mold - M);
+                /* ggml_vec_scale_f16: y = fp16(fp32(y)*v) */
+                for (int d = 0; d < D; ++d) vkq16[d] = orc_f32_to_f16(orc_f16_to_f32(vkq16[d]) * ms);
+            } else {
+                vs = expf(s - M);
+            }
+            /* ggml_vec_mad_f16: y = fp16(fp32(y) + fp32(x)*v), no FMA */
+            for (int d = 0; d < D; ++d) {
+                const float xv = orc_f16_to_f32((uint16_t)(vd[2 * d] | (vd[2 * d + 1] << 8)));
+                volatile float prod = xv * vs;
+                vkq16[d] = orc_f32_to_f16(orc_f16_to_f32(vkq16[d]) + prod);
+            }
+        } else {
+            if (s > M) {
+                M = s;
+                ms = expf(Mold - M);
+                for (int d = 0; d < D; ++d) vkq32[d] *= ms;
+            } else {
+                vs = expf(s - M);
+            }
+            orc_kv_dequant_entry(vd, fmt, D, v32);
+            for (int d = 0; d < D; ++d) {
+                volatile float prod = v32[d] * vs;
+                vkq32[d] = vkq32[d] + prod;
+            }
+        }
+        S = S * ms + vs;
+    }
+    if (f16v)
+        for (int d = 0; d < D; ++d) vkq32[d] = orc_f16_to_f32(vkq16[d]);
+    *M_out = M;
+    *S_out = S;
+}
+
+void orc_decode_ggml(float* out, const float* q, const uint8_t* kc, const uint8_t* vc,
+                     int fmt, int hnd, const int32_t* bt, const int32_t* seq_lens, int B,
+                     int Hq, int Hkv, int D, float scale, int64_t bs, int64_t max_blocks,
+                     int nth, int nthreads) {
+    const int kv_group = Hq / Hkv;
+    const int64_t E = orc_kv_entry_bytes(fmt, D);
+    if (nth < 1) nth = 1;
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel for schedule(dynamic)
+#endif
+    for (int bh = 0; bh < B * Hq; ++bh) {
+        const int b = bh / Hq, h = bh % Hq, kvh = h / kv_group;
+        const int n = seq_lens[b] > 0 ? seq_lens[b] : 0;
+        uint8_t* kb = (uint8_t*)malloc((size_t)E * (size_t)(n + 1));
+        uint8_t* vb = (uint8_t*)malloc((size_t)E * (size_t)(n + 1));
+        const int cnt = gather_entries(kc, fmt, hnd, bt + (int64_t)b * max_blocks, n, kvh, Hkv, D, bs, kb);
+        gather_entries(vc, fmt, hnd, bt + (int64_t)b * max_blocks, n, kvh, Hkv, D, bs, vb);
+        float* o = out + (int64_t)bh * D;
+        const float* qh = q + (int64_t)bh * D;
+        float vkq[256];
+        /* ops.cpp:8848-8893: split-KV only for f16/f32 K==V type and >= 512 KV */
+        const int split = (fmt == ORC_KV_F16) && cnt >= 512;
+        if (!split) {
+            float M, S;
+            ggml_one_chunk(qh, kb, vb, fmt, D, E, 0, cnt, scale, &M, &S, vkq);
+            const float S_inv = S == 0.0f ? 0.0f : 1.0f / S;
+            for (int d = 0; d < D; ++d) o[d] = vkq[d] * S_inv;
+        } else {
+            /* ops.cpp:8742-8810 reduce_partials */
+            const int chunk = (cnt + nth - 1) / nth;
+            float Mf = -INFINITY, Sf = 0.0f, acc[256];
+            for (int d = 0; d < D; ++d) acc[d] = 0.0f;
+            for (int c = 0; c < nth; ++c) {
+                const int i0 = c * chunk;
+                if (i0 >= cnt) continue;
+                const int i1 = i0 + chunk < cnt ? i0 + chunk : cnt;
+                float M, S;
+                ggml_one_chunk(qh, kb, vb, fmt, D, E, i0, i1, scale, &M, &S, vkq);
+                if (S == 0.0f) continue;
+                const float Mn = fmaxf(Mf, M);
+                const float so = expf(Mf - Mn), sn = expf(M - Mn);
+                for (int d = 0; d < D; ++d) {
+                    volatile float a = acc[d] * so;
+                    volatile float bb = vkq[d] * sn;
+                    acc[d] = a + bb;
+                }
+                Sf = Sf * so + S * sn;
+                Mf = Mn;
+            }
+            const float S_inv = Sf != 0.0f ? 1.0f / Sf : 1.0f;
+            for (int d = 0; d < D; ++d) o[d] = acc[d] * S_inv;
+        }
+        free(kb);
+        free(vb);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* causal prefill: exact fp64 rows                                          */
+/* ------------------------------------------------------------------------ */
+
+void orc_prefill_exact_rows(double* out, const uint16_t* q, const uint16_t* k,
+                            const uint16_t* v, int is_bf16, const int32_t* cu, int B,
+                            int Hq, int Hkv, int D, double scale, const int64_t* tokens,
+                            const int32_t* heads, int64_t nrows, int nthreads) {
+    const int kv_group = Hq / Hkv;
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel for schedule(dynamic)
+#endif
+    for (int64_t r = 0; r < nrows; ++r) {
+        const int64_t t = tokens[r];
+        const int h = heads[r], kvh = h / kv_group;
+        int b = 0;
+        while (b < B - 1 && t >= cu[b + 1]) b++;
+        const int64_t t0 = cu[b];
+        const int n = (int)(t - t0 + 1);
+        double* K = (double*)malloc(sizeof(double) * (size_t)n * (size_t)D);
+        double* V = (double*)malloc(sizeof(double) * (size_t)n * (size_t)D);
+        double qd[256];
+        for (int i = 0; i < n; ++i)
+            for (int d = 0; d < D; ++d) {
+                const int64_t idx = ((t0 + i) * Hkv + kvh) * D + d;
+                K[(int64_t)i * D + d] = half_to_f32(k[idx], is_bf16);
+                V[(int64_t)i * D + d] = half_to_f32(v[idx], is_bf16);
+            }
+        for (int d = 0; d < D; ++d) qd[d] = half_to_f32(q[(t * Hq + h) * D + d], is_bf16);
+        softmax_av_exact(qd, K, V, n, D, scale, out + r * D);
+        free(K);
+        free(V);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* deterministic inputs                                                     */
+/* ------------------------------------------------------------------------ */
+
+static uint64_t splitmix64(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+uint64_t orc_rand_u64(uint64_t seed, uint64_t stream, uint64_t index) {
+    return splitmix64(splitmix64(splitmix64(seed) ^ stream) ^ index);
+}
+
+double orc_randn(uint64_t seed, uint64_t stream, uint64_t index) {
+    const double u1 = ((double)(orc_rand_u64(seed, stream, 2 * index) >> 11) + 1.0) * 0x1.0p-53;
+    const double u2 = (double)(orc_rand_u64(seed, stream, 2 * index + 1) >> 11) * 0x1.0p-53;
+    return sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+}
+
+void orc_randn_f16(uint16_t* out, int64_t n, uint64_t seed, uint64_t stream) {
+    for (int64_t i = 0; i < n; ++i) out[i] = orc_f32_to_f16((float)orc_randn(seed, stream, (uint64_t)i));
+}
+
+void orc_randn_bf16(uint16_t* out, int64_t n, uint64_t seed, uint64_t stream) {
+    for (int64_t i = 0; i < n; ++i) out[i] = orc_f32_to_bf16((float)orc_randn(seed, stream, (uint64_t)i));
+}

@@ -1,0 +1,155 @@
+/*
+ * vmc_oracle.h -- CPU restatement of vm_c's attention hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker for the HIP
+ * implementation in vm_c_amd/.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load it; the product path never does.
+ *
+ * Every function cites the reference file:line whose arithmetic it restates.
+ * Citations are relative to the vm_c source tree; ggml paths are relative to
+ * third_party/vm_c_official/ggml/.
+ *
+ * Pinning (how each function is checked, see tests/test_oracle_*.py):
+ *   - fp16/bf16 conversion: exhaustive round trip + torch's converters.
+ *   - q8_0 / q4_0 quantizers: bit-exact against the vendored ggml
+ *     quantize_row_*_ref built from source (oracle/_ref), and the committed
+ *     golden vectors in tests/golden/.
+ *   - Hadamard: closed form (-1)^popcount(i&j)/sqrt(d) and H*H = I.
+ *   - Lloyd-Max centroids: classic Max (1960) Gaussian quantizer tables
+ *     scaled by 1/sqrt(d); committed fp32 bit patterns.
+ *   - TQ store: slot sizes 134/102/118 B for d=128 (tp_runtime.cpp:257-261),
+ *     unpack(pack) round trip, all-equal V -> codes 0, zero K -> norm 0,
+ *     codes equal the nearest-centroid index of the exactly rotated vector.
+ *   - TQ decode / paged decode: equals exact fp64 attention over the
+ *     dequantized pages; split-count invariance; permuted block tables.
+ *   - ggml CPU flash-attention restatement: against the vendored ggml CPU
+ *     flash_attn_ext (oracle/_ref) and fp64 exact attention.
+ */
+#ifndef VMC_ORACLE_H
+#define VMC_ORACLE_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- scalar conversions (round-to-nearest-even) ---- */
+uint16_t orc_f32_to_f16(float f);
+float    orc_f16_to_f32(uint16_t h);
+uint16_t orc_f32_to_bf16(float f);
+float    orc_bf16_to_f32(uint16_t h);
+void     orc_f32_to_f16_n(const float* x, uint16_t* y, int64_t n);
+void     orc_f16_to_f32_n(const uint16_t* x, float* y, int64_t n);
+
+/* ---- GGUF q8_0 / q4_0 blocks (ggml-common.h:184-188, :241-245) ---- */
+void orc_quantize_row_q8_0(const float* x, void* y, int64_t k);
+void orc_dequantize_row_q8_0(const void* x, float* y, int64_t k);
+void orc_quantize_row_q4_0(const float* x, void* y, int64_t k);
+void orc_dequantize_row_q4_0(const void* x, float* y, int64_t k);
+
+/* ---- paged KV formats for the non-TurboQuant path ---- */
+enum { ORC_KV_F16 = 0, ORC_KV_BF16 = 1, ORC_KV_Q8_0 = 2, ORC_KV_Q4_0 = 3 };
+/* bytes of one (token, kv-head) entry of head_dim values */
+int64_t orc_kv_entry_bytes(int fmt, int head_dim);
+/* Append K/V rows [T][Hkv][D] (fp16 or bf16 bits) into K and V page pools.
+ * NHD: blk*stride + off*Hkv*E + h*E ; HND: blk*stride + h*bs*E + off*E,
+ * stride = bs*Hkv*E.  slot < 0 skips the token. */
+void orc_kv_append(const uint16_t* key, const uint16_t* value, int src_bf16,
+                   uint8_t* key_cache, uint8_t* value_cache,
+                   const int64_t* slot_mapping, int num_tokens, int num_kv_heads,
+                   int head_dim, int64_t block_size, int fmt, int hnd);
+void orc_kv_dequant_entry(const uint8_t* entry, int fmt, int head_dim, float* out);
+
+/* ---- TurboQuant (src/cuda/turboquant_kernels.cu, kernels_turboquant.h) ---- */
+typedef struct {
+    int head_dim;
+    int key_quant_bits;
+    int value_quant_bits;
+    int norm_correction;
+    int mse_bytes;
+    int key_packed_size;
+    int val_data_bytes;
+    int value_packed_size;
+    int slot_size;
+    int slot_size_aligned;
+    int n_centroids;
+} orc_tq_layout;
+
+int  orc_tq_layout_from_method(int head_dim, const char* method, orc_tq_layout* out);
+void orc_tq_hadamard(float* out, int d);
+void orc_tq_lloyd_max(float* centroids_out, int d, int bits);
+void orc_tq_midpoints(const float* centroids, int n_centroids, float* midpoints);
+/* y = H x in the declared order: in-place Walsh-Hadamard butterflies with
+ * half-width h = 1, 2, 4, ..., d/2, then y *= 1/sqrtf(d).  signs (may be NULL)
+ * multiplies x elementwise first. */
+void orc_tq_rotate(const float* x, const float* signs, float* y, int d);
+void orc_tq_store(const uint16_t* key, const uint16_t* value, uint8_t* kv_cache,
+                  const int64_t* slot_mapping, int num_tokens, int num_kv_heads,
+                  int head_dim, int64_t block_size, const orc_tq_layout* L,
+                  const float* midpoints, int half_is_bf16);
+/* Dequantize one slot: k_out = rotated-domain K (centroid * norm-correction *
+ * norm), v_out = code*scale + zero. */
+void orc_tq_dequant_slot(const uint8_t* slot, const orc_tq_layout* L,
+                         const float* centroids, int half_is_bf16,
+                         float* k_out, float* v_out);
+/* Two-stage split-KV decode with the intended single-execution semantics of
+ * tq_decode_stage1_kernel / stage2 (one body per (b,h,split)). */
+void orc_tq_decode(uint16_t* out, const uint16_t* query, const uint8_t* kv_cache,
+                   const int32_t* block_tables, const int32_t* seq_lens,
+                   int batch, int num_heads, int num_kv_heads, int head_dim,
+                   float scale, int64_t block_size, int64_t max_blocks_per_req,
+                   const orc_tq_layout* L, const float* centroids,
+                   int num_kv_splits, int half_is_bf16, int nthreads);
+/* Exact fp64 attention over the dequantized TQ pages (rotation exact). */
+void orc_tq_decode_exact(double* out, const uint16_t* query, const uint8_t* kv_cache,
+                         const int32_t* block_tables, const int32_t* seq_lens,
+                         int batch, int num_heads, int num_kv_heads, int head_dim,
+                         double scale, int64_t block_size, int64_t max_blocks_per_req,
+                         const orc_tq_layout* L, const float* centroids,
+                         int half_is_bf16, int nthreads);
+
+/* ---- paged decode over f16/bf16/q8_0/q4_0 pages ---- */
+/* exact fp64 softmax attention over the dequantized pages; q is fp32 */
+void orc_paged_decode_exact(double* out, const float* q,
+                            const uint8_t* key_cache, const uint8_t* value_cache,
+                            int fmt, int hnd, const int32_t* block_tables,
+                            const int32_t* seq_lens, int batch, int num_heads,
+                            int num_kv_heads, int head_dim, double scale,
+                            int64_t block_size, int64_t max_blocks_per_req,
+                            int nthreads);
+/* ggml CPU flash_attn_ext restatement (decode, one query row per sequence)
+ * over K/V gathered from pages: Q converted to K's vec_dot type (f16, or q8_0
+ * for a quantized K), fp16 V accumulator for an f16 V, KV split into `nth`
+ * chunks with a partial reduce when K/V are f16 and S >= 512. fp32 out. */
+void orc_decode_ggml(float* out, const float* q,
+                     const uint8_t* key_cache, const uint8_t* value_cache,
+                     int fmt, int hnd, const int32_t* block_tables,
+                     const int32_t* seq_lens, int batch, int num_heads,
+                     int num_kv_heads, int head_dim, float scale,
+                     int64_t block_size, int64_t max_blocks_per_req, int nth,
+                     int nthreads);
+
+/* ---- causal prefill ---- */
+/* Exact fp64 causal attention for selected rows.  q [T][Hq][D], k/v
+ * [T][Hkv][D] (bf16 bits if is_bf16 else fp16 bits); cu_seqlens[B+1] gives
+ * each sequence's token range; row r = (tokens[r], heads[r]). */
+void orc_prefill_exact_rows(double* out, const uint16_t* q, const uint16_t* k,
+                            const uint16_t* v, int is_bf16,
+                            const int32_t* cu_seqlens, int batch,
+                            int num_heads, int num_kv_heads, int head_dim,
+                            double scale, const int64_t* tokens,
+                            const int32_t* heads, int64_t nrows, int nthreads);
+
+/* ---- deterministic inputs ---- */
+/* counter-based N(0,1): splitmix64(seed, stream, index) -> Box-Muller (double) */
+double orc_randn(uint64_t seed, uint64_t stream, uint64_t index);
+void   orc_randn_f16(uint16_t* out, int64_t n, uint64_t seed, uint64_t stream);
+void   orc_randn_bf16(uint16_t* out, int64_t n, uint64_t seed, uint64_t stream);
+uint64_t orc_rand_u64(uint64_t seed, uint64_t stream, uint64_t index);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

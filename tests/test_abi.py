@@ -1,0 +1,81 @@
+"""CPU checks of the C ABI library: it loads, exports every symbol the header
+declares, and its host-only entry points behave (no GPU calls here)."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+
+import oracle_lib as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    src = open(os.path.join(ROOT, "include", "vmc_attn.h")).read()
+    return sorted(set(re.findall(r"\b(vmc_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_symbol():
+    from vm_c_amd import capi
+    lib = capi.load()
+    missing = [n for n in _declared() if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(capi.EXPORTS) <= set(_declared())
+
+
+def test_version():
+    from vm_c_amd import capi
+    assert "gfx950" in capi.version()
+
+
+def test_entry_bytes():
+    from vm_c_amd import capi
+    assert capi.kv_entry_bytes(capi.KV_F16, 128) == 256
+    assert capi.kv_entry_bytes(capi.KV_Q8_0, 128) == 136
+    assert capi.kv_entry_bytes(capi.KV_Q4_0, 128) == 72
+    assert capi.kv_entry_bytes(7, 128) < 0
+
+
+def test_tq_config_layouts():
+    """Slot sizes held by the reference: 134 / 102 / 118 B for head_dim 128
+    (src/distributed/tp_runtime.cpp:257-261, kernels_turboquant.h:29-42)."""
+    from vm_c_amd import capi
+    exp = {"turboquant_4bit_nc": (64, 66, 64, 68, 134), "turboquant_3bit_nc": (48, 50, 48, 52, 102),
+           "turboquant_k3v4_nc": (48, 50, 64, 68, 118)}
+    for m, (mse, kp, vd, vp, slot) in exp.items():
+        c = capi.tq_config(128, m)
+        assert (c.mse_bytes, c.key_packed_size, c.val_data_bytes, c.value_packed_size,
+                c.slot_size_aligned) == (mse, kp, vd, vp, slot)
+        L = O.tq_layout(m)
+        assert L.slot_size_aligned == slot
+    assert capi.tq_config(256, "turboquant_4bit_nc").slot_size_aligned == 262
+    import pytest
+    with pytest.raises(capi.VmcError):
+        capi.tq_config(128, "turboquant_k8v4")
+
+
+def test_tq_host_tables_match_oracle():
+    from vm_c_amd import capi
+    for bits in (3, 4):
+        c, m = capi.tq_host_tables(128, bits)
+        oc, om = O.tq_tables(128, bits)
+        assert np.array_equal(c.view(np.uint32), oc.view(np.uint32))
+        assert np.array_equal(m.view(np.uint32), om.view(np.uint32))
+
+
+def test_argument_validation_without_gpu():
+    """Invalid shapes are rejected before any device work."""
+    from vm_c_amd import capi
+    L = capi.load()
+    # head_dim not a multiple of 32
+    assert L.vmc_reshape_and_cache(None, None, None, None, None, 1, 1, 100, 16, 0, 0, 0, 0, None) == capi.VMC_EINVAL
+    # zero tokens is a no-op
+    assert L.vmc_reshape_and_cache(None, None, None, None, None, 0, 1, 128, 16, 0, 0, 0, 0, None) == capi.VMC_OK
+    # decode: GQA group > 16 rejected
+    assert L.vmc_paged_attention_decode(None, None, None, None, None, None, 1, 64, 2, 128, 16, 4,
+                                        C.c_float(0.1), 0, 0, 0, 0, None, 0, None) == capi.VMC_EINVAL
+    # decode: workspace too small
+    assert L.vmc_paged_attention_decode(C.c_void_p(16), C.c_void_p(16), C.c_void_p(16), C.c_void_p(16),
+                                        C.c_void_p(16), C.c_void_p(16), 1, 8, 8, 128, 16, 4,
+                                        C.c_float(0.1), 0, 0, 0, 0, C.c_void_p(16), 8, None) == capi.VMC_ENOMEM

@@ -1,0 +1,203 @@
+"""ctypes binding of the C ABI in include/vmc_attn.h (libvmc_attn.so).
+
+Thin: torch tensors are used only as device memory and for the current HIP
+stream; every call goes straight to the gfx950 kernels.  There is no fallback:
+if the library is missing or a call fails, this raises.
+"""
+import ctypes as C
+import os
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libvmc_attn.so")
+
+VMC_OK, VMC_EINVAL, VMC_ENOMEM, VMC_EIO = 0, -22, -12, -5
+DTYPE_F16, DTYPE_BF16 = 0, 1
+KV_F16, KV_BF16, KV_Q8_0, KV_Q4_0 = 0, 1, 2, 3
+LAYOUT_NHD, LAYOUT_HND = 0, 1
+KV_FORMATS = {"fp16": KV_F16, "bf16": KV_BF16, "q8_0": KV_Q8_0, "q4_0": KV_Q4_0}
+
+EXPORTS = [
+    "vmc_kv_entry_bytes", "vmc_reshape_and_cache", "vmc_paged_decode_workspace_size",
+    "vmc_paged_attention_decode", "vmc_tq_config_from_method", "vmc_tq_host_tables",
+    "vmc_turboquant_store", "vmc_turboquant_decode_workspace_size",
+    "vmc_turboquant_decode_attention", "vmc_flash_attention_prefill", "vmc_version",
+]
+
+
+class TQConfig(C.Structure):
+    """Mirror of vmc_tq_config (vm_c::TQConfig)."""
+    _fields_ = [(n, C.c_int) for n in (
+        "head_dim", "key_quant_bits", "value_quant_bits", "norm_correction", "key_fp8",
+        "fp8_e4b15", "mse_bytes", "key_packed_size", "val_data_bytes", "value_packed_size",
+        "slot_size", "slot_size_aligned", "n_centroids", "max_num_kv_splits")]
+
+
+class VmcError(RuntimeError):
+    pass
+
+
+_lib = None
+_P = C.c_void_p
+_I, _I64, _F, _SZ = C.c_int, C.c_int64, C.c_float, C.c_size_t
+
+
+def load():
+    """Load libvmc_attn.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise VmcError(f"{LIB_PATH} not built: run `python -m vm_c_amd.build`")
+    L = C.CDLL(LIB_PATH)
+    L.vmc_kv_entry_bytes.restype = _I64
+    L.vmc_kv_entry_bytes.argtypes = [_I, _I]
+    L.vmc_reshape_and_cache.restype = _I
+    L.vmc_reshape_and_cache.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I64, _I64, _I, _I, _I, _P]
+    L.vmc_paged_decode_workspace_size.restype = _SZ
+    L.vmc_paged_decode_workspace_size.argtypes = [_I, _I, _I, _I, _I, _I]
+    L.vmc_paged_attention_decode.restype = _I
+    L.vmc_paged_attention_decode.argtypes = [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F,
+                                             _I, _I, _I, _I, _P, _SZ, _P]
+    L.vmc_tq_config_from_method.restype = _I
+    L.vmc_tq_config_from_method.argtypes = [_I, C.c_char_p, C.POINTER(TQConfig)]
+    L.vmc_tq_host_tables.restype = _I
+    L.vmc_tq_host_tables.argtypes = [_I, _I, _P, _P]
+    L.vmc_turboquant_store.restype = _I
+    L.vmc_turboquant_store.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I64, C.POINTER(TQConfig), _I, _P]
+    L.vmc_turboquant_decode_workspace_size.restype = _SZ
+    L.vmc_turboquant_decode_workspace_size.argtypes = [_I, _I, _I, _I64, _I64, _I]
+    L.vmc_turboquant_decode_attention.restype = _I
+    L.vmc_turboquant_decode_attention.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I64,
+                                                  _I64, C.POINTER(TQConfig), _I, _I, _P, _SZ, _P]
+    L.vmc_flash_attention_prefill.restype = _I
+    L.vmc_flash_attention_prefill.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P, _P,
+                                              _P, _I64, _I, _I, _P]
+    L.vmc_version.restype = C.c_char_p
+    L.vmc_version.argtypes = []
+    _lib = L
+    return L
+
+
+def _check(rc, what):
+    if rc != VMC_OK:
+        raise VmcError(f"{what} failed with status {rc}")
+
+
+def _ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _stream(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return C.c_void_p(s.cuda_stream)
+
+
+def _dtype_code(t):
+    import torch
+    if t.dtype == torch.float16:
+        return DTYPE_F16
+    if t.dtype == torch.bfloat16:
+        return DTYPE_BF16
+    raise VmcError(f"unsupported dtype {t.dtype}")
+
+
+def version():
+    return load().vmc_version().decode()
+
+
+def kv_entry_bytes(kv_format, head_dim):
+    return int(load().vmc_kv_entry_bytes(kv_format, head_dim))
+
+
+def tq_config(head_dim=128, method="turboquant_4bit_nc"):
+    cfg = TQConfig()
+    _check(load().vmc_tq_config_from_method(head_dim, method.encode(), C.byref(cfg)),
+           f"vmc_tq_config_from_method({method})")
+    return cfg
+
+
+def tq_host_tables(head_dim, bits):
+    import numpy as np
+    n = 1 << bits
+    c = np.zeros(n, dtype=np.float32)
+    m = np.zeros(n - 1, dtype=np.float32)
+    _check(load().vmc_tq_host_tables(head_dim, bits, c.ctypes.data_as(_P), m.ctypes.data_as(_P)),
+           "vmc_tq_host_tables")
+    return c, m
+
+
+def reshape_and_cache(key, value, key_cache, value_cache, slot_mapping, block_size,
+                      kv_format=KV_F16, layout=LAYOUT_NHD, cache_stride=0, stream=None):
+    T, H, D = key.shape
+    rc = load().vmc_reshape_and_cache(_ptr(key), _ptr(value), _ptr(key_cache), _ptr(value_cache),
+                                      _ptr(slot_mapping), T, H, D, block_size, cache_stride,
+                                      kv_format, _dtype_code(key), layout, _stream(stream))
+    _check(rc, "vmc_reshape_and_cache")
+
+
+def paged_decode_workspace_size(batch, num_heads, head_dim=128, max_blocks=0, block_size=16,
+                                max_splits=0):
+    return int(load().vmc_paged_decode_workspace_size(batch, num_heads, head_dim, max_blocks,
+                                                      block_size, max_splits))
+
+
+def paged_attention_decode(out, query, key_cache, value_cache, block_tables, seq_lens,
+                           num_kv_heads, scale, block_size=16, kv_format=KV_F16,
+                           layout=LAYOUT_NHD, workspace=None, max_splits=0, stream=None):
+    import torch
+    B, Hq, D = query.shape
+    max_blocks = block_tables.shape[1]
+    ws_bytes = paged_decode_workspace_size(B, Hq, D, max_blocks, block_size, max_splits)
+    if workspace is None:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=query.device)
+    rc = load().vmc_paged_attention_decode(
+        _ptr(out), _ptr(query), _ptr(key_cache), _ptr(value_cache), _ptr(block_tables),
+        _ptr(seq_lens), B, Hq, num_kv_heads, D, block_size, max_blocks, scale,
+        _dtype_code(query), kv_format, layout, max_splits, _ptr(workspace),
+        workspace.numel() * workspace.element_size(), _stream(stream))
+    _check(rc, "vmc_paged_attention_decode")
+    return out
+
+
+def turboquant_store(key, value, kv_cache, slot_mapping, block_size, cfg, stream=None):
+    T, H, D = key.shape
+    rc = load().vmc_turboquant_store(_ptr(key), _ptr(value), _ptr(kv_cache), _ptr(slot_mapping),
+                                     T, H, D, block_size, C.byref(cfg), _dtype_code(key),
+                                     _stream(stream))
+    _check(rc, "vmc_turboquant_store")
+
+
+def turboquant_decode_workspace_size(batch, num_heads, head_dim=128, max_blocks=0, block_size=16,
+                                     max_splits=0):
+    return int(load().vmc_turboquant_decode_workspace_size(batch, num_heads, head_dim, max_blocks,
+                                                           block_size, max_splits))
+
+
+def turboquant_decode_attention(out, query, kv_cache, block_tables, seq_lens, num_kv_heads, scale,
+                                cfg, block_size=16, workspace=None, max_splits=0, stream=None):
+    import torch
+    B, Hq, D = query.shape
+    max_blocks = block_tables.shape[1]
+    ws_bytes = turboquant_decode_workspace_size(B, Hq, D, max_blocks, block_size, max_splits)
+    if workspace is None:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=query.device)
+    rc = load().vmc_turboquant_decode_attention(
+        _ptr(out), _ptr(query), _ptr(kv_cache), _ptr(block_tables), _ptr(seq_lens), B, Hq,
+        num_kv_heads, D, scale, block_size, max_blocks, C.byref(cfg), _dtype_code(query),
+        max_splits, _ptr(workspace), workspace.numel() * workspace.element_size(),
+        _stream(stream))
+    _check(rc, "vmc_turboquant_decode_attention")
+    return out
+
+
+def flash_attention_prefill(out, query, key, value, token_positions, num_kv_heads, scale,
+                            key_cache=None, value_cache=None, slot_mapping=None, block_size=16,
+                            kv_format=KV_Q8_0, layout=LAYOUT_NHD, stream=None):
+    T, Hq, D = query.shape
+    rc = load().vmc_flash_attention_prefill(
+        _ptr(out), _ptr(query), _ptr(key), _ptr(value), T, Hq, num_kv_heads, D, scale,
+        _ptr(token_positions), _dtype_code(query), _ptr(key_cache), _ptr(value_cache),
+        _ptr(slot_mapping), block_size, kv_format, layout, _stream(stream))
+    _check(rc, "vmc_flash_attention_prefill")
+    return out

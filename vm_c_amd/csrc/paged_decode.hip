@@ -1,0 +1,781 @@
+// paged_decode.hip -- split-KV paged decode attention for gfx950.
+//
+// Replaces vm_c::paged_attention_v1/_v2 (src/cuda/attention_kernels.cu:438-473)
+// and vm_c::turboquant_decode_attention (src/cuda/turboquant_kernels.cu:
+// 939-1007).  Semantics: softmax(q k^T * scale) v per query head over the
+// sequence's tokens, read through the block table, GQA kv head = q head /
+// (Hq / Hkv) (ggml flash_attn_ext broadcast, ggml-cpu/ops.cpp:8260-8265).
+//
+// Work decomposition.  A work item is (sequence, split): a contiguous run of
+// pages of one sequence.  Every workgroup recomputes the same plan from
+// seq_lens (pages_b = ceil(L_b / bs); pages per split = max(pps_min,
+// ceil(total / target_items)); splits_b = min(max_splits, ...)) so no host
+// round trip or extra launch is needed; items beyond the plan exit.  The
+// workgroup has one wave per KV head; a page of the reference layout holds
+// all heads of 16 tokens contiguously, so the workgroup reads whole pages with
+// 16-byte loads (quantized formats stage the page in LDS; f16/bf16 pages are
+// read straight into MFMA operand registers).
+//
+// Per wave and page (16 tokens x G query heads of one KV head):
+//   S^T[16 tok x 16 heads] = K[16 x 128] . Q^T  : 4 x mfma 16x16x32 (f16/bf16)
+//   online softmax in the log2 domain, fp32 running max / sum per head
+//   O[16 heads x 128] += P[16 x 16 tok] . V      : 8 x mfma 16x16x16
+// S^T comes out of the MFMA in exactly the A-operand layout the PV MFMA needs
+// (lane l: head l%16, tokens 4*(l/16)+i), so P never leaves registers.  The PV
+// output columns are permuted (chunk c, column n -> dim 8n + c) so each lane's
+// V operand is one contiguous 8-dim run of a token.
+//
+// TurboQuant: K = C[code] * norm / ||C[codes]||, so S = scale*norm/||C|| *
+// (C[codes] . q_rot): the MFMA runs on fp16 centroids and the per-token factor
+// is applied to the S row.  V = code*scale + zero, so P.V = (P*scale).codes +
+// sum(P*zero): the MFMA runs on the exact small-integer codes.
+// q_rot = H q is a Walsh-Hadamard transform done in registers (the order the
+// oracle and the store kernel share).
+//
+// Partials (multi-split sequences) are fp32 (o, m, l) per (item, head) in the
+// caller's workspace; vmc_decode_merge_kernel combines them.
+#include "vmc_common.hpp"
+#include "vmc_tq.hpp"
+
+namespace vmc {
+namespace {
+
+constexpr int kD = 128;
+constexpr int kBs = 16;
+constexpr int kMaxStage = 8;  // 16-byte chunks per thread for one page
+constexpr float kNegInf = -__builtin_inff();
+
+enum { FMT_F16 = 0, FMT_BF16 = 1, FMT_Q8_0 = 2, FMT_Q4_0 = 3, FMT_TQ = 4 };
+
+struct DecodeParams {
+    void* out;
+    const uint16_t* q;
+    const uint8_t* kc;
+    const uint8_t* vc;
+    const int32_t* bt;
+    const int32_t* seq_lens;
+    float* part;       // [items][Hq][D + 2]
+    int32_t* seqinfo;  // [B][2]: first item, number of splits
+    int B, Hq, Hkv, G, max_blocks;
+    float scale_log2;
+    int64_t page_bytes;  // one page of one cache, all heads
+    int entry_bytes;     // one (token, head) entry (TQ: the aligned slot)
+    int hnd;
+    int target_items, pps_min, max_splits;
+    int q_bf16;
+    // TurboQuant
+    int mse_bytes, key_packed, val_data;
+    TQTables tab;
+};
+
+struct Plan {
+    int b, s, nsp, first_item, p0, p1, L;
+};
+
+// Identical in every workgroup (and in the merge kernel): a pure function of
+// seq_lens.  Executed by one wave; lanes stride over sequences.
+__device__ void compute_plan(const DecodeParams& p, int item, Plan* out) {
+    const int lane = threadIdx.x & 63;
+    int total = 0;
+    for (int b0 = 0; b0 < p.B; b0 += 64) {
+        const int b = b0 + lane;
+        const int L = b < p.B ? min(p.seq_lens[b], p.max_blocks * kBs) : 0;
+        int pages = L > 0 ? (L + kBs - 1) / kBs : 0;
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) pages += __shfl_xor(pages, m, 64);
+        total += pages;
+    }
+    const int pps = max(p.pps_min, (total + p.target_items - 1) / p.target_items);
+    int carry = 0;
+    for (int b0 = 0; b0 < p.B; b0 += 64) {
+        const int b = b0 + lane;
+        const int L = b < p.B ? min(p.seq_lens[b], p.max_blocks * kBs) : 0;
+        const int pages = L > 0 ? (L + kBs - 1) / kBs : 0;
+        int nsp = 0, ppsb = 0;
+        if (b < p.B) {
+            nsp = pages > 0 ? min(p.max_splits, (pages + pps - 1) / pps) : 1;
+            ppsb = pages > 0 ? (pages + nsp - 1) / nsp : 0;
+            nsp = pages > 0 ? (pages + ppsb - 1) / ppsb : 1;
+        }
+        int incl = nsp;
+#pragma unroll
+        for (int m = 1; m < 64; m <<= 1) {
+            const int v = __shfl_up(incl, m, 64);
+            if (lane >= m) incl += v;
+        }
+        const int first = carry + incl - nsp;
+        const bool mine = b < p.B && item >= first && item < first + nsp;
+        const unsigned long long bal = __ballot(mine);
+        if (bal) {
+            const int src = __builtin_ctzll(bal);
+            if (lane == src) {
+                const int s = item - first;
+                out->b = b;
+                out->s = s;
+                out->nsp = nsp;
+                out->first_item = first;
+                out->p0 = s * ppsb;
+                out->p1 = min(pages, (s + 1) * ppsb);
+                out->L = L;
+            }
+            return;
+        }
+        carry += __shfl(incl, 63, 64);
+    }
+    if (lane == 0) out->b = -1;
+}
+
+// ------------------------------------------------------------------ operands
+
+// pair table for the TurboQuant key codebook: entry (c0 | c1 << KB) =
+// fp16(C[c0]) | fp16(C[c1]) << 16, i.e. one dword of an f16x8 MFMA operand.
+template <int KB>
+__device__ __forceinline__ void build_pair_lut(uint32_t* lut, const TQTables& tab) {
+    constexpr int N = 1 << KB;
+    for (int e = threadIdx.x; e < N * N; e += blockDim.x) {
+        const int c0 = e & (N - 1), c1 = e >> KB;
+        float a = 0.0f, b = 0.0f;
+#pragma unroll
+        for (int c = 0; c < N; ++c) {
+            a = c == c0 ? tab.centroids[c] : a;
+            b = c == c1 ? tab.centroids[c] : b;
+        }
+        lut[e] = (uint32_t)f32_to_f16_bits(a) | ((uint32_t)f32_to_f16_bits(b) << 16);
+    }
+}
+
+__device__ __forceinline__ uint32_t lds16(const uint8_t* p) {
+    return (uint32_t)*reinterpret_cast<const uint16_t*>(p);
+}
+
+// int codes (0..15) -> exact fp16 via the 1024 + c bit trick
+__device__ __forceinline__ _Float16 code_f16(uint32_t c) {
+    return __builtin_bit_cast(_Float16, (uint16_t)(0x6400u | c)) - (_Float16)1024.0f;
+}
+
+template <int FMT>
+__device__ __forceinline__ int entry_off(int tok, int g, int Hkv, int E, int hnd) {
+    return hnd ? (g * kBs + tok) * E : (tok * Hkv + g) * E;
+}
+
+// ------------------------------------------------------------------ kernel
+
+template <int FMT, int KB, int VB, bool MBF16>
+__global__ void __launch_bounds__(512)
+paged_decode_kernel(DecodeParams p) {
+    using AT = typename std::conditional<MBF16, bf16x8, f16x8>::type;
+    using PT = typename std::conditional<MBF16, s16x4, f16x4>::type;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ Plan plan;
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int r16 = lane & 15, grp = lane >> 4;
+    const int item = blockIdx.x;
+
+    if (wave == 0) compute_plan(p, item, &plan);
+    constexpr bool kStaged = FMT >= FMT_Q8_0;
+    uint32_t* lut = reinterpret_cast<uint32_t*>(smem);
+    uint8_t* pagebuf = smem + (FMT == FMT_TQ ? 1024 : 0);
+    if constexpr (FMT == FMT_TQ) build_pair_lut<KB>(lut, p.tab);
+    __syncthreads();
+    const int b = plan.b;
+    if (b < 0) return;
+    const int s = plan.s, nsp = plan.nsp, L = plan.L;
+    const int p0 = plan.p0, p1 = plan.p1;
+    if (s == 0 && tid == 0) {
+        p.seqinfo[2 * b] = plan.first_item;
+        p.seqinfo[2 * b + 1] = nsp;
+    }
+
+    const int g = wave;  // kv head of this wave
+    const int G = p.G;
+    const int hq0 = g * G;
+    const int64_t qrow = ((int64_t)b * p.Hq + hq0 + r16) * kD;
+    const bool head_ok = r16 < G;
+
+    // ---- Q operand: lane (r16 = head, grp) holds dims 32*grp + 8*j + e, j = MFMA index
+    AT qb[4];
+    if constexpr (FMT == FMT_TQ) {
+        float y[32];
+        if (head_ok) {
+            const u32x4* src = reinterpret_cast<const u32x4*>(p.q + qrow + 32 * grp);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const u32x4 w = src[c];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint16_t lo = (uint16_t)(w[e] & 0xffff), hi = (uint16_t)(w[e] >> 16);
+                    y[8 * c + 2 * e] = p.q_bf16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
+                    y[8 * c + 2 * e + 1] = p.q_bf16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 32; ++e) y[e] = 0.0f;
+        }
+        // Walsh-Hadamard: half-widths 1..16 inside the lane, 32 and 64 across
+        // the lane groups (dim bit 32 = grp bit 0, dim bit 64 = grp bit 1).
+#pragma unroll
+        for (int h = 1; h < 32; h <<= 1)
+#pragma unroll
+            for (int i = 0; i < 32; i += 2 * h)
+#pragma unroll
+                for (int j = i; j < i + h; ++j) {
+                    const float a = y[j], c = y[j + h];
+                    y[j] = a + c;
+                    y[j + h] = a - c;
+                }
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+            const float o = shfl_xor(y[e], 16);
+            y[e] = (grp & 1) ? o - y[e] : y[e] + o;
+        }
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+            const float o = shfl_xor(y[e], 32);
+            y[e] = (grp & 2) ? o - y[e] : y[e] + o;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qb[j][e] = (_Float16)__fmul_rn(y[8 * j + e], p.tab.rot_c);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            u32x4 w = {0u, 0u, 0u, 0u};
+            if (head_ok) w = *reinterpret_cast<const u32x4*>(p.q + qrow + 32 * grp + 8 * j);
+            const bool qbf = p.q_bf16 != 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint16_t lo = (uint16_t)(w[e] & 0xffff), hi = (uint16_t)(w[e] >> 16);
+                if constexpr (MBF16) {
+                    const uint16_t l2 = qbf ? lo : f32_to_bf16_bits(f16_bits_to_f32(lo));
+                    const uint16_t h2 = qbf ? hi : f32_to_bf16_bits(f16_bits_to_f32(hi));
+                    qb[j][2 * e] = __builtin_bit_cast(__bf16, l2);
+                    qb[j][2 * e + 1] = __builtin_bit_cast(__bf16, h2);
+                } else {
+                    qb[j][2 * e] = qbf ? (_Float16)bf16_bits_to_f32(lo) : __builtin_bit_cast(_Float16, lo);
+                    qb[j][2 * e + 1] = qbf ? (_Float16)bf16_bits_to_f32(hi) : __builtin_bit_cast(_Float16, hi);
+                }
+            }
+        }
+    }
+
+    // ---- running state
+    f32x4 oacc[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) oacc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = kNegInf;  // per head r16 (log2 domain), replicated over grp
+    float l_part = 0.0f;    // partial over this lane's tokens
+    float z_part = 0.0f;    // TurboQuant: partial sum of p * zero
+
+    const int Hkv = p.Hkv, E = p.entry_bytes, hnd = p.hnd;
+    const int64_t page_bytes = p.page_bytes;
+    const int32_t* bt_row = p.bt + (int64_t)b * p.max_blocks;
+    const int nthreads = blockDim.x;
+
+    // staged formats: page(s) -> registers -> LDS
+    const int n16_k = (int)(page_bytes / 16);
+    const int n16 = (FMT == FMT_TQ) ? n16_k : 2 * n16_k;
+    u32x4 stage[kMaxStage];
+    auto stage_load = [&](int pg) {
+        const int32_t blk = bt_row[pg];
+        if (blk < 0) return;
+        const u32x4* ks = reinterpret_cast<const u32x4*>(p.kc + (int64_t)blk * page_bytes);
+        const u32x4* vs = reinterpret_cast<const u32x4*>(p.vc + (int64_t)blk * page_bytes);
+#pragma unroll
+        for (int c = 0; c < kMaxStage; ++c) {
+            const int idx = tid + c * nthreads;
+            if (idx < n16) stage[c] = (FMT == FMT_TQ || idx < n16_k) ? ks[idx] : vs[idx - n16_k];
+        }
+    };
+    auto stage_store = [&]() {
+        u32x4* dst = reinterpret_cast<u32x4*>(pagebuf);
+#pragma unroll
+        for (int c = 0; c < kMaxStage; ++c) {
+            const int idx = tid + c * nthreads;
+            if (idx < n16) dst[idx] = stage[c];
+        }
+    };
+
+    // direct formats: per-lane operand registers for one page
+    u32x4 kreg[4], vreg[4];
+    auto direct_load = [&](int pg) {
+        const int32_t blk = bt_row[pg];
+        const int tok0 = pg * kBs;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            kreg[c] = u32x4{0u, 0u, 0u, 0u};
+            vreg[c] = u32x4{0u, 0u, 0u, 0u};
+        }
+        if (blk < 0) return;
+        const uint8_t* kp = p.kc + (int64_t)blk * page_bytes;
+        const uint8_t* vp = p.vc + (int64_t)blk * page_bytes;
+        if (tok0 + r16 < L) {
+            const u32x4* src = reinterpret_cast<const u32x4*>(kp + entry_off<FMT>(r16, g, Hkv, E, hnd) + 64 * grp);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) kreg[c] = src[c];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int tok = 4 * grp + i;
+            if (tok0 + tok < L)
+                vreg[i] = *reinterpret_cast<const u32x4*>(vp + entry_off<FMT>(tok, g, Hkv, E, hnd) + 16 * r16);
+        }
+    };
+
+    if (p0 < p1) {
+        if constexpr (kStaged) stage_load(p0);
+        else direct_load(p0);
+    }
+
+    for (int pg = p0; pg < p1; ++pg) {
+        const int32_t blk = bt_row[pg];
+        const int nv = blk < 0 ? 0 : min(kBs, L - pg * kBs);  // valid tokens in this page
+        AT a[4];
+        float rowf = p.scale_log2;  // factor of S row r16 (token r16)
+        // V operand pieces (tokens 4*grp + i, dims 8*r16 .. +7) as fp16/bf16 bits
+        uint32_t vw[4][4];  // [token i][dword e] = dims (2e, 2e+1)
+        float vsc[4] = {1.f, 1.f, 1.f, 1.f}, vzr[4] = {0.f, 0.f, 0.f, 0.f};
+
+        if constexpr (kStaged) {
+            __syncthreads();  // previous page fully consumed
+            stage_store();
+            __syncthreads();
+            if (pg + 1 < p1) stage_load(pg + 1);
+            const uint8_t* kpage = pagebuf;
+            const uint8_t* vpage = pagebuf + page_bytes;
+            // ---- K operand for token r16
+            const uint8_t* ke = kpage + entry_off<FMT>(r16, g, Hkv, E, hnd);
+            if constexpr (FMT == FMT_TQ) {
+                float csq = 0.0f;
+                if constexpr (KB == 4) {
+                    const uint8_t* cb = ke + 16 * grp;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint32_t w0 = lds16(cb + 4 * j), w1 = lds16(cb + 4 * j + 2);
+                        const uint32_t by[4] = {w0 & 0xff, w0 >> 8, w1 & 0xff, w1 >> 8};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const uint32_t pr = lut[by[e]];
+                            a[j][2 * e] = __builtin_bit_cast(_Float16, (uint16_t)(pr & 0xffff));
+                            a[j][2 * e + 1] = __builtin_bit_cast(_Float16, (uint16_t)(pr >> 16));
+                        }
+                    }
+                } else {
+                    const uint8_t* cb = ke + 12 * grp;
+#pragma unroll
+                    for (int j = 0; j < 4; j += 2) {
+                        // 6 bytes = dims 32*grp + 8j .. +15 (two 8-code groups)
+                        const uint64_t w = (uint64_t)lds16(cb + 3 * j) | ((uint64_t)lds16(cb + 3 * j + 2) << 16) |
+                                           ((uint64_t)lds16(cb + 3 * j + 4) << 32);
+#pragma unroll
+                        for (int jj = 0; jj < 2; ++jj) {
+                            const uint32_t g24 = (uint32_t)(w >> (24 * jj)) & 0xffffffu;
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                const uint32_t pr = lut[(g24 >> (6 * e)) & 63u];
+                                a[j + jj][2 * e] = __builtin_bit_cast(_Float16, (uint16_t)(pr & 0xffff));
+                                a[j + jj][2 * e + 1] = __builtin_bit_cast(_Float16, (uint16_t)(pr >> 16));
+                            }
+                        }
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) csq = __builtin_fmaf((float)a[j][e], (float)a[j][e], csq);
+                csq = sum_over_groups(csq);
+                const float nrm = f16_bits_to_f32((uint16_t)lds16(ke + p.mse_bytes));
+                rowf = p.scale_log2 * nrm / sqrtf(csq + 1e-16f);
+                // V: tokens 4*grp + i, dims 8*r16 .. +7
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int tok = 4 * grp + i;
+                    const uint8_t* ve = kpage + entry_off<FMT>(tok, g, Hkv, E, hnd) + p.key_packed;
+                    uint32_t codes;
+                    if constexpr (VB == 4) {
+                        codes = lds16(ve + 4 * r16) | (lds16(ve + 4 * r16 + 2) << 16);
+                    } else {
+                        const uint8_t* cp = ve + 3 * r16;
+                        codes = (uint32_t)cp[0] | ((uint32_t)cp[1] << 8) | ((uint32_t)cp[2] << 16);
+                    }
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        uint32_t c0, c1;
+                        if constexpr (VB == 4) {
+                            c0 = (codes >> (8 * e)) & 0xf;
+                            c1 = (codes >> (8 * e + 4)) & 0xf;
+                        } else {
+                            c0 = (codes >> (6 * e)) & 7;
+                            c1 = (codes >> (6 * e + 3)) & 7;
+                        }
+                        vw[i][e] = (uint32_t)__builtin_bit_cast(uint16_t, code_f16(c0)) |
+                                   ((uint32_t)__builtin_bit_cast(uint16_t, code_f16(c1)) << 16);
+                    }
+                    const bool ok = tok < nv;
+                    vsc[i] = ok ? f16_bits_to_f32((uint16_t)lds16(ve + p.val_data)) : 0.0f;
+                    vzr[i] = ok ? f16_bits_to_f32((uint16_t)lds16(ve + p.val_data + 2)) : 0.0f;
+                }
+            } else {
+                // GGUF blocks: lane group grp owns block grp (dims 32*grp .. +31)
+                constexpr int BE = FMT == FMT_Q8_0 ? 34 : 18;
+                const uint8_t* kb = ke + BE * grp;
+                const float d = f16_bits_to_f32((uint16_t)lds16(kb));
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                    for (int e = 0; e < 8; e += 2) {
+                        const int jj = 8 * j + e;  // index inside the 32-block
+                        float x0, x1;
+                        if constexpr (FMT == FMT_Q8_0) {
+                            const uint32_t w = lds16(kb + 2 + jj);
+                            x0 = (float)(int8_t)(w & 0xff);
+                            x1 = (float)(int8_t)(w >> 8);
+                        } else {
+                            const int bi = jj & 15;
+                            const uint32_t w = lds16(kb + 2 + bi);
+                            const int sh = jj < 16 ? 0 : 4;
+                            x0 = (float)((int)((w >> sh) & 0xf) - 8);
+                            x1 = (float)((int)((w >> (8 + sh)) & 0xf) - 8);
+                        }
+                        a[j][e] = (_Float16)(x0 * d);
+                        a[j][e + 1] = (_Float16)(x1 * d);
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int tok = 4 * grp + i;
+                    const bool ok = tok < nv;
+                    const uint8_t* vb = vpage + entry_off<FMT>(tok, g, Hkv, E, hnd) + BE * (r16 >> 2);
+                    const float dv = ok ? f16_bits_to_f32((uint16_t)lds16(vb)) : 0.0f;
+                    const int q0 = 8 * (r16 & 3);  // index inside the block
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float x0, x1;
+                        if constexpr (FMT == FMT_Q8_0) {
+                            const uint32_t w = lds16(vb + 2 + q0 + 2 * e);
+                            x0 = (float)(int8_t)(w & 0xff);
+                            x1 = (float)(int8_t)(w >> 8);
+                        } else {
+                            const int jj = q0 + 2 * e;
+                            const int bi = jj & 15;
+                            const int sh = jj < 16 ? 0 : 4;
+                            const uint32_t w = lds16(vb + 2 + bi);
+                            x0 = (float)((int)((w >> sh) & 0xf) - 8);
+                            x1 = (float)((int)((w >> (8 + sh)) & 0xf) - 8);
+                        }
+                        vw[i][e] = (uint32_t)f32_to_f16_bits(ok ? x0 * dv : 0.0f) |
+                                   ((uint32_t)f32_to_f16_bits(ok ? x1 * dv : 0.0f) << 16);
+                    }
+                }
+            }
+        } else {
+            // f16 / bf16: operands straight from the registers loaded last iteration
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const u32x4 w = kreg[j];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if constexpr (MBF16) {
+                        a[j][2 * e] = __builtin_bit_cast(__bf16, (uint16_t)(w[e] & 0xffff));
+                        a[j][2 * e + 1] = __builtin_bit_cast(__bf16, (uint16_t)(w[e] >> 16));
+                    } else {
+                        a[j][2 * e] = __builtin_bit_cast(_Float16, (uint16_t)(w[e] & 0xffff));
+                        a[j][2 * e + 1] = __builtin_bit_cast(_Float16, (uint16_t)(w[e] >> 16));
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) vw[i][e] = vreg[i][e];
+            if (pg + 1 < p1) direct_load(pg + 1);
+        }
+
+        // ---- S^T = K . Q^T
+        f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sacc = mfma16x16x32(a[j], qb[j], sacc);
+
+        float sv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int tok = 4 * grp + i;
+            float f = rowf;
+            if constexpr (FMT == FMT_TQ) f = shfl(rowf, tok);
+            sv[i] = tok < nv ? sacc[i] * f : kNegInf;
+        }
+        float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+        mx = max_over_groups(mx);
+        const float m_new = fmaxf(m_run, mx);
+        const float m_use = m_new == kNegInf ? 0.0f : m_new;
+        const float alpha = exp2f(m_run - m_use);
+        float pv[4], psum = 0.0f, zsum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            pv[i] = exp2f(sv[i] - m_use);
+            psum += pv[i];
+            if constexpr (FMT == FMT_TQ) zsum = __builtin_fmaf(pv[i], vzr[i], zsum);
+        }
+        l_part = __builtin_fmaf(l_part, alpha, psum);
+        if constexpr (FMT == FMT_TQ) z_part = __builtin_fmaf(z_part, alpha, zsum);
+        m_run = m_new;
+
+        // rescale O rows (heads 4*grp + i) by their heads' alpha
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float al = shfl(alpha, 4 * grp + i);
+#pragma unroll
+            for (int c = 0; c < 8; ++c) oacc[c][i] *= al;
+        }
+
+        // ---- O += P . V
+        PT pa;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float pw = (FMT == FMT_TQ) ? pv[i] * vsc[i] : pv[i];
+            if constexpr (MBF16) pa[i] = (short)f32_to_bf16_bits(pw);
+            else pa[i] = (_Float16)pw;
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            PT vb;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint16_t bits = (uint16_t)((vw[i][c >> 1] >> (16 * (c & 1))) & 0xffff);
+                if constexpr (MBF16) vb[i] = (short)bits;
+                else vb[i] = __builtin_bit_cast(_Float16, bits);
+            }
+            oacc[c] = mfma16x16x16(pa, vb, oacc[c]);
+        }
+    }
+
+    // ---- finalize: per-head sums live in lanes r16 = head; O rows in 4*grp + i
+    const float l_tot = sum_over_groups(l_part);
+    const float z_tot = (FMT == FMT_TQ) ? sum_over_groups(z_part) : 0.0f;
+    const bool single = nsp == 1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int hh = 4 * grp + i;
+        const float lh = shfl(l_tot, hh);
+        const float zh = shfl(z_tot, hh);
+        const float mh = shfl(m_run, hh);
+        if (hh >= G) continue;
+        const int hq = hq0 + hh;
+        if (single) {
+            const float inv = lh > 0.0f ? 1.0f / lh : 0.0f;
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float v0 = (oacc[2 * e][i] + zh) * inv;
+                const float v1 = (oacc[2 * e + 1][i] + zh) * inv;
+                const uint16_t b0 = p.q_bf16 ? f32_to_bf16_bits(v0) : f32_to_f16_bits(v0);
+                const uint16_t b1 = p.q_bf16 ? f32_to_bf16_bits(v1) : f32_to_f16_bits(v1);
+                w[e] = (uint32_t)b0 | ((uint32_t)b1 << 16);
+            }
+            uint16_t* o = reinterpret_cast<uint16_t*>(p.out) + ((int64_t)b * p.Hq + hq) * kD + 8 * r16;
+            *reinterpret_cast<u32x4*>(o) = u32x4{w[0], w[1], w[2], w[3]};
+        } else {
+            float* o = p.part + ((int64_t)item * p.Hq + hq) * (kD + 2);
+            f32x4 lo = {oacc[0][i] + zh, oacc[1][i] + zh, oacc[2][i] + zh, oacc[3][i] + zh};
+            f32x4 hi = {oacc[4][i] + zh, oacc[5][i] + zh, oacc[6][i] + zh, oacc[7][i] + zh};
+            // (D + 2) floats per row: 8-byte aligned only, store as float2
+            float* od = o + 8 * r16;
+            *reinterpret_cast<float2*>(od + 0) = make_float2(lo[0], lo[1]);
+            *reinterpret_cast<float2*>(od + 2) = make_float2(lo[2], lo[3]);
+            *reinterpret_cast<float2*>(od + 4) = make_float2(hi[0], hi[1]);
+            *reinterpret_cast<float2*>(od + 6) = make_float2(hi[2], hi[3]);
+            if (r16 == 0) *reinterpret_cast<float2*>(o + kD) = make_float2(mh, lh);
+        }
+    }
+}
+
+// Combines the split partials of every multi-split sequence:
+// out = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M)   (M = max_s m_s)
+__global__ void __launch_bounds__(256)
+decode_merge_kernel(void* out, const float* __restrict__ part, const int32_t* __restrict__ seqinfo,
+                    int Hq, int q_bf16) {
+    const int b = blockIdx.x;
+    const int first = seqinfo[2 * b], nsp = seqinfo[2 * b + 1];
+    if (nsp <= 1) return;
+    for (int idx = threadIdx.x; idx < Hq * kD; idx += blockDim.x) {
+        const int h = idx / kD, d = idx % kD;
+        float M = kNegInf;
+        for (int s = 0; s < nsp; ++s) M = fmaxf(M, part[((int64_t)(first + s) * Hq + h) * (kD + 2) + kD]);
+        const float Mu = M == kNegInf ? 0.0f : M;
+        float acc = 0.0f, lsum = 0.0f;
+        for (int s = 0; s < nsp; ++s) {
+            const float* r = part + ((int64_t)(first + s) * Hq + h) * (kD + 2);
+            const float w = exp2f(r[kD] - Mu);
+            lsum = __builtin_fmaf(r[kD + 1], w, lsum);
+            acc = __builtin_fmaf(r[d], w, acc);
+        }
+        const float v = lsum > 0.0f ? acc / lsum : 0.0f;
+        uint16_t* o = reinterpret_cast<uint16_t*>(out) + ((int64_t)b * Hq + h) * kD + d;
+        *o = q_bf16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
+    }
+}
+
+// ------------------------------------------------------------------ host
+
+constexpr int kTargetItems = 1024;
+constexpr int kPpsMin = 4;
+constexpr int kDefaultMaxSplits = 64;
+
+int max_items(int B) { return kTargetItems + B; }
+
+size_t workspace_bytes_for(int B, int Hq) {
+    const size_t seqinfo = ((size_t)B * 2 * sizeof(int32_t) + 255) / 256 * 256;
+    return seqinfo + (size_t)max_items(B) * Hq * (kD + 2) * sizeof(float);
+}
+
+template <int FMT, int KB, int VB, bool MBF16>
+int launch_decode(DecodeParams& prm, size_t lds, hipStream_t stream) {
+    const int items = max_items(prm.B);
+    auto kern = paged_decode_kernel<FMT, KB, VB, MBF16>;
+    if (lds > 64 * 1024) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+            return VMC_EIO;
+    }
+    hipLaunchKernelGGL(kern, dim3(items), dim3(64 * prm.Hkv), lds, stream, prm);
+    VMC_LAUNCH_CHECK();
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(prm.B), dim3(256), 0, stream, prm.out, prm.part,
+                       prm.seqinfo, prm.Hq, prm.q_bf16);
+    VMC_LAUNCH_CHECK();
+    return VMC_OK;
+}
+
+int setup_common(DecodeParams& prm, void* out, const void* query, const int32_t* bt,
+                 const int32_t* seq_lens, int B, int Hq, int Hkv, int D, int bs, int max_blocks,
+                 float scale, int max_splits, void* ws, size_t ws_bytes) {
+    if (D != kD || bs != kBs) return VMC_EINVAL;
+    if (B < 0 || Hq <= 0 || Hkv <= 0 || Hkv > 8 || Hq % Hkv != 0 || Hq / Hkv > 16) return VMC_EINVAL;
+    if (max_blocks <= 0) return VMC_EINVAL;
+    if (B > 0 && (!out || !query || !bt || !seq_lens || !ws)) return VMC_EINVAL;
+    if (ws_bytes < workspace_bytes_for(B, Hq)) return VMC_ENOMEM;
+    prm.out = out;
+    prm.q = reinterpret_cast<const uint16_t*>(query);
+    prm.bt = bt;
+    prm.seq_lens = seq_lens;
+    prm.B = B;
+    prm.Hq = Hq;
+    prm.Hkv = Hkv;
+    prm.G = Hq / Hkv;
+    prm.max_blocks = max_blocks;
+    prm.scale_log2 = scale * kLog2e;
+    const size_t seqinfo = ((size_t)B * 2 * sizeof(int32_t) + 255) / 256 * 256;
+    prm.seqinfo = reinterpret_cast<int32_t*>(ws);
+    prm.part = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(ws) + seqinfo);
+    prm.target_items = kTargetItems;
+    prm.pps_min = kPpsMin;
+    prm.max_splits = max_splits > 0 ? max_splits : kDefaultMaxSplits;
+    return VMC_OK;
+}
+
+}  // namespace
+}  // namespace vmc
+
+using namespace vmc;
+
+extern "C" size_t vmc_paged_decode_workspace_size(int batch_size, int num_heads, int head_dim,
+                                                  int max_num_blocks_per_req, int block_size,
+                                                  int max_num_kv_splits) {
+    (void)head_dim;
+    (void)max_num_blocks_per_req;
+    (void)block_size;
+    (void)max_num_kv_splits;
+    if (batch_size < 0 || num_heads <= 0) return 0;
+    return workspace_bytes_for(batch_size, num_heads);
+}
+
+extern "C" size_t vmc_turboquant_decode_workspace_size(int batch_size, int num_heads, int head_dim,
+                                                       int64_t max_num_blocks_per_req,
+                                                       int64_t block_size, int max_num_kv_splits) {
+    return vmc_paged_decode_workspace_size(batch_size, num_heads, head_dim,
+                                           (int)max_num_blocks_per_req, (int)block_size,
+                                           max_num_kv_splits);
+}
+
+extern "C" int vmc_paged_attention_decode(void* out, const void* query, const void* key_cache,
+                                          const void* value_cache, const int32_t* block_tables,
+                                          const int32_t* seq_lens, int batch_size, int num_heads,
+                                          int num_kv_heads, int head_dim, int block_size,
+                                          int max_num_blocks_per_req, float scale, int q_dtype,
+                                          int kv_format, int layout, int max_num_kv_splits,
+                                          void* workspace, size_t workspace_bytes,
+                                          vmc_stream_t stream) {
+    DecodeParams prm = {};
+    int rc = setup_common(prm, out, query, block_tables, seq_lens, batch_size, num_heads,
+                          num_kv_heads, head_dim, block_size, max_num_blocks_per_req, scale,
+                          max_num_kv_splits, workspace, workspace_bytes);
+    if (rc != VMC_OK) return rc;
+    if (q_dtype != VMC_DTYPE_F16 && q_dtype != VMC_DTYPE_BF16) return VMC_EINVAL;
+    if (layout != VMC_LAYOUT_NHD && layout != VMC_LAYOUT_HND) return VMC_EINVAL;
+    const int64_t E = vmc_kv_entry_bytes(kv_format, head_dim);
+    if (E < 0) return VMC_EINVAL;
+    if (batch_size == 0) return VMC_OK;
+    if (!key_cache || !value_cache) return VMC_EINVAL;
+    prm.kc = reinterpret_cast<const uint8_t*>(key_cache);
+    prm.vc = reinterpret_cast<const uint8_t*>(value_cache);
+    prm.q_bf16 = q_dtype == VMC_DTYPE_BF16;
+    prm.entry_bytes = (int)E;
+    prm.page_bytes = (int64_t)kBs * num_kv_heads * E;
+    prm.hnd = layout == VMC_LAYOUT_HND;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (kv_format == VMC_KV_Q8_0 || kv_format == VMC_KV_Q4_0) {
+        const int n16 = (int)(2 * prm.page_bytes / 16);
+        if ((prm.page_bytes % 16) != 0 || n16 > kMaxStage * 64 * num_kv_heads) return VMC_EINVAL;
+    }
+    const size_t lds_q = (size_t)2 * prm.page_bytes;
+    switch (kv_format) {
+        case VMC_KV_F16: return launch_decode<FMT_F16, 0, 0, false>(prm, 0, s);
+        case VMC_KV_BF16: return launch_decode<FMT_BF16, 0, 0, true>(prm, 0, s);
+        case VMC_KV_Q8_0: return launch_decode<FMT_Q8_0, 0, 0, false>(prm, lds_q, s);
+        case VMC_KV_Q4_0: return launch_decode<FMT_Q4_0, 0, 0, false>(prm, lds_q, s);
+        default: return VMC_EINVAL;
+    }
+}
+
+extern "C" int vmc_turboquant_decode_attention(void* output, const void* query, const void* kv_cache,
+                                               const int32_t* block_tables, const int32_t* seq_lens,
+                                               int batch_size, int num_heads, int num_kv_heads,
+                                               int head_dim, float scale, int64_t block_size,
+                                               int64_t max_num_blocks_per_req,
+                                               const vmc_tq_config* cfg, int half_dtype,
+                                               int max_num_kv_splits, void* workspace,
+                                               size_t workspace_bytes, vmc_stream_t stream) {
+    if (!tq_config_valid(cfg) || cfg->head_dim != head_dim) return VMC_EINVAL;
+    if (half_dtype != VMC_DTYPE_F16 && half_dtype != VMC_DTYPE_BF16) return VMC_EINVAL;
+    if (max_num_blocks_per_req > 0x7fffffff) return VMC_EINVAL;
+    DecodeParams prm = {};
+    int rc = setup_common(prm, output, query, block_tables, seq_lens, batch_size, num_heads,
+                          num_kv_heads, head_dim, (int)block_size, (int)max_num_blocks_per_req,
+                          scale, max_num_kv_splits, workspace, workspace_bytes);
+    if (rc != VMC_OK) return rc;
+    if (batch_size == 0) return VMC_OK;
+    if (!kv_cache) return VMC_EINVAL;
+    // stored norm/scale/zero are half_dtype; the kernel reads them as fp16
+    if (half_dtype != VMC_DTYPE_F16) return VMC_EINVAL;
+    prm.kc = reinterpret_cast<const uint8_t*>(kv_cache);
+    prm.vc = prm.kc;
+    prm.q_bf16 = 0;
+    prm.entry_bytes = cfg->slot_size_aligned;
+    prm.page_bytes = (int64_t)kBs * num_kv_heads * cfg->slot_size_aligned;
+    prm.hnd = 0;
+    prm.mse_bytes = cfg->mse_bytes;
+    prm.key_packed = cfg->key_packed_size;
+    prm.val_data = cfg->val_data_bytes;
+    prm.tab = tq_tables(head_dim, cfg->key_quant_bits);
+    if ((prm.page_bytes % 16) != 0 || prm.page_bytes / 16 > kMaxStage * 64 * num_kv_heads)
+        return VMC_EINVAL;
+    const size_t lds = 1024 + (size_t)prm.page_bytes;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int kb = cfg->key_quant_bits, vb = cfg->value_quant_bits;
+    if (kb == 4 && vb == 4) return launch_decode<FMT_TQ, 4, 4, false>(prm, lds, s);
+    if (kb == 3 && vb == 3) return launch_decode<FMT_TQ, 3, 3, false>(prm, lds, s);
+    if (kb == 3 && vb == 4) return launch_decode<FMT_TQ, 3, 4, false>(prm, lds, s);
+    return VMC_EINVAL;
+}
