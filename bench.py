@@ -1,0 +1,288 @@
+"""Benchmark of the attention hot path on one MI355X.
+
+Headline (one JSON line on stdout): the long-context ragged decode step --
+batch 64, 64 query heads, 8 KV heads (GQA 8:1), head_dim 128, context lengths
+log-uniform in [1024, 32768] (seed 4) with one sequence at 32768, 3-bit
+TurboQuant KV (turboquant_3bit_nc, 102-byte slots), block size 16.  A step is
+one single-layer decode: quantize-on-append of one new K/V token per sequence
+into the paged cache, then split-KV paged decode attention over every
+sequence's full context.  Inputs are resident in HBM before timing; the KV
+page pool is replicated into >= 2 GiB of distinct copies and the steps rotate
+through them so the 256 MB last-level cache cannot serve the pages.
+
+Also measured in the same run (extra fields of the same line):
+  * causal prefill: batch 4 x 4096 tokens, 32/8 heads, bf16, fused q8_0
+    quantize-on-append into the paged cache -> TFLOP/s;
+  * cpu_baseline: the CPU restatement of the TurboQuant decode (OpenMP over
+    all host cores) on a bounded sample of the same workload.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+BS = 16
+D = 128
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------ workloads
+
+def decode_workload():
+    rng = np.random.default_rng(4)
+    B, Hq, Hkv = 64, 64, 8
+    lens = np.exp(rng.uniform(np.log(1024), np.log(32768), B)).astype(np.int64)
+    lens[0] = 32768
+    lens = np.clip(lens, 1024, 32768).astype(np.int32)
+    pages = (lens + BS - 1) // BS
+    nblk = int(pages.sum())
+    perm = rng.permutation(nblk).astype(np.int32)
+    max_blocks = int(pages.max())
+    bt = np.full((B, max_blocks), -1, np.int32)
+    k = 0
+    for b in range(B):
+        bt[b, :pages[b]] = perm[k:k + pages[b]]
+        k += pages[b]
+    return dict(B=B, Hq=Hq, Hkv=Hkv, lens=lens, bt=bt, nblk=nblk, max_blocks=max_blocks)
+
+
+def slots_for(bt, lens, positions_of):
+    """slot of (sequence b, position p) = bt[b, p // 16] * 16 + p % 16."""
+    b_idx, p_idx = positions_of
+    return bt[b_idx, p_idx // BS].astype(np.int64) * BS + p_idx % BS
+
+
+# ------------------------------------------------------------------ decode
+
+def bench_decode(args, torch, capi, dev):
+    w = decode_workload()
+    B, Hq, Hkv, lens, bt = w["B"], w["Hq"], w["Hkv"], w["lens"], w["bt"]
+    cfg = capi.tq_config(D, "turboquant_3bit_nc")
+    slot_bytes = cfg.slot_size_aligned
+    pool_bytes = w["nblk"] * BS * Hkv * slot_bytes
+    npool = max(2, math.ceil(2 * 1024 ** 3 / pool_bytes))
+    log(f"decode: B={B} Hq={Hq} Hkv={Hkv} sum(L)={int(lens.sum())} max(L)={int(lens.max())} "
+        f"pool={pool_bytes / 1e6:.1f} MB x {npool} copies")
+    pools = [torch.empty(pool_bytes, dtype=torch.uint8, device=dev) for _ in range(npool)]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4)
+    # fill pool 0 with every token's K/V (N(0,1) fp16) through the store kernel
+    b_all = np.repeat(np.arange(B), lens)
+    p_all = np.concatenate([np.arange(n) for n in lens])
+    slots_all = slots_for(bt, lens, (b_all, p_all))
+    chunk = 65536
+    for s in range(0, slots_all.size, chunk):
+        n = min(chunk, slots_all.size - s)
+        kk = torch.randn((n, Hkv, D), generator=gen, device=dev, dtype=torch.float32).half()
+        vv = torch.randn((n, Hkv, D), generator=gen, device=dev, dtype=torch.float32).half()
+        capi.turboquant_store(kk, vv, pools[0], torch.from_numpy(slots_all[s:s + n]).to(dev), BS, cfg)
+    for i in range(1, npool):
+        pools[i].copy_(pools[0])
+    torch.cuda.synchronize()
+    # per-step inputs: the new token of every sequence (position L-1) and q
+    new_slots = torch.from_numpy(slots_for(bt, lens, (np.arange(B), lens - 1))).to(dev)
+    k_new = torch.randn((B, Hkv, D), generator=gen, device=dev).half()
+    v_new = torch.randn((B, Hkv, D), generator=gen, device=dev).half()
+    q = torch.randn((B, Hq, D), generator=gen, device=dev).half()
+    out = torch.empty_like(q)
+    bt_d = torch.from_numpy(bt).to(dev)
+    lens_d = torch.from_numpy(lens).to(dev)
+    ws = torch.empty(capi.turboquant_decode_workspace_size(B, Hq, D, bt.shape[1], BS),
+                     dtype=torch.uint8, device=dev)
+    scale = 1.0 / math.sqrt(D)
+    stream = torch.cuda.current_stream()
+
+    def step(i):
+        pool = pools[i % npool]
+        capi.turboquant_store(k_new, v_new, pool, new_slots, BS, cfg, stream=stream)
+        capi.turboquant_decode_attention(out, q, pool, bt_d, lens_d, Hkv, scale, cfg, BS,
+                                         workspace=ws, stream=stream)
+
+    def attn_only(i):
+        capi.turboquant_decode_attention(out, q, pools[i % npool], bt_d, lens_d, Hkv, scale, cfg,
+                                         BS, workspace=ws, stream=stream)
+
+    def timed(fn, n, warm):
+        for i in range(warm):
+            fn(i)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(n):
+            fn(warm + i)
+        e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / n  # ms
+
+    ms_step = timed(step, args.steps, args.warmup)
+    ms_attn = timed(attn_only, args.steps, args.warmup)
+    assert torch.isfinite(out.float()).all().item(), "decode produced non-finite values"
+
+    sum_l = int(lens.sum())
+    kv_bytes = sum_l * Hkv * slot_bytes
+    qo_bytes = 2 * B * Hq * D * 2
+    table_bytes = int(((lens + BS - 1) // BS).sum()) * 4 + B * 4
+    attn_bytes = kv_bytes + qo_bytes + table_bytes
+    append_bytes = B * Hkv * (2 * D * 2 + slot_bytes) + B * 8
+    step_bytes = attn_bytes + append_bytes
+    res = dict(w=w, ms_step=ms_step, ms_attn=ms_attn, attn_bytes=attn_bytes, step_bytes=step_bytes,
+               kv_bytes=kv_bytes, sum_l=sum_l, q=q, pools=pools, bt=bt, lens=lens, cfg=cfg)
+    log(f"decode step {ms_step * 1e3:.1f} us, attention {ms_attn * 1e3:.1f} us, "
+        f"{attn_bytes / ms_attn / 1e6:.0f} GB/s attention-only")
+    return res
+
+
+# ------------------------------------------------------------------ prefill
+
+def bench_prefill(args, torch, capi, dev):
+    B, S, Hq, Hkv = 4, 4096, 32, 8
+    T = B * S
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3)
+    q = torch.randn((T, Hq, D), generator=gen, device=dev).bfloat16()
+    k = torch.randn((T, Hkv, D), generator=gen, device=dev).bfloat16()
+    v = torch.randn((T, Hkv, D), generator=gen, device=dev).bfloat16()
+    pos = torch.arange(S, dtype=torch.int32, device=dev).repeat(B)
+    nblk = T // BS
+    perm = torch.randperm(nblk, generator=torch.Generator().manual_seed(3)).to(dev)
+    t = torch.arange(T, device=dev)
+    slots = (perm[t // BS] * BS + t % BS).to(torch.int64)
+    E = capi.kv_entry_bytes(capi.KV_Q8_0, D)
+    kc = torch.empty(nblk * BS * Hkv * E, dtype=torch.uint8, device=dev)
+    vc = torch.empty_like(kc)
+    out = torch.empty_like(q)
+    scale = 1.0 / math.sqrt(D)
+    stream = torch.cuda.current_stream()
+
+    def run():
+        capi.flash_attention_prefill(out, q, k, v, pos, Hkv, scale, key_cache=kc, value_cache=vc,
+                                     slot_mapping=slots, block_size=BS, kv_format=capi.KV_Q8_0,
+                                     stream=stream)
+
+    for _ in range(max(2, args.warmup // 2)):
+        run()
+    torch.cuda.synchronize()
+    n = max(5, args.steps // 2)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(n):
+        run()
+    e1.record(stream)
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / n
+    flops = 4.0 * B * Hq * D * S * (S + 1) / 2
+    tflops = flops / (ms * 1e-3) / 1e12
+    assert torch.isfinite(out.float()).all().item(), "prefill produced non-finite values"
+    log(f"prefill {ms * 1e3:.1f} us, {tflops:.1f} TFLOP/s")
+    return dict(ms=ms, tflops=tflops, flops=flops)
+
+
+# ------------------------------------------------------------------ CPU baseline
+
+def cpu_baseline(dec, torch):
+    """CPU restatement of the TurboQuant two-stage decode (oracle, OpenMP) on
+    the 32768-token sequence plus the next sequences until ~1/8 of the tokens."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+    lens, bt = dec["lens"], dec["bt"]
+    order = list(range(len(lens)))
+    pick, tok = [], 0
+    for b in order:
+        pick.append(b)
+        tok += int(lens[b])
+        if tok >= dec["sum_l"] // 8:
+            break
+    cache = dec["pools"][0].cpu().numpy()
+    qb = dec["q"].cpu().numpy().view(np.uint16)[pick]
+    L = O.tq_layout("turboquant_3bit_nc")
+    c, _ = O.tq_tables(D, 3)
+    nthreads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+    t0 = time.time()
+    O.tq_decode(qb, cache, bt[pick], lens[pick], dec["w"]["Hkv"], np.float32(1 / math.sqrt(D)), BS,
+                L, c, num_splits=32, nthreads=nthreads)
+    dt = time.time() - t0
+    Hq, Hkv = dec["w"]["Hq"], dec["w"]["Hkv"]
+    sample_bytes = tok * Hkv * dec["cfg"].slot_size_aligned + 2 * len(pick) * Hq * D * 2
+    return dict(value=round(sample_bytes / dt / 1e9, 3), unit="GB/s", cores=nthreads, kind="port",
+                sample=f"{len(pick)} of 64 sequences ({tok} tokens incl. the 32768 one), "
+                       f"two-stage TurboQuant decode restated in C, {dt:.2f} s")
+
+
+# ------------------------------------------------------------------ main
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--skip-prefill", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the attention hot path is single-device here "
+              "(sharding by KV head / sequence is a design note, not a run). Use --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from vm_c_amd import capi
+    capi.load()
+    dev = torch.device("cuda:0")
+    dec = bench_decode(args, torch, capi, dev)
+    pre = None if args.skip_prefill else bench_prefill(args, torch, capi, dev)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(dec, torch)
+
+    ms_step = dec["ms_step"]
+    gbs_step = dec["step_bytes"] / (ms_step * 1e-3) / 1e9
+    gbs_attn = dec["attn_bytes"] / (dec["ms_attn"] * 1e-3) / 1e9
+    line = {
+        "metric": "decode attn HBM GB/s (% peak) + tokens/s at 32k ctx; prefill TFLOP/s",
+        "value": round(gbs_step, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8 codes + fp16",
+        "data": "synthetic",
+        "config": {"workload": "ragged 32k-context TurboQuant 3-bit paged decode step "
+                               "(append 1 token/seq + split-KV attention)",
+                   "batch": 64, "num_heads": 64, "num_kv_heads": 8, "head_dim": 128,
+                   "block_size": 16, "kv": "turboquant_3bit_nc (102 B slot)",
+                   "ctx": "log-uniform [1024, 32768] seed 4, one at 32768",
+                   "sum_ctx": dec["sum_l"], "parallelism": "single GPU"},
+        "pct_peak_hbm": round(100 * gbs_step / HBM_PEAK_GBS, 2),
+        "tokens_per_s": round(dec["w"]["B"] / (ms_step * 1e-3), 1),
+        "roofline": {"bound": "hbm", "achieved": round(gbs_attn, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs_attn / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "TurboQuant split-KV decode (decode + merge launches)",
+                     "ms": round(dec["ms_attn"], 4), "bytes": dec["attn_bytes"]},
+        "cpu_baseline": cpu,
+    }
+    if pre is not None:
+        line["prefill"] = {"workload": "causal prefill B=4 S=4096 Hq=32 Hkv=8 bf16, fused q8_0 append",
+                           "ms": round(pre["ms"], 4), "tflops": round(pre["tflops"], 1),
+                           "pct_peak_mfma_bf16": round(100 * pre["tflops"] / MFMA_BF16_PEAK_TFLOPS, 2)}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

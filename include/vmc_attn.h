@@ -168,6 +168,13 @@ int vmc_flash_attention_prefill(void* output, const void* query, const void* key
                                 int64_t block_size, int kv_format, int layout,
                                 vmc_stream_t stream);
 
+/* Device self-check of the lane-level assumptions the kernels rely on (MFMA
+ * operand/result layouts of the shapes used, cross-row reductions, the
+ * wave-private LDS exchange).  No counterpart in the reference: a guard for
+ * toolchain / hardware changes.  Synchronous.  Returns 0 when all pass, a
+ * bitmask of failed checks (> 0), or a negative status. */
+int vmc_selftest(void);
+
 /* Library self-description: "vmc_attn <version> gfx950". */
 const char* vmc_version(void);
 

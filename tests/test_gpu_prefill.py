@@ -1,0 +1,111 @@
+"""Causal prefill parity on the GPU: HIP MFMA prefill vs exact fp64 causal
+attention (oracle), tolerance |got - ref| <= 2e-3 + 1e-2 |ref|; the fused
+quantize-on-append must write the same bytes as the standalone append."""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from kvgen import BS, close_report, f32_to_bf16_bits
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-3, 1e-2
+
+
+def _inputs(seq_lens, Hq, Hkv, D=128, seed=0, bf16=True):
+    rng = np.random.default_rng(seed)
+    T = int(sum(seq_lens))
+    mk = lambda *s: rng.standard_normal(s).astype(np.float32)
+    q, k, v = mk(T, Hq, D), mk(T, Hkv, D), mk(T, Hkv, D)
+    if bf16:
+        qb, kb, vb = (f32_to_bf16_bits(x) for x in (q, k, v))
+    else:
+        qb, kb, vb = (x.astype(np.float16).view(np.uint16) for x in (q, k, v))
+    pos = np.concatenate([np.arange(n) for n in seq_lens]).astype(np.int32)
+    cu = np.concatenate([[0], np.cumsum(seq_lens)]).astype(np.int32)
+    return qb, kb, vb, pos, cu
+
+
+def _run(dev, qb, kb, vb, pos, Hkv, scale, bf16=True, append=None):
+    import torch
+    from vm_c_amd import capi
+    tdt = torch.bfloat16 if bf16 else torch.float16
+    to = lambda a: torch.from_numpy(a.view(np.int16)).to(dev).view(tdt)
+    q, k, v = to(qb), to(kb), to(vb)
+    out = torch.full_like(q, float("nan"))
+    kw = {}
+    if append is not None:
+        fmt, slots, nbytes = append
+        kc = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        vc = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        kw = dict(key_cache=kc, value_cache=vc, slot_mapping=torch.from_numpy(slots).to(dev),
+                  block_size=BS, kv_format=fmt)
+    capi.flash_attention_prefill(out, q, k, v, torch.from_numpy(pos).to(dev), Hkv, scale, **kw)
+    torch.cuda.synchronize()
+    res = out.float().cpu().numpy()
+    if append is not None:
+        return res, kw["key_cache"].cpu().numpy(), kw["value_cache"].cpu().numpy()
+    return res
+
+
+@pytest.mark.parametrize("bf16", [True, False])
+@pytest.mark.parametrize("seq_lens,Hq,Hkv", [([300, 77], 8, 2), ([1, 2, 129, 64, 200], 4, 4),
+                                              ([513], 8, 1)])
+def test_prefill_all_rows_vs_exact(dev, bf16, seq_lens, Hq, Hkv):
+    qb, kb, vb, pos, cu = _inputs(seq_lens, Hq, Hkv, seed=len(seq_lens), bf16=bf16)
+    T = qb.shape[0]
+    scale = 1.0 / np.sqrt(128)
+    got = _run(dev, qb, kb, vb, pos, Hkv, scale, bf16=bf16)
+    toks = np.repeat(np.arange(T), Hq)
+    heads = np.tile(np.arange(Hq), T)
+    ex = O.prefill_exact_rows(qb, kb, vb, cu, Hkv, scale, toks, heads, is_bf16=bf16)
+    ok, err = close_report(got.reshape(T * Hq, 128), ex, ATOL, RTOL)
+    assert ok, f"max err {err}"
+
+
+def _slots_for(T, seed):
+    rng = np.random.default_rng(seed)
+    nblk = (T + BS - 1) // BS
+    perm = rng.permutation(nblk).astype(np.int64)
+    t = np.arange(T)
+    return perm[t // BS] * BS + t % BS, nblk
+
+
+@pytest.mark.parametrize("fmt", [O.KV_Q8_0, O.KV_Q4_0, O.KV_F16, O.KV_BF16])
+def test_prefill_fused_append_bitexact(dev, fmt):
+    seq_lens, Hq, Hkv = [333, 190], 8, 2
+    qb, kb, vb, pos, cu = _inputs(seq_lens, Hq, Hkv, seed=13)
+    T = qb.shape[0]
+    slots, nblk = _slots_for(T, 3)
+    slots[7] = -1
+    E = O.entry_bytes(fmt, 128)
+    nbytes = nblk * BS * Hkv * E
+    got, kc, vc = _run(dev, qb, kb, vb, pos, Hkv, 1.0 / np.sqrt(128), append=(fmt, slots, nbytes))
+    kr = np.zeros(nbytes, np.uint8)
+    vr = np.zeros(nbytes, np.uint8)
+    O.kv_append(kb, vb, slots, kr, vr, BS, fmt, src_bf16=True)
+    assert np.array_equal(kc, kr) and np.array_equal(vc, vr)
+
+
+def test_prefill_config4_full_size(dev):
+    """B=4, S=4096, Hq=32, Hkv=8, bf16, causal, fused q8_0 append (seed 3):
+    sampled rows vs exact fp64, every page byte vs the oracle's append."""
+    seq_lens, Hq, Hkv = [4096] * 4, 32, 8
+    qb, kb, vb, pos, cu = _inputs(seq_lens, Hq, Hkv, seed=3)
+    T = qb.shape[0]
+    slots, nblk = _slots_for(T, 4)
+    E = O.entry_bytes(O.KV_Q8_0, 128)
+    nbytes = nblk * BS * Hkv * E
+    scale = 1.0 / np.sqrt(128)
+    got, kc, vc = _run(dev, qb, kb, vb, pos, Hkv, scale, append=(O.KV_Q8_0, slots, nbytes))
+    rng = np.random.default_rng(0)
+    toks = np.concatenate([rng.integers(0, T, 96), [0, 4095, 4096, T - 1, 127, 128]])
+    heads = rng.integers(0, Hq, toks.size)
+    ex = O.prefill_exact_rows(qb, kb, vb, cu, Hkv, scale, toks, heads)
+    ok, err = close_report(got[toks, heads], ex, ATOL, RTOL)
+    assert ok, f"max err {err}"
+    assert np.isfinite(got).all()
+    kr = np.zeros(nbytes, np.uint8)
+    vr = np.zeros(nbytes, np.uint8)
+    O.kv_append(kb, vb, slots, kr, vr, BS, O.KV_Q8_0, src_bf16=True)
+    assert np.array_equal(kc, kr) and np.array_equal(vc, vr)

@@ -20,7 +20,8 @@ EXPORTS = [
     "vmc_kv_entry_bytes", "vmc_reshape_and_cache", "vmc_paged_decode_workspace_size",
     "vmc_paged_attention_decode", "vmc_tq_config_from_method", "vmc_tq_host_tables",
     "vmc_turboquant_store", "vmc_turboquant_decode_workspace_size",
-    "vmc_turboquant_decode_attention", "vmc_flash_attention_prefill", "vmc_version",
+    "vmc_turboquant_decode_attention", "vmc_flash_attention_prefill", "vmc_selftest",
+    "vmc_version",
 ]
 
 
@@ -72,6 +73,8 @@ def load():
     L.vmc_flash_attention_prefill.restype = _I
     L.vmc_flash_attention_prefill.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P, _P,
                                               _P, _I64, _I, _I, _P]
+    L.vmc_selftest.restype = _I
+    L.vmc_selftest.argtypes = []
     L.vmc_version.restype = C.c_char_p
     L.vmc_version.argtypes = []
     _lib = L
@@ -100,6 +103,21 @@ def _dtype_code(t):
     if t.dtype == torch.bfloat16:
         return DTYPE_BF16
     raise VmcError(f"unsupported dtype {t.dtype}")
+
+
+SELFTEST_CHECKS = {1: "sum over rows", 2: "max over rows", 4: "LDS gather",
+                   8: "mfma 16x16x32 f16", 16: "mfma 16x16x16 f16", 32: "mfma 32x32x16 f16",
+                   64: "mfma 16x16x32 bf16", 128: "mfma 32x32x16 bf16"}
+
+
+def selftest():
+    """Run the device self-check; raises VmcError naming the failed checks."""
+    rc = load().vmc_selftest()
+    if rc < 0:
+        raise VmcError(f"vmc_selftest failed with status {rc}")
+    if rc:
+        raise VmcError("device self-check failed: " +
+                       ", ".join(n for b, n in SELFTEST_CHECKS.items() if rc & b))
 
 
 def version():

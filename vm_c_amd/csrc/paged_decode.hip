@@ -37,15 +37,37 @@
 #include "vmc_common.hpp"
 #include "vmc_tq.hpp"
 
+#include <utility>
+
 namespace vmc {
 namespace {
 
 constexpr int kD = 128;
 constexpr int kBs = 16;
-constexpr int kMaxStage = 8;  // 16-byte chunks per thread for one page
+constexpr int kMaxItemPages = 1024;  // block-table slice of one work item, staged in LDS
 constexpr float kNegInf = -__builtin_inff();
 
 enum { FMT_F16 = 0, FMT_BF16 = 1, FMT_Q8_0 = 2, FMT_Q4_0 = 3, FMT_TQ = 4 };
+
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Register staging of LDS-staged formats: SPP 16-byte chunks per thread per
+// page (= ceil(bytes per token-head / 64) for one wave per KV head) and PF
+// pages in flight per workgroup.
+template <int FMT, int KB, int VB>
+struct StagePlan {
+    static constexpr int entry = FMT == FMT_TQ ? (16 * KB + 2 + 16 * VB + 4 + 1) / 2 * 2
+                                 : FMT == FMT_Q8_0 ? 2 * 136 : FMT == FMT_Q4_0 ? 2 * 72 : 0;
+    static constexpr int spp = entry > 0 ? (entry + 63) / 64 : 1;
+    static constexpr int pf = entry == 0 ? 1 : (spp <= 2 ? 4 : (spp <= 3 ? 3 : 2));
+};
 
 struct DecodeParams {
     void* out;
@@ -94,7 +116,7 @@ __device__ void compute_plan(const DecodeParams& p, int item, Plan* out) {
         int nsp = 0, ppsb = 0;
         if (b < p.B) {
             nsp = pages > 0 ? min(p.max_splits, (pages + pps - 1) / pps) : 1;
-            ppsb = pages > 0 ? (pages + nsp - 1) / nsp : 0;
+            ppsb = pages > 0 ? min(kMaxItemPages, (pages + nsp - 1) / nsp) : 0;
             nsp = pages > 0 ? (pages + ppsb - 1) / ppsb : 1;
         }
         int incl = nsp;
@@ -167,6 +189,8 @@ paged_decode_kernel(DecodeParams p) {
     using PT = typename std::conditional<MBF16, s16x4, f16x4>::type;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ Plan plan;
+    __shared__ __attribute__((aligned(16))) float wscr_all[8][48];  // per-wave exchange
+    __shared__ int32_t bt_lds[kMaxItemPages];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
@@ -179,16 +203,21 @@ paged_decode_kernel(DecodeParams p) {
     uint8_t* pagebuf = smem + (FMT == FMT_TQ ? 1024 : 0);
     if constexpr (FMT == FMT_TQ) build_pair_lut<KB>(lut, p.tab);
     __syncthreads();
-    const int b = plan.b;
+    const int b = __builtin_amdgcn_readfirstlane(plan.b);
     if (b < 0) return;
-    const int s = plan.s, nsp = plan.nsp, L = plan.L;
-    const int p0 = plan.p0, p1 = plan.p1;
+    // wave-uniform: keep them in SGPRs so block-table reads are scalar loads
+    const int s = __builtin_amdgcn_readfirstlane(plan.s);
+    const int nsp = __builtin_amdgcn_readfirstlane(plan.nsp);
+    const int L = __builtin_amdgcn_readfirstlane(plan.L);
+    const int p0 = __builtin_amdgcn_readfirstlane(plan.p0);
+    const int p1 = __builtin_amdgcn_readfirstlane(plan.p1);
     if (s == 0 && tid == 0) {
         p.seqinfo[2 * b] = plan.first_item;
         p.seqinfo[2 * b + 1] = nsp;
     }
 
     const int g = wave;  // kv head of this wave
+    float* wscr = wscr_all[wave];
     const int G = p.G;
     const int hq0 = g * G;
     const int64_t qrow = ((int64_t)b * p.Hq + hq0 + r16) * kD;
@@ -272,37 +301,51 @@ paged_decode_kernel(DecodeParams p) {
 
     const int Hkv = p.Hkv, E = p.entry_bytes, hnd = p.hnd;
     const int64_t page_bytes = p.page_bytes;
-    const int32_t* bt_row = p.bt + (int64_t)b * p.max_blocks;
+    // this item's block-table slice -> LDS, so the page loop issues no vector
+    // loads besides the page prefetch (keeps the load counter exact)
+    {
+        const int32_t* bt_row = p.bt + (int64_t)b * p.max_blocks;
+        for (int i = tid; i < p1 - p0; i += blockDim.x) bt_lds[i] = bt_row[p0 + i];
+        __syncthreads();
+    }
     const int nthreads = blockDim.x;
 
-    // staged formats: page(s) -> registers -> LDS
+    // staged formats: PF pages in flight in registers -> LDS double buffer
+    using SP = StagePlan<FMT, KB, VB>;
+    constexpr int SPP = SP::spp, PF = SP::pf;
     const int n16_k = (int)(page_bytes / 16);
     const int n16 = (FMT == FMT_TQ) ? n16_k : 2 * n16_k;
-    u32x4 stage[kMaxStage];
-    auto stage_load = [&](int pg) {
-        const int32_t blk = bt_row[pg];
-        if (blk < 0) return;
+    const int lds_page = (FMT == FMT_TQ) ? (int)page_bytes : 2 * (int)page_bytes;
+    u32x4 stage[PF][SPP];
+    auto stage_load = [&](auto slot_c, int pg) __attribute__((always_inline)) {
+        constexpr int S = decltype(slot_c)::value;
+        // Branch-free so the compiler can count outstanding loads exactly (a
+        // hole reads page 0, whose tokens are then masked; chunks past the
+        // page re-read its last chunk and are not stored).
+        const int32_t blk = max(bt_lds[pg - p0], 0);
         const u32x4* ks = reinterpret_cast<const u32x4*>(p.kc + (int64_t)blk * page_bytes);
         const u32x4* vs = reinterpret_cast<const u32x4*>(p.vc + (int64_t)blk * page_bytes);
 #pragma unroll
-        for (int c = 0; c < kMaxStage; ++c) {
-            const int idx = tid + c * nthreads;
-            if (idx < n16) stage[c] = (FMT == FMT_TQ || idx < n16_k) ? ks[idx] : vs[idx - n16_k];
+        for (int c = 0; c < SPP; ++c) {
+            const int idx = min(tid + c * nthreads, n16 - 1);
+            const u32x4* src = (FMT == FMT_TQ || idx < n16_k) ? ks + idx : vs + (idx - n16_k);
+            stage[S][c] = *src;
         }
     };
-    auto stage_store = [&]() {
-        u32x4* dst = reinterpret_cast<u32x4*>(pagebuf);
+    auto stage_store = [&](auto slot_c, uint8_t* dstb) __attribute__((always_inline)) {
+        constexpr int S = decltype(slot_c)::value;
+        u32x4* dst = reinterpret_cast<u32x4*>(dstb);
 #pragma unroll
-        for (int c = 0; c < kMaxStage; ++c) {
+        for (int c = 0; c < SPP; ++c) {
             const int idx = tid + c * nthreads;
-            if (idx < n16) dst[idx] = stage[c];
+            if (idx < n16) dst[idx] = stage[S][c];
         }
     };
 
     // direct formats: per-lane operand registers for one page
     u32x4 kreg[4], vreg[4];
-    auto direct_load = [&](int pg) {
-        const int32_t blk = bt_row[pg];
+    auto direct_load = [&](int pg) __attribute__((always_inline)) {
+        const int32_t blk = bt_lds[pg - p0];
         const int tok0 = pg * kBs;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -325,13 +368,8 @@ paged_decode_kernel(DecodeParams p) {
         }
     };
 
-    if (p0 < p1) {
-        if constexpr (kStaged) stage_load(p0);
-        else direct_load(p0);
-    }
-
-    for (int pg = p0; pg < p1; ++pg) {
-        const int32_t blk = bt_row[pg];
+    auto process = [&](int pg, const uint8_t* kpage, const uint8_t* vpage) __attribute__((always_inline)) {
+        const int32_t blk = bt_lds[pg - p0];
         const int nv = blk < 0 ? 0 : min(kBs, L - pg * kBs);  // valid tokens in this page
         AT a[4];
         float rowf = p.scale_log2;  // factor of S row r16 (token r16)
@@ -340,12 +378,6 @@ paged_decode_kernel(DecodeParams p) {
         float vsc[4] = {1.f, 1.f, 1.f, 1.f}, vzr[4] = {0.f, 0.f, 0.f, 0.f};
 
         if constexpr (kStaged) {
-            __syncthreads();  // previous page fully consumed
-            stage_store();
-            __syncthreads();
-            if (pg + 1 < p1) stage_load(pg + 1);
-            const uint8_t* kpage = pagebuf;
-            const uint8_t* vpage = pagebuf + page_bytes;
             // ---- K operand for token r16
             const uint8_t* ke = kpage + entry_off<FMT>(r16, g, Hkv, E, hnd);
             if constexpr (FMT == FMT_TQ) {
@@ -499,13 +531,13 @@ paged_decode_kernel(DecodeParams p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) sacc = mfma16x16x32(a[j], qb[j], sacc);
 
+        f32x4 rf = {rowf, rowf, rowf, rowf};
+        if constexpr (FMT == FMT_TQ) rf = gather4_from_row0(rowf, wscr, r16, grp);
         float sv[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int tok = 4 * grp + i;
-            float f = rowf;
-            if constexpr (FMT == FMT_TQ) f = shfl(rowf, tok);
-            sv[i] = tok < nv ? sacc[i] * f : kNegInf;
+            sv[i] = tok < nv ? sacc[i] * rf[i] : kNegInf;
         }
         float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
         mx = max_over_groups(mx);
@@ -524,12 +556,11 @@ paged_decode_kernel(DecodeParams p) {
         m_run = m_new;
 
         // rescale O rows (heads 4*grp + i) by their heads' alpha
+        const f32x4 al = gather4_from_row0(alpha, wscr + 16, r16, grp);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float al = shfl(alpha, 4 * grp + i);
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int c = 0; c < 8; ++c) oacc[c][i] *= al;
-        }
+            for (int c = 0; c < 8; ++c) oacc[c][i] *= al[i];
 
         // ---- O += P . V
         PT pa;
@@ -550,18 +581,52 @@ paged_decode_kernel(DecodeParams p) {
             }
             oacc[c] = mfma16x16x16(pa, vb, oacc[c]);
         }
+    };
+
+    if constexpr (kStaged) {
+        // Ring of PF register slots: slot S holds page base+S+PF while page
+        // base+S is computed from LDS.  Loads and LDS stores are unconditional
+        // (tail pages clamp to the last page), so the only branch holds no
+        // memory loads and the compiler keeps exact load counters: each LDS
+        // store waits only for its own slot, PF-1 pages stay in flight.
+        const int npg = p1 - p0;
+        if (npg > 0) {
+            static_for<PF>([&](auto sc) __attribute__((always_inline)) {
+                stage_load(sc, p0 + min((int)decltype(sc)::value, npg - 1));
+            });
+            stage_store(std::integral_constant<int, 0>{}, pagebuf);
+            __syncthreads();
+            for (int base = 0; base < npg; base += PF) {
+                static_for<PF>([&](auto sc) __attribute__((always_inline)) {
+                    constexpr int S = decltype(sc)::value;
+                    const int i = base + S;
+                    const int cur = i & 1;
+                    if (i < npg) {  // uniform over the workgroup
+                        const uint8_t* kp = pagebuf + cur * lds_page;
+                        process(p0 + i, kp, kp + page_bytes);
+                    }
+                    stage_load(sc, p0 + min(i + PF, npg - 1));
+                    stage_store(std::integral_constant<int, (S + 1) % PF>{}, pagebuf + (cur ^ 1) * lds_page);
+                    __syncthreads();
+                });
+            }
+        }
+    } else {
+        if (p0 < p1) direct_load(p0);
+        for (int pg = p0; pg < p1; ++pg) process(pg, nullptr, nullptr);
     }
 
     // ---- finalize: per-head sums live in lanes r16 = head; O rows in 4*grp + i
     const float l_tot = sum_over_groups(l_part);
     const float z_tot = (FMT == FMT_TQ) ? sum_over_groups(z_part) : 0.0f;
     const bool single = nsp == 1;
+    const f32x4 lh4 = gather4_from_row0(l_tot, wscr, r16, grp);
+    const f32x4 zh4 = gather4_from_row0(z_tot, wscr + 16, r16, grp);
+    const f32x4 mh4 = gather4_from_row0(m_run, wscr + 32, r16, grp);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int hh = 4 * grp + i;
-        const float lh = shfl(l_tot, hh);
-        const float zh = shfl(z_tot, hh);
-        const float mh = shfl(m_run, hh);
+        const float lh = lh4[i], zh = zh4[i], mh = mh4[i];
         if (hh >= G) continue;
         const int hq = hq0 + hh;
         if (single) {
@@ -592,30 +657,31 @@ paged_decode_kernel(DecodeParams p) {
     }
 }
 
-// Combines the split partials of every multi-split sequence:
+// Combines the split partials of every multi-split sequence, one workgroup
+// per (sequence, head), one thread per dim:
 // out = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M)   (M = max_s m_s)
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(kD)
 decode_merge_kernel(void* out, const float* __restrict__ part, const int32_t* __restrict__ seqinfo,
                     int Hq, int q_bf16) {
-    const int b = blockIdx.x;
+    const int b = blockIdx.x / Hq, h = blockIdx.x % Hq;
     const int first = seqinfo[2 * b], nsp = seqinfo[2 * b + 1];
     if (nsp <= 1) return;
-    for (int idx = threadIdx.x; idx < Hq * kD; idx += blockDim.x) {
-        const int h = idx / kD, d = idx % kD;
-        float M = kNegInf;
-        for (int s = 0; s < nsp; ++s) M = fmaxf(M, part[((int64_t)(first + s) * Hq + h) * (kD + 2) + kD]);
-        const float Mu = M == kNegInf ? 0.0f : M;
-        float acc = 0.0f, lsum = 0.0f;
-        for (int s = 0; s < nsp; ++s) {
-            const float* r = part + ((int64_t)(first + s) * Hq + h) * (kD + 2);
-            const float w = exp2f(r[kD] - Mu);
-            lsum = __builtin_fmaf(r[kD + 1], w, lsum);
-            acc = __builtin_fmaf(r[d], w, acc);
-        }
-        const float v = lsum > 0.0f ? acc / lsum : 0.0f;
-        uint16_t* o = reinterpret_cast<uint16_t*>(out) + ((int64_t)b * Hq + h) * kD + d;
-        *o = q_bf16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
+    const int d = threadIdx.x;
+    const float* base = part + ((int64_t)first * Hq + h) * (kD + 2);
+    const int64_t stride = (int64_t)Hq * (kD + 2);
+    float M = kNegInf;
+    for (int s = 0; s < nsp; ++s) M = fmaxf(M, base[s * stride + kD]);
+    const float Mu = M == kNegInf ? 0.0f : M;
+    float acc = 0.0f, lsum = 0.0f;
+    for (int s = 0; s < nsp; ++s) {
+        const float* r = base + s * stride;
+        const float w = exp2f(r[kD] - Mu);
+        lsum = __builtin_fmaf(r[kD + 1], w, lsum);
+        acc = __builtin_fmaf(r[d], w, acc);
     }
+    const float v = lsum > 0.0f ? acc / lsum : 0.0f;
+    uint16_t* o = reinterpret_cast<uint16_t*>(out) + ((int64_t)b * Hq + h) * kD + d;
+    *o = q_bf16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
 }
 
 // ------------------------------------------------------------------ host
@@ -624,16 +690,20 @@ constexpr int kTargetItems = 1024;
 constexpr int kPpsMin = 4;
 constexpr int kDefaultMaxSplits = 64;
 
-int max_items(int B) { return kTargetItems + B; }
+// upper bound of the plan's item count: sum_b ceil(pages_b / min(pps, cap))
+// <= target + B (+ B * ceil(max_blocks / cap) when the per-item page cap binds)
+int max_items(int B, int max_blocks) {
+    return kTargetItems + B + B * ((max_blocks + kMaxItemPages - 1) / kMaxItemPages);
+}
 
-size_t workspace_bytes_for(int B, int Hq) {
+size_t workspace_bytes_for(int B, int Hq, int max_blocks) {
     const size_t seqinfo = ((size_t)B * 2 * sizeof(int32_t) + 255) / 256 * 256;
-    return seqinfo + (size_t)max_items(B) * Hq * (kD + 2) * sizeof(float);
+    return seqinfo + (size_t)max_items(B, max_blocks) * Hq * (kD + 2) * sizeof(float);
 }
 
 template <int FMT, int KB, int VB, bool MBF16>
 int launch_decode(DecodeParams& prm, size_t lds, hipStream_t stream) {
-    const int items = max_items(prm.B);
+    const int items = max_items(prm.B, prm.max_blocks);
     auto kern = paged_decode_kernel<FMT, KB, VB, MBF16>;
     if (lds > 64 * 1024) {
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -642,7 +712,7 @@ int launch_decode(DecodeParams& prm, size_t lds, hipStream_t stream) {
     }
     hipLaunchKernelGGL(kern, dim3(items), dim3(64 * prm.Hkv), lds, stream, prm);
     VMC_LAUNCH_CHECK();
-    hipLaunchKernelGGL(decode_merge_kernel, dim3(prm.B), dim3(256), 0, stream, prm.out, prm.part,
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(prm.B * prm.Hq), dim3(kD), 0, stream, prm.out, prm.part,
                        prm.seqinfo, prm.Hq, prm.q_bf16);
     VMC_LAUNCH_CHECK();
     return VMC_OK;
@@ -655,7 +725,7 @@ int setup_common(DecodeParams& prm, void* out, const void* query, const int32_t*
     if (B < 0 || Hq <= 0 || Hkv <= 0 || Hkv > 8 || Hq % Hkv != 0 || Hq / Hkv > 16) return VMC_EINVAL;
     if (max_blocks <= 0) return VMC_EINVAL;
     if (B > 0 && (!out || !query || !bt || !seq_lens || !ws)) return VMC_EINVAL;
-    if (ws_bytes < workspace_bytes_for(B, Hq)) return VMC_ENOMEM;
+    if (ws_bytes < workspace_bytes_for(B, Hq, max_blocks)) return VMC_ENOMEM;
     prm.out = out;
     prm.q = reinterpret_cast<const uint16_t*>(query);
     prm.bt = bt;
@@ -684,11 +754,10 @@ extern "C" size_t vmc_paged_decode_workspace_size(int batch_size, int num_heads,
                                                   int max_num_blocks_per_req, int block_size,
                                                   int max_num_kv_splits) {
     (void)head_dim;
-    (void)max_num_blocks_per_req;
     (void)block_size;
     (void)max_num_kv_splits;
     if (batch_size < 0 || num_heads <= 0) return 0;
-    return workspace_bytes_for(batch_size, num_heads);
+    return workspace_bytes_for(batch_size, num_heads, max_num_blocks_per_req);
 }
 
 extern "C" size_t vmc_turboquant_decode_workspace_size(int batch_size, int num_heads, int head_dim,
@@ -727,9 +796,10 @@ extern "C" int vmc_paged_attention_decode(void* out, const void* query, const vo
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (kv_format == VMC_KV_Q8_0 || kv_format == VMC_KV_Q4_0) {
         const int n16 = (int)(2 * prm.page_bytes / 16);
-        if ((prm.page_bytes % 16) != 0 || n16 > kMaxStage * 64 * num_kv_heads) return VMC_EINVAL;
+        (void)n16;
+        if ((prm.page_bytes % 16) != 0) return VMC_EINVAL;
     }
-    const size_t lds_q = (size_t)2 * prm.page_bytes;
+    const size_t lds_q = (size_t)4 * prm.page_bytes;  // K+V, double buffered
     switch (kv_format) {
         case VMC_KV_F16: return launch_decode<FMT_F16, 0, 0, false>(prm, 0, s);
         case VMC_KV_BF16: return launch_decode<FMT_BF16, 0, 0, true>(prm, 0, s);
@@ -769,9 +839,9 @@ extern "C" int vmc_turboquant_decode_attention(void* output, const void* query, 
     prm.key_packed = cfg->key_packed_size;
     prm.val_data = cfg->val_data_bytes;
     prm.tab = tq_tables(head_dim, cfg->key_quant_bits);
-    if ((prm.page_bytes % 16) != 0 || prm.page_bytes / 16 > kMaxStage * 64 * num_kv_heads)
+    if ((prm.page_bytes % 16) != 0)
         return VMC_EINVAL;
-    const size_t lds = 1024 + (size_t)prm.page_bytes;
+    const size_t lds = 1024 + (size_t)2 * prm.page_bytes;  // LUT + double-buffered page
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int kb = cfg->key_quant_bits, vb = cfg->value_quant_bits;
     if (kb == 4 && vb == 4) return launch_decode<FMT_TQ, 4, 4, false>(prm, lds, s);

@@ -1,0 +1,115 @@
+// selftest.hip -- device check of the lane-level assumptions the kernels rely
+// on: cross-row reductions, the wave-private LDS gather, and the operand /
+// result layouts of the MFMA shapes used (16x16x32 f16/bf16, 16x16x16 f16,
+// 32x32x16 f16/bf16).  One wave, fixed small integer inputs (exact in every
+// format), every lane compares its own results with the expected values.
+#include "vmc_common.hpp"
+
+namespace vmc {
+namespace {
+
+enum {
+    kSumGroups = 1, kMaxGroups = 2, kGather = 4, kMfma16x32 = 8, kMfma16x16 = 16,
+    kMfma32x16 = 32, kMfma16x32bf = 64, kMfma32x16bf = 128
+};
+
+// A[i][k] = (i + 2k) % 5 - 2, B[k][j] = (3k + j) % 7 - 3 (all exact)
+__device__ __forceinline__ float Aval(int i, int k) { return (float)((i + 2 * k) % 5 - 2); }
+__device__ __forceinline__ float Bval(int k, int j) { return (float)((3 * k + j) % 7 - 3); }
+
+__global__ void __launch_bounds__(64) selftest_kernel(int* fail) {
+    __shared__ __attribute__((aligned(16))) float sc[16];
+    const int l = threadIdx.x, r16 = l & 15, grp = l >> 4;
+    int bad = 0;
+    // cross-row reductions
+    {
+        const float s = sum_over_groups((float)l);
+        if (s != (float)(4 * r16 + 96)) bad |= kSumGroups;
+        const float m = max_over_groups((float)l);
+        if (m != (float)(48 + r16)) bad |= kMaxGroups;
+        const f32x4 g = gather4_from_row0((float)(100 + l), sc, r16, grp);
+        for (int i = 0; i < 4; ++i)
+            if (g[i] != (float)(100 + 4 * grp + i)) bad |= kGather;
+    }
+    // 16x16x32 f16: A lane (row l%16, k = 8*(l/16) + e), D rows 4*(l/16)+i, col l%16
+    {
+        f16x8 a, b;
+        bf16x8 ab, bb;
+        for (int e = 0; e < 8; ++e) {
+            const int k = 8 * grp + e;
+            a[e] = (_Float16)Aval(r16, k);
+            b[e] = (_Float16)Bval(k, r16);
+            ab[e] = (__bf16)Aval(r16, k);
+            bb[e] = (__bf16)Bval(k, r16);
+        }
+        const f32x4 d = mfma16x16x32(a, b, f32x4{0.f, 0.f, 0.f, 0.f});
+        const f32x4 db = mfma16x16x32(ab, bb, f32x4{0.f, 0.f, 0.f, 0.f});
+        for (int i = 0; i < 4; ++i) {
+            float ref = 0.0f;
+            for (int k = 0; k < 32; ++k) ref += Aval(4 * grp + i, k) * Bval(k, r16);
+            if (d[i] != ref) bad |= kMfma16x32;
+            if (db[i] != ref) bad |= kMfma16x32bf;
+        }
+    }
+    // 16x16x16 f16: k = 4*(l/16) + e
+    {
+        f16x4 a, b;
+        for (int e = 0; e < 4; ++e) {
+            const int k = 4 * grp + e;
+            a[e] = (_Float16)Aval(r16, k);
+            b[e] = (_Float16)Bval(k, r16);
+        }
+        const f32x4 d = mfma16x16x16(a, b, f32x4{0.f, 0.f, 0.f, 0.f});
+        for (int i = 0; i < 4; ++i) {
+            float ref = 0.0f;
+            for (int k = 0; k < 16; ++k) ref += Aval(4 * grp + i, k) * Bval(k, r16);
+            if (d[i] != ref) bad |= kMfma16x16;
+        }
+    }
+    // 32x32x16: A lane (row l%32, k = 8*(l/32) + e), D col l%32, rows 8*(v/4) + 4*(l/32) + v%4
+    {
+        const int c32 = l & 31, h = l >> 5;
+        f16x8 a, b;
+        bf16x8 ab, bb;
+        for (int e = 0; e < 8; ++e) {
+            const int k = 8 * h + e;
+            a[e] = (_Float16)Aval(c32, k);
+            b[e] = (_Float16)Bval(k, c32);
+            ab[e] = (__bf16)Aval(c32, k);
+            bb[e] = (__bf16)Bval(k, c32);
+        }
+        f32x16 z;
+        for (int v = 0; v < 16; ++v) z[v] = 0.0f;
+        const f32x16 d = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, z, 0, 0, 0);
+        const f32x16 db = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ab, bb, z, 0, 0, 0);
+        for (int v = 0; v < 16; ++v) {
+            const int row = 8 * (v >> 2) + 4 * h + (v & 3);
+            float ref = 0.0f;
+            for (int k = 0; k < 16; ++k) ref += Aval(row, k) * Bval(k, c32);
+            if (d[v] != ref) bad |= kMfma32x16;
+            if (db[v] != ref) bad |= kMfma32x16bf;
+        }
+    }
+    atomicOr(fail, bad);
+}
+
+}  // namespace
+}  // namespace vmc
+
+// Returns 0 when every check passes, a bitmask of failed checks (> 0), or a
+// negative status on a HIP error.  Synchronous; allocates 4 bytes.
+extern "C" int vmc_selftest(void) {
+    int* d = nullptr;
+    if (hipMalloc(&d, sizeof(int)) != hipSuccess) return VMC_EIO;
+    int h = 0;
+    int rc = VMC_OK;
+    if (hipMemset(d, 0, sizeof(int)) != hipSuccess) rc = VMC_EIO;
+    if (rc == VMC_OK) {
+        hipLaunchKernelGGL(vmc::selftest_kernel, dim3(1), dim3(64), 0, 0, d);
+        if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess ||
+            hipMemcpy(&h, d, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
+            rc = VMC_EIO;
+    }
+    hipFree(d);
+    return rc == VMC_OK ? h : rc;
+}

@@ -63,16 +63,53 @@ __device__ __forceinline__ uint16_t f32_to_half(float f) {
 __device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, kWave); }
 __device__ __forceinline__ float shfl(float v, int src) { return __shfl(v, src, kWave); }
 
-// sum / max over the four 16-lane groups that share l % 16
+// sum / max over the four 16-lane rows that share l % 16, with the gfx950
+// row-swap instructions (no LDS traffic): v_permlane16_swap exchanges rows
+// 1 <-> 0 and 3 <-> 2 between its two operands, v_permlane32_swap the two
+// halves; combining both results of each swap reduces over the pair.
+// The second operand is a copy the compiler cannot see through: given two
+// provably equal operands it treats both results as equal and drops one.
+__device__ __forceinline__ void swap_pair16(uint32_t& a, uint32_t& b) {
+    asm volatile("" : "+v"(b));
+    auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+    a = r[0];
+    b = r[1];
+}
+__device__ __forceinline__ void swap_pair32(uint32_t& a, uint32_t& b) {
+    asm volatile("" : "+v"(b));
+    auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+    a = r[0];
+    b = r[1];
+}
 __device__ __forceinline__ float sum_over_groups(float v) {
-    v += shfl_xor(v, 16);
-    v += shfl_xor(v, 32);
-    return v;
+    uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+    swap_pair16(a, b);
+    v = __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+    a = __builtin_bit_cast(uint32_t, v);
+    b = a;
+    swap_pair32(a, b);
+    return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
 }
 __device__ __forceinline__ float max_over_groups(float v) {
-    v = fmaxf(v, shfl_xor(v, 16));
-    v = fmaxf(v, shfl_xor(v, 32));
-    return v;
+    uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+    swap_pair16(a, b);
+    v = fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+    a = __builtin_bit_cast(uint32_t, v);
+    b = a;
+    swap_pair32(a, b);
+    return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+
+// Wave-private LDS exchange: lanes of row 0 publish v[l % 16]; every lane
+// reads back the four values v[4*(l/16) .. +3] (one 16-byte LDS read).
+__device__ __forceinline__ f32x4 gather4_from_row0(float v, float* sc, int r16, int grp) {
+    if (grp == 0) sc[r16] = v;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const f32x4 r = *reinterpret_cast<const f32x4*>(sc + 4 * grp);
+    __builtin_amdgcn_wave_barrier();
+    return r;
 }
 
 // ---------------------------------------------------------------- MFMA
