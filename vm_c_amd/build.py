@@ -24,9 +24,12 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 # -ffp-contract=off: every fused multiply-add in the kernels is written out
 # (the quantizers are bit-exact against their references).  Packed fp32 ops
-# are disabled for the device code.
+# are disabled for the device code.  Unaligned-access mode is off so the
+# compiler never fuses naturally aligned narrow LDS reads into a wider,
+# misaligned one (the LDS serves those with long stalls).
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-ffp-contract=off",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+             "-Xclang", "-target-feature", "-Xclang", "-unaligned-access-mode",
              "-I", os.path.join(ROOT, "include"), "-I", CSRC]
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-ffp-contract=off", "-D__HIP_PLATFORM_AMD__",
              "-I", os.path.join(ROOT, "include"), "-I", os.path.join(HOST, "include"),

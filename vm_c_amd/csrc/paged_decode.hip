@@ -199,8 +199,9 @@ paged_decode_kernel(DecodeParams p) {
 
     if (wave == 0) compute_plan(p, item, &plan);
     constexpr bool kStaged = FMT >= FMT_Q8_0;
-    uint32_t* lut = reinterpret_cast<uint32_t*>(smem);
-    uint8_t* pagebuf = smem + (FMT == FMT_TQ ? 1024 : 0);
+    // static LDS: the LUT's address is a compile-time offset of each read
+    __shared__ uint32_t lut[FMT == FMT_TQ ? 256 : 1];
+    uint8_t* pagebuf = smem;
     if constexpr (FMT == FMT_TQ) build_pair_lut<KB>(lut, p.tab);
     __syncthreads();
     const int b = __builtin_amdgcn_readfirstlane(plan.b);
@@ -375,80 +376,87 @@ paged_decode_kernel(DecodeParams p) {
         float rowf = p.scale_log2;  // factor of S row r16 (token r16)
         // V operand pieces (tokens 4*grp + i, dims 8*r16 .. +7) as fp16/bf16 bits
         uint32_t vw[4][4];  // [token i][dword e] = dims (2e, 2e+1)
+        uint32_t bop[8][2];  // PV B operands: dim 8*r16 + c, tokens {0,1} / {2,3}
         float vsc[4] = {1.f, 1.f, 1.f, 1.f}, vzr[4] = {0.f, 0.f, 0.f, 0.f};
 
         if constexpr (kStaged) {
             // ---- K operand for token r16
             const uint8_t* ke = kpage + entry_off<FMT>(r16, g, Hkv, E, hnd);
             if constexpr (FMT == FMT_TQ) {
-                float csq = 0.0f;
+                // K: lane group grp owns dims 32*grp .. +31 of token r16; each
+                // code pair indexes the LUT of packed fp16 centroid pairs.
+                u32x4 aw[4];
                 if constexpr (KB == 4) {
-                    const uint8_t* cb = ke + 16 * grp;
+                    const uint8_t* cb = ke + 16 * grp;  // 16 bytes, 2-byte aligned
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        const uint32_t w0 = lds16(cb + 4 * j), w1 = lds16(cb + 4 * j + 2);
-                        const uint32_t by[4] = {w0 & 0xff, w0 >> 8, w1 & 0xff, w1 >> 8};
+                        const uint32_t w = lds16(cb + 4 * j) | (lds16(cb + 4 * j + 2) << 16);
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const uint32_t pr = lut[by[e]];
-                            a[j][2 * e] = __builtin_bit_cast(_Float16, (uint16_t)(pr & 0xffff));
-                            a[j][2 * e + 1] = __builtin_bit_cast(_Float16, (uint16_t)(pr >> 16));
-                        }
+                        for (int e = 0; e < 4; ++e) aw[j][e] = lut[(w >> (8 * e)) & 0xffu];
                     }
                 } else {
-                    const uint8_t* cb = ke + 12 * grp;
+                    const uint8_t* cb = ke + 12 * grp;  // 12 bytes = four 8-code groups
+                    uint32_t h[6];
 #pragma unroll
-                    for (int j = 0; j < 4; j += 2) {
-                        // 6 bytes = dims 32*grp + 8j .. +15 (two 8-code groups)
-                        const uint64_t w = (uint64_t)lds16(cb + 3 * j) | ((uint64_t)lds16(cb + 3 * j + 2) << 16) |
-                                           ((uint64_t)lds16(cb + 3 * j + 4) << 32);
+                    for (int q = 0; q < 6; ++q) h[q] = lds16(cb + 2 * q);
+                    const uint32_t g24[4] = {h[0] | ((h[1] & 0xffu) << 16), (h[1] >> 8) | (h[2] << 8),
+                                             h[3] | ((h[4] & 0xffu) << 16), (h[4] >> 8) | (h[5] << 8)};
 #pragma unroll
-                        for (int jj = 0; jj < 2; ++jj) {
-                            const uint32_t g24 = (uint32_t)(w >> (24 * jj)) & 0xffffffu;
+                    for (int j = 0; j < 4; ++j)
 #pragma unroll
-                            for (int e = 0; e < 4; ++e) {
-                                const uint32_t pr = lut[(g24 >> (6 * e)) & 63u];
-                                a[j + jj][2 * e] = __builtin_bit_cast(_Float16, (uint16_t)(pr & 0xffff));
-                                a[j + jj][2 * e + 1] = __builtin_bit_cast(_Float16, (uint16_t)(pr >> 16));
-                            }
-                        }
-                    }
+                        for (int e = 0; e < 4; ++e) aw[j][e] = lut[(g24[j] >> (6 * e)) & 63u];
                 }
+                // sum of squared centroids (one mixed-precision fma per value;
+                // v_dot2 with a squared operand gave wrong sums on this toolchain)
+                float csq = 0.0f;
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < 4; ++j) {
+                    a[j] = __builtin_bit_cast(AT, aw[j]);
 #pragma unroll
                     for (int e = 0; e < 8; ++e) csq = __builtin_fmaf((float)a[j][e], (float)a[j][e], csq);
+                }
                 csq = sum_over_groups(csq);
                 const float nrm = f16_bits_to_f32((uint16_t)lds16(ke + p.mse_bytes));
-                rowf = p.scale_log2 * nrm / sqrtf(csq + 1e-16f);
-                // V: tokens 4*grp + i, dims 8*r16 .. +7
+                rowf = p.scale_log2 * nrm * __builtin_amdgcn_rsqf(csq + 1e-16f);
+                // V: codes of tokens 4*grp + i, dims 8*r16 .. +7, scale and zero
+                uint32_t cw[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int tok = 4 * grp + i;
                     const uint8_t* ve = kpage + entry_off<FMT>(tok, g, Hkv, E, hnd) + p.key_packed;
-                    uint32_t codes;
                     if constexpr (VB == 4) {
-                        codes = lds16(ve + 4 * r16) | (lds16(ve + 4 * r16 + 2) << 16);
+                        cw[i] = lds16(ve + 4 * r16) | (lds16(ve + 4 * r16 + 2) << 16);
                     } else {
-                        const uint8_t* cp = ve + 3 * r16;
-                        codes = (uint32_t)cp[0] | ((uint32_t)cp[1] << 8) | ((uint32_t)cp[2] << 16);
-                    }
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        uint32_t c0, c1;
-                        if constexpr (VB == 4) {
-                            c0 = (codes >> (8 * e)) & 0xf;
-                            c1 = (codes >> (8 * e + 4)) & 0xf;
-                        } else {
-                            c0 = (codes >> (6 * e)) & 7;
-                            c1 = (codes >> (6 * e + 3)) & 7;
-                        }
-                        vw[i][e] = (uint32_t)__builtin_bit_cast(uint16_t, code_f16(c0)) |
-                                   ((uint32_t)__builtin_bit_cast(uint16_t, code_f16(c1)) << 16);
+                        // ve is even, so ve + 3*r16 is odd exactly when r16 is:
+                        // read the two aligned 16-bit words around it
+                        const uint8_t* al2 = ve + 3 * r16 - (r16 & 1);
+                        const uint32_t w = lds16(al2) | (lds16(al2 + 2) << 16);
+                        cw[i] = (w >> (8 * (r16 & 1))) & 0xffffffu;
                     }
                     const bool ok = tok < nv;
                     vsc[i] = ok ? f16_bits_to_f32((uint16_t)lds16(ve + p.val_data)) : 0.0f;
                     vzr[i] = ok ? f16_bits_to_f32((uint16_t)lds16(ve + p.val_data + 2)) : 0.0f;
+                }
+                // B operands {token a, token b} per dim, exact fp16 codes via 1024 + c
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        uint32_t x;
+                        if constexpr (VB == 4) {
+                            const uint32_t t = __builtin_amdgcn_perm(cw[2 * hh + 1], cw[2 * hh],
+                                                                     (uint32_t)(c >> 1) | 0x0c00u |
+                                                                         ((uint32_t)(4 + (c >> 1)) << 16) | 0x0c000000u);
+                            x = (c & 1) ? (t >> 4) : t;
+                            x = (x & 0x000f000fu) | 0x64006400u;
+                        } else {
+                            const uint32_t c0 = (cw[2 * hh] >> (3 * c)) & 7u;
+                            const uint32_t c1 = (cw[2 * hh + 1] >> (3 * c)) & 7u;
+                            x = (c0 | (c1 << 16)) | 0x64006400u;
+                        }
+                        const f16x2 v2 = __builtin_bit_cast(f16x2, x) - f16x2{(_Float16)1024.0f, (_Float16)1024.0f};
+                        bop[c][hh] = __builtin_bit_cast(uint32_t, v2);
+                    }
                 }
             } else {
                 // GGUF blocks: lane group grp owns block grp (dims 32*grp .. +31)
@@ -541,26 +549,32 @@ paged_decode_kernel(DecodeParams p) {
         }
         float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
         mx = max_over_groups(mx);
-        const float m_new = fmaxf(m_run, mx);
-        const float m_use = m_new == kNegInf ? 0.0f : m_new;
-        const float alpha = exp2f(m_run - m_use);
+        // Lazy reference max: m_run moves only when a head's max exceeds it by
+        // more than 8 (log2 units), so p <= 256 and most pages skip the O
+        // rescale.  Every term of l, z and O uses the same reference: exact.
+        const bool upd = mx > m_run + 8.0f;
+        if (__ballot(upd)) {  // wave-uniform
+            const float m_new = upd ? mx : m_run;
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 when m_run = -inf
+            l_part *= alpha;
+            if constexpr (FMT == FMT_TQ) z_part *= alpha;
+            const f32x4 al = gather4_from_row0(alpha, wscr + 16, r16, grp);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int c = 0; c < 8; ++c) oacc[c][i] *= al[i];
+            m_run = m_new;
+        }
+        const float m_use = m_run == kNegInf ? 0.0f : m_run;
         float pv[4], psum = 0.0f, zsum = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            pv[i] = exp2f(sv[i] - m_use);
+            pv[i] = __builtin_amdgcn_exp2f(sv[i] - m_use);
             psum += pv[i];
             if constexpr (FMT == FMT_TQ) zsum = __builtin_fmaf(pv[i], vzr[i], zsum);
         }
-        l_part = __builtin_fmaf(l_part, alpha, psum);
-        if constexpr (FMT == FMT_TQ) z_part = __builtin_fmaf(z_part, alpha, zsum);
-        m_run = m_new;
-
-        // rescale O rows (heads 4*grp + i) by their heads' alpha
-        const f32x4 al = gather4_from_row0(alpha, wscr + 16, r16, grp);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int c = 0; c < 8; ++c) oacc[c][i] *= al[i];
+        l_part += psum;
+        if constexpr (FMT == FMT_TQ) z_part += zsum;
 
         // ---- O += P . V
         PT pa;
@@ -570,15 +584,18 @@ paged_decode_kernel(DecodeParams p) {
             if constexpr (MBF16) pa[i] = (short)f32_to_bf16_bits(pw);
             else pa[i] = (_Float16)pw;
         }
+        if constexpr (FMT != FMT_TQ) {
+            // {token 0,1} and {token 2,3} halves of dims (2e, 2e+1)
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+                bop[c][0] = __builtin_amdgcn_perm(vw[1][c >> 1], vw[0][c >> 1], sel);
+                bop[c][1] = __builtin_amdgcn_perm(vw[3][c >> 1], vw[2][c >> 1], sel);
+            }
+        }
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
-            PT vb;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint16_t bits = (uint16_t)((vw[i][c >> 1] >> (16 * (c & 1))) & 0xffff);
-                if constexpr (MBF16) vb[i] = (short)bits;
-                else vb[i] = __builtin_bit_cast(_Float16, bits);
-            }
+            const PT vb = __builtin_bit_cast(PT, u32x2{bop[c][0], bop[c][1]});
             oacc[c] = mfma16x16x16(pa, vb, oacc[c]);
         }
     };
@@ -841,7 +858,7 @@ extern "C" int vmc_turboquant_decode_attention(void* output, const void* query, 
     prm.tab = tq_tables(head_dim, cfg->key_quant_bits);
     if ((prm.page_bytes % 16) != 0)
         return VMC_EINVAL;
-    const size_t lds = 1024 + (size_t)2 * prm.page_bytes;  // LUT + double-buffered page
+    const size_t lds = (size_t)2 * prm.page_bytes;  // double-buffered page
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int kb = cfg->key_quant_bits, vb = cfg->value_quant_bits;
     if (kb == 4 && vb == 4) return launch_decode<FMT_TQ, 4, 4, false>(prm, lds, s);
