@@ -420,9 +420,11 @@ void orc_tq_store(const uint16_t* key, const uint16_t* value, uint8_t* kv_cache,
                   int head_dim, int64_t block_size, const orc_tq_layout* L,
                   const float* midpoints, int bf16) {
     const int D = head_dim;
-    float kf[256], xh[256], y[256], vf[256];
-    int q[256];
+    /* tokens are independent (distinct slots): parallel over tokens */
+#pragma omp parallel for schedule(static)
     for (int t = 0; t < num_tokens; ++t) {
+        float kf[256], xh[256], y[256], vf[256];
+        int q[256];
         const int64_t slot = slot_mapping[t];
         if (slot < 0) continue; /* :266-267 */
         const int64_t blk = slot / block_size, off = slot % block_size;

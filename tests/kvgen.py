@@ -69,3 +69,44 @@ def close_report(got, ref, atol=2e-3, rtol=1e-2):
     err = np.abs(got - ref)
     ok = err <= atol + rtol * np.abs(ref)
     return bool(ok.all()), float(err.max()) if err.size else 0.0
+
+
+# ------------------------------------------------------------ named workloads
+# The decode / prefill shapes the benchmarks and golden fixtures are quoted on.
+
+def single_seq_fp16_workload():
+    """Batch 1, 32/8 heads, 2048-token context, fp16 KV, block table a seeded
+    permutation of 128 pages, seed 0."""
+    return make_workload([2048], Hq=32, Hkv=8, seed=0)
+
+
+def batched_q8_0_lens():
+    """16 context lengths uniform in [512, 4096], seed 1."""
+    return np.random.default_rng(1).integers(512, 4097, 16).astype(np.int32)
+
+
+def batched_q8_0_workload():
+    """Batch 16, 32/8 heads, lengths from batched_q8_0_lens(), seed 1."""
+    return make_workload(batched_q8_0_lens(), Hq=32, Hkv=8, seed=1)
+
+
+def prefill_inputs(seq_lens, Hq, Hkv, D=128, seed=0, bf16=True):
+    """Q [T][Hq][D], K/V [T][Hkv][D] as bf16 (or fp16) bits, N(0,1) from
+    `seed`; positions restart at 0 per sequence; cu_seqlens [B+1]."""
+    rng = np.random.default_rng(seed)
+    T = int(sum(seq_lens))
+    mk = lambda *s: rng.standard_normal(s).astype(np.float32)
+    q, k, v = mk(T, Hq, D), mk(T, Hkv, D), mk(T, Hkv, D)
+    if bf16:
+        qb, kb, vb = (f32_to_bf16_bits(x) for x in (q, k, v))
+    else:
+        qb, kb, vb = (x.astype(np.float16).view(np.uint16) for x in (q, k, v))
+    pos = np.concatenate([np.arange(n) for n in seq_lens]).astype(np.int32)
+    cu = np.concatenate([[0], np.cumsum(seq_lens)]).astype(np.int32)
+    return qb, kb, vb, pos, cu
+
+
+def crc(a):
+    """crc32 of an array's bytes (fixtures record it for their inputs)."""
+    import zlib
+    return zlib.crc32(np.ascontiguousarray(a).tobytes()) & 0xFFFFFFFF

@@ -1,11 +1,13 @@
 """Causal prefill parity on the GPU: HIP MFMA prefill vs exact fp64 causal
 attention (oracle), tolerance |got - ref| <= 2e-3 + 1e-2 |ref|; the fused
 quantize-on-append must write the same bytes as the standalone append."""
+import os
+
 import numpy as np
 import pytest
 
 import oracle_lib as O
-from kvgen import BS, close_report, f32_to_bf16_bits
+from kvgen import BS, close_report, crc, prefill_inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -13,17 +15,7 @@ ATOL, RTOL = 2e-3, 1e-2
 
 
 def _inputs(seq_lens, Hq, Hkv, D=128, seed=0, bf16=True):
-    rng = np.random.default_rng(seed)
-    T = int(sum(seq_lens))
-    mk = lambda *s: rng.standard_normal(s).astype(np.float32)
-    q, k, v = mk(T, Hq, D), mk(T, Hkv, D), mk(T, Hkv, D)
-    if bf16:
-        qb, kb, vb = (f32_to_bf16_bits(x) for x in (q, k, v))
-    else:
-        qb, kb, vb = (x.astype(np.float16).view(np.uint16) for x in (q, k, v))
-    pos = np.concatenate([np.arange(n) for n in seq_lens]).astype(np.int32)
-    cu = np.concatenate([[0], np.cumsum(seq_lens)]).astype(np.int32)
-    return qb, kb, vb, pos, cu
+    return prefill_inputs(seq_lens, Hq, Hkv, D=D, seed=seed, bf16=bf16)
 
 
 def _run(dev, qb, kb, vb, pos, Hkv, scale, bf16=True, append=None):
@@ -89,7 +81,8 @@ def test_prefill_fused_append_bitexact(dev, fmt):
 
 def test_prefill_config4_full_size(dev):
     """B=4, S=4096, Hq=32, Hkv=8, bf16, causal, fused q8_0 append (seed 3):
-    sampled rows vs exact fp64, every page byte vs the oracle's append."""
+    sampled rows vs the reference's output (golden fixture) and exact fp64,
+    every page byte vs the oracle's append."""
     seq_lens, Hq, Hkv = [4096] * 4, 32, 8
     qb, kb, vb, pos, cu = _inputs(seq_lens, Hq, Hkv, seed=3)
     T = qb.shape[0]
@@ -105,6 +98,11 @@ def test_prefill_config4_full_size(dev):
     ok, err = close_report(got[toks, heads], ex, ATOL, RTOL)
     assert ok, f"max err {err}"
     assert np.isfinite(got).all()
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                             "fa_prefill_bf16.npz"))
+    assert (crc(qb), crc(kb), crc(vb)) == (g["crc_q"], g["crc_k"], g["crc_v"])
+    ok, err = close_report(got[g["tokens"], g["heads"]], g["out"], ATOL, RTOL)
+    assert ok, f"vs reference rows: max err {err}"
     kr = np.zeros(nbytes, np.uint8)
     vr = np.zeros(nbytes, np.uint8)
     O.kv_append(kb, vb, slots, kr, vr, BS, O.KV_Q8_0, src_bf16=True)
