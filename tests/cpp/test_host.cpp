@@ -1,0 +1,324 @@
+// CPU tests of the vm_c host layer (no GPU calls): block manager behaviour,
+// layouts, metadata construction, token read/write offsets, swap paths and
+// the C++ error convention.  Built and run by tests/test_host_cpp.py.
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "vm_c/attention_backend.hpp"
+#include "vm_c/attention_metadata.hpp"
+#include "vm_c/kv_cache_manager.hpp"
+
+using namespace vm_c;
+
+static int g_fail = 0;
+#define CHECK(c)                                                            \
+    do {                                                                    \
+        if (!(c)) {                                                         \
+            std::printf("FAIL %s:%d: %s\n", __FILE__, __LINE__, #c);        \
+            ++g_fail;                                                       \
+        }                                                                   \
+    } while (0)
+
+// host memory standing in for device memory
+class HostMemory : public KVMemory {
+public:
+    void* alloc_device(size_t n) override { return std::calloc(n, 1); }
+    void free_device(void* p) override { std::free(p); }
+    void* alloc_host(size_t n) override { return std::calloc(n, 1); }
+    void free_host(void* p) override { std::free(p); }
+    void copy(void* d, const void* s, size_t n) override { std::memcpy(d, s, n); }
+    void copy_async(void* d, const void* s, size_t n, hipStream_t) override { std::memcpy(d, s, n); }
+};
+
+static std::shared_ptr<KVMemory> hostmem() { return std::make_shared<HostMemory>(); }
+
+static CacheConfig cache_cfg(const std::string& dtype = "bf16", const std::string& method = "",
+                             const std::string& layout = "nhd", bool prefix = true) {
+    CacheConfig c;
+    c.block_size = 16;
+    c.kv_cache_dtype = dtype;
+    c.kv_cache_quant_method = method;
+    c.kv_cache_layout = layout;
+    c.enable_prefix_caching = prefix;
+    return c;
+}
+
+static std::vector<int64_t> ids_of(const std::vector<KVCacheSlot>& s) {
+    std::vector<int64_t> r;
+    for (auto& x : s) r.push_back(x.block_id);
+    return r;
+}
+
+static void test_free_queue() {
+    std::vector<KVCacheBlock> blocks(6);
+    for (int i = 0; i < 6; ++i) blocks[i].block_id = i;
+    FreeKVCacheBlockQueue q(blocks);
+    CHECK(q.num_free_blocks() == 6);
+    CHECK(q.popleft()->block_id == 0);
+    auto two = q.popleft_n(2);
+    CHECK(two.size() == 2 && two[0]->block_id == 1 && two[1]->block_id == 2);
+    CHECK(q.popleft_n(4).empty());  // all or nothing
+    CHECK(q.num_free_blocks() == 3);
+    q.remove(&blocks[4]);
+    CHECK((q.ids() == std::vector<int64_t>{3, 5}));
+    q.append(&blocks[0]);
+    q.append_n({&blocks[2], &blocks[1]});
+    CHECK((q.ids() == std::vector<int64_t>{3, 5, 0, 2, 1}));
+    q.remove(&blocks[4]);  // not queued: no effect
+    CHECK(q.num_free_blocks() == 5);
+}
+
+static void test_allocation_order() {
+    KVCacheManager m(cache_cfg(), ModelConfig{}, 2, 8, 128, 0, false, hostmem());
+    m.allocate_gpu_blocks_for_group(0, 10);
+    CHECK(m.num_gpu_blocks() == 10);
+    CHECK(m.num_free_gpu_blocks() == 9);  // block 0 is the null block
+    CHECK(m.gpu_blocks()[0].is_null && m.gpu_blocks()[0].ref_cnt == 1);
+    CHECK((ids_of(m.allocate_slots("a", 33)) == std::vector<int64_t>{1, 2, 3}));
+    CHECK((ids_of(m.allocate_slots("b", 16)) == std::vector<int64_t>{4}));
+    CHECK(m.allocate_slots("c", 16 * 6).empty());  // needs 6, 5 free
+    CHECK(m.num_free_gpu_blocks() == 5);
+    CHECK((ids_of(m.allocate_slots("a", 49)) == std::vector<int64_t>{1, 2, 3, 5}));  // grows
+    m.free_slots("a");
+    CHECK((m.free_block_ids() == std::vector<int64_t>{6, 7, 8, 9, 5, 3, 2, 1}));  // reversed
+    CHECK(m.request_slots().count("a") == 0);
+    m.trim_request_to_tokens("b", 0);
+    CHECK(m.request_slots().at("b").empty());
+    CHECK(m.free_block_ids().back() == 4);
+    CHECK(m.usage() == 0.0f);
+    m.allocate_slots("d", 16 * 9);
+    CHECK(m.usage() == 1.0f);
+    bool threw = false;
+    try {
+        m.trim_request_to_tokens("d", -1);
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    CHECK(threw);
+}
+
+static void test_prefix_cache() {
+    KVCacheManager m(cache_cfg(), ModelConfig{}, 1, 8, 128, 0, false, hostmem());
+    m.allocate_gpu_blocks_for_group(0, 8);
+    auto s = ids_of(m.allocate_slots("a", 48));
+    CHECK((s == std::vector<int64_t>{1, 2, 3}));
+    m.cache_full_blocks("a", {111, 222, 333}, 0, 2);  // blocks 1, 2 full
+    std::vector<int64_t> hit;
+    CHECK(m.find_longest_prefix_hit({111, 222, 333}, 3, hit) == 2);
+    CHECK((hit == std::vector<int64_t>{1, 2}));
+    CHECK(m.find_longest_prefix_hit({999, 222}, 2, hit) == 0);
+    m.free_slots("a");
+    // freed blocks keep their hash and can be reused by a new request
+    CHECK(m.find_longest_prefix_hit({111, 222}, 2, hit) == 2);
+    auto r = ids_of(m.allocate_slots("b", 40, {111, 222}, 32, {1, 2}));
+    CHECK(r.size() == 3 && r[0] == 1 && r[1] == 2);
+    CHECK(m.gpu_blocks()[1].ref_cnt == 1 && m.gpu_blocks()[2].ref_cnt == 1);
+    auto fr = m.free_block_ids();
+    CHECK(std::find(fr.begin(), fr.end(), 1) == fr.end());
+    // sharing: a second request on the same prefix raises the count
+    m.allocate_slots("c", 32, {111, 222}, 32, {1, 2});
+    CHECK(m.gpu_blocks()[1].ref_cnt == 2);
+    m.free_slots("c");
+    CHECK(m.gpu_blocks()[1].ref_cnt == 1);
+    CHECK(!m.reset_prefix_cache());  // blocks in use
+    m.free_slots("b");
+    // a hashed block taken for new content loses its hash
+    m.allocate_slots("e", 16 * 7);
+    CHECK(m.find_longest_prefix_hit({111}, 1, hit) == 0);
+    m.free_slots("e");
+    CHECK(m.reset_prefix_cache());
+}
+
+static void test_layouts() {
+    auto l4 = TurboQuantLayout::create(128, "turboquant_4bit_nc");
+    auto l3 = TurboQuantLayout::create(128, "turboquant_3bit_nc");
+    auto lk = TurboQuantLayout::create(128, "turboquant_k3v4_nc");
+    auto l8 = TurboQuantLayout::create(128, "turboquant_k8v4");
+    CHECK(l4.slot_size_aligned == 134 && l3.slot_size_aligned == 102);
+    CHECK(lk.slot_size_aligned == 118 && l8.slot_size_aligned == 196);
+    for (const char* meth : {"turboquant_4bit_nc", "turboquant_3bit_nc", "turboquant_k3v4_nc"}) {
+        TQConfig a = TQConfig::from_method(128, meth);
+        vmc_tq_config b;
+        CHECK(vmc_tq_config_from_method(128, meth, &b) == VMC_OK);
+        vmc_tq_config c = a.to_c();
+        c.max_num_kv_splits = b.max_num_kv_splits;
+        CHECK(std::memcmp(&b, &c, sizeof(b)) == 0);
+    }
+    CHECK((TurboQuantLayout::get_boundary_skip_layers(10, 2) == std::vector<int>{0, 1, 8, 9}));
+    CHECK(TurboQuantLayout::get_boundary_skip_layers(10, 2, {"attention", "linear_attention"}).empty());
+    CHECK((TurboQuantLayout::get_boundary_skip_layers(3, 2) == std::vector<int>{0, 2}));
+
+    KVCacheManager tq(cache_cfg("auto", "turboquant_3bit_nc"), ModelConfig{}, 6, 8, 128, 0, false, hostmem());
+    CHECK(tq.is_turboquant() && tq.num_kv_cache_groups() == 1);
+    CHECK(tq.group(0).bytes_per_block == (size_t)16 * 8 * 102);
+    CHECK(tq.kv_bytes_per_token(3) == (size_t)8 * 102);
+    tq.set_tq_boundary_layers(TurboQuantLayout::get_boundary_skip_layers(6, 1));
+    CHECK(tq.num_kv_cache_groups() == 2);
+    CHECK(tq.group_id_for_layer(0) == 1 && tq.group_id_for_layer(2) == 0);
+    CHECK(tq.group(1).bytes_per_block == (size_t)16 * 8 * 128 * 2);  // bf16 standard pages
+    CHECK(!tq.is_layer_turboquant(5) && tq.is_layer_turboquant(4));
+    tq.allocate_gpu_blocks_for_group(0, 5);
+    tq.allocate_gpu_blocks_for_group(1, 5);
+    CHECK(tq.key_cache_ptr(2) && !tq.value_cache_ptr(2));  // packed TQ pool
+    CHECK(tq.key_cache_ptr(0) && tq.value_cache_ptr(0));
+    CHECK(tq.gpu_kv_cache_bytes() == (size_t)5 * 16 * 8 * 102 * 4 + (size_t)5 * 32768 * 2 * 2);
+    // the second group's blocks extend the same id space; the queue survived the move
+    CHECK(tq.num_free_gpu_blocks() == 9);
+    auto s = ids_of(tq.allocate_slots("x", 16 * 9));
+    CHECK(s.size() == 9 && s.front() == 1 && s.back() == 9);
+
+    KVCacheManager q8(cache_cfg("q8_0"), ModelConfig{}, 1, 8, 128, 0, false, hostmem());
+    CHECK(q8.group(0).bytes_per_block == (size_t)16 * 8 * 136);
+    CHECK(q8.kv_bytes_per_token(0) == (size_t)8 * 136 * 2);
+    ModelConfig skip;
+    skip.kv_cache_layers = {true, false, true};
+    KVCacheManager sk(cache_cfg("fp16"), skip, 3, 8, 128, 0, false, hostmem());
+    CHECK((sk.group(0).layer_indices == std::vector<int>{0, 2}));
+    CHECK(sk.group(0).bytes_per_block == (size_t)16 * 8 * 128 * 2);
+}
+
+static void test_token_io(const std::string& layout) {
+    const int H = 4, D = 64;
+    KVCacheManager m(cache_cfg("fp16", "", layout), ModelConfig{}, 1, H, D, 0, false, hostmem());
+    m.allocate_gpu_blocks_for_group(0, 4);
+    const size_t E = D * 2, T = H * E, page = 16 * T;
+    std::vector<uint8_t> tok(2 * T);
+    for (size_t i = 0; i < tok.size(); ++i) tok[i] = (uint8_t)(i * 7 + 1);
+    const int64_t slot = 2 * 16 + 5;
+    m.write_kv_token(0, slot, tok.data(), nullptr);
+    auto* K = static_cast<uint8_t*>(m.key_cache_ptr(0));
+    auto* V = static_cast<uint8_t*>(m.value_cache_ptr(0));
+    for (int h = 0; h < H; ++h) {
+        const size_t off = layout == "hnd" ? 2 * page + ((size_t)h * 16 + 5) * E : 2 * page + 5 * T + h * E;
+        CHECK(std::memcmp(K + off, tok.data() + h * E, E) == 0);
+        CHECK(std::memcmp(V + off, tok.data() + T + h * E, E) == 0);
+    }
+    std::vector<uint8_t> back(2 * T, 0);
+    m.read_kv_token(0, slot, back.data(), nullptr);
+    CHECK(back == tok);
+
+    KVCacheManager tq(cache_cfg("auto", "turboquant_4bit_nc"), ModelConfig{}, 1, H, 128, 0, false, hostmem());
+    tq.allocate_gpu_blocks_for_group(0, 3);
+    std::vector<uint8_t> t2(H * 134);
+    for (size_t i = 0; i < t2.size(); ++i) t2[i] = (uint8_t)(i ^ 0x5a);
+    tq.write_kv_token(0, 16 + 3, t2.data(), nullptr);
+    auto* P = static_cast<uint8_t*>(tq.key_cache_ptr(0));
+    CHECK(std::memcmp(P + (size_t)16 * H * 134 + 3 * H * 134, t2.data(), t2.size()) == 0);
+}
+
+static void test_swap() {
+    KVCacheManager m(cache_cfg("fp16"), ModelConfig{}, 2, 2, 64, 0, false, hostmem());
+    m.allocate_gpu_blocks_for_group(0, 6);
+    m.allocate_cpu_blocks_for_group(0, 4);
+    auto s = ids_of(m.allocate_slots("r", 32));  // blocks 1, 2
+    const size_t bb = m.group(0).bytes_per_block;
+    for (int l = 0; l < 2; ++l)
+        for (int64_t b : s) {
+            std::memset(static_cast<uint8_t*>(m.key_cache_ptr(l)) + b * bb, (int)(10 * l + b), bb);
+            std::memset(static_cast<uint8_t*>(m.value_cache_ptr(l)) + b * bb, (int)(50 + 10 * l + b), bb);
+        }
+    m.swap_request_slots("r");
+    CHECK(m.num_free_cpu_blocks() == 2);
+    CHECK(m.num_free_gpu_blocks() == 5);
+    for (int l = 0; l < 2; ++l)
+        for (int64_t b : s) std::memset(static_cast<uint8_t*>(m.key_cache_ptr(l)) + b * bb, 0xEE, bb);
+    // other requests take the device blocks meanwhile
+    m.allocate_slots("other", 32);
+    m.swap_back_request_slots("r");
+    auto now = ids_of(m.request_slots().at("r"));
+    CHECK(now.size() == 2);
+    CHECK(m.num_free_cpu_blocks() == 4);
+    for (int l = 0; l < 2; ++l)
+        for (size_t i = 0; i < now.size(); ++i) {
+            auto* k = static_cast<uint8_t*>(m.key_cache_ptr(l)) + now[i] * bb;
+            auto* v = static_cast<uint8_t*>(m.value_cache_ptr(l)) + now[i] * bb;
+            CHECK(k[0] == (uint8_t)(10 * l + s[i]) && k[bb - 1] == (uint8_t)(10 * l + s[i]));
+            CHECK(v[0] == (uint8_t)(50 + 10 * l + s[i]));
+        }
+}
+
+static void test_metadata() {
+    KVCacheManager m(cache_cfg(), ModelConfig{}, 1, 8, 128, 0, false, hostmem());
+    m.allocate_gpu_blocks_for_group(0, 32);
+    // a request with 20 cached tokens decoding one more, and a fresh prefill of 18
+    m.allocate_slots("dec", 20);  // blocks 1, 2
+    std::vector<ScheduledRequest> reqs(2);
+    reqs[0].request_id = "dec";
+    reqs[0].num_computed_tokens = 20;
+    reqs[0].is_prefill = false;
+    reqs[1].request_id = "pre";
+    reqs[1].num_scheduled_tokens = 18;
+    reqs[1].is_prefill = true;
+    auto h = build_batch_metadata(m, reqs);
+    CHECK(h.ok && h.num_reqs == 2 && h.num_tokens == 19);
+    CHECK(h.max_num_blocks_per_req == 2);
+    CHECK((h.seq_lens == std::vector<int32_t>{21, 18}));
+    CHECK((h.block_tables == std::vector<int32_t>{1, 2, 3, 4}));
+    CHECK(h.slot_mapping[0] == 2 * 16 + 4);  // position 20 -> block 2, offset 4
+    for (int i = 0; i < 18; ++i) {
+        const int64_t blk = i < 16 ? 3 : 4;
+        CHECK(h.slot_mapping[1 + i] == blk * 16 + i % 16);
+        CHECK(h.token_positions[1 + i] == i && h.token_to_seq[1 + i] == 1);
+    }
+    CHECK((h.cu_seqlens == std::vector<int32_t>{0, 1, 19}));
+    CHECK(h.num_prefills == 1 && h.num_decodes == 1 && h.num_prefill_tokens == 18);
+    // a request that cannot get blocks marks the batch
+    std::vector<ScheduledRequest> big(1);
+    big[0].request_id = "huge";
+    big[0].num_scheduled_tokens = 16 * 40;
+    big[0].is_prefill = true;
+    CHECK(!build_batch_metadata(m, big).ok);
+}
+
+static void test_errors() {
+    bool threw = false;
+    try {
+        reshape_and_cache(nullptr, nullptr, nullptr, nullptr, nullptr, 0, 8, 128, 16, 0, "fp8_e4m3",
+                          nullptr, nullptr, ScalarType::FLOAT16);
+    } catch (const std::runtime_error& e) {
+        threw = std::string(e.what()).find("kv_cache_dtype") != std::string::npos;
+    }
+    CHECK(threw);
+    threw = false;
+    try {
+        VMC_CALL(vmc_tq_config_from_method(128, "turboquant_k8v4", nullptr));
+    } catch (const std::runtime_error& e) {
+        threw = std::string(e.what()).find("invalid argument") != std::string::npos;
+    }
+    CHECK(threw);
+    threw = false;
+    try {
+        PagedAttentionBackend b("xyz");
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    CHECK(threw);
+    CHECK(vmc_layout_of("hnd") == VMC_LAYOUT_HND);
+    CHECK(vmc_kv_format_of("auto", ScalarType::BFLOAT16) == VMC_KV_BF16);
+    CHECK(vmc_kv_format_of("q4_0", ScalarType::FLOAT16) == VMC_KV_Q4_0);
+}
+
+int main() {
+    const std::vector<std::pair<const char*, std::function<void()>>> tests = {
+        {"free_queue", test_free_queue},
+        {"allocation_order", test_allocation_order},
+        {"prefix_cache", test_prefix_cache},
+        {"layouts", test_layouts},
+        {"token_io_nhd", [] { test_token_io("nhd"); }},
+        {"token_io_hnd", [] { test_token_io("hnd"); }},
+        {"swap", test_swap},
+        {"metadata", test_metadata},
+        {"errors", test_errors},
+    };
+    for (auto& t : tests) {
+        const int before = g_fail;
+        t.second();
+        std::printf("%s %s\n", g_fail == before ? "ok  " : "FAIL", t.first);
+    }
+    return g_fail == 0 ? 0 : 1;
+}

@@ -1,0 +1,228 @@
+// GPU test of the vm_c host layer end to end: KVCacheManager pools (HIP),
+// the Engine-style metadata builder, and the PagedAttentionBackend /
+// TurboQuantBackend operators, checked against the oracle (oracle/vmc_oracle.h):
+// appended bytes bit-exact, attention within |d| <= 2e-3 + 1e-2 |ref|.
+// Built by __graft_entry__.build(); run by tests/test_gpu_host_cpp.py.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "vm_c/attention_backend.hpp"
+#include "vm_c/attention_metadata.hpp"
+#include "vm_c/kv_cache_manager.hpp"
+#include "vmc_oracle.h"
+
+using namespace vm_c;
+
+static int g_fail = 0;
+#define CHECK(c)                                                                \
+    do {                                                                        \
+        if (!(c)) {                                                             \
+            std::printf("FAIL %s:%d: %s\n", __FILE__, __LINE__, #c);            \
+            std::fflush(stdout);                                                \
+            ++g_fail;                                                           \
+        }                                                                       \
+    } while (0)
+
+template <typename T>
+struct Dev {
+    T* p = nullptr;
+    size_t n = 0;
+    explicit Dev(size_t count) : n(count) { HIP_CHECK(hipMalloc(&p, sizeof(T) * (count ? count : 1))); }
+    Dev(const std::vector<T>& h) : Dev(h.size()) { put(h); }
+    ~Dev() { (void)hipFree(p); }
+    void put(const std::vector<T>& h) { HIP_CHECK(hipMemcpy(p, h.data(), sizeof(T) * h.size(), hipMemcpyHostToDevice)); }
+    std::vector<T> get() const {
+        std::vector<T> h(n);
+        HIP_CHECK(hipMemcpy(h.data(), p, sizeof(T) * n, hipMemcpyDeviceToHost));
+        return h;
+    }
+};
+
+static std::vector<uint8_t> pool_bytes(const void* p, size_t n) {
+    std::vector<uint8_t> h(n);
+    HIP_CHECK(hipMemcpy(h.data(), p, n, hipMemcpyDeviceToHost));
+    return h;
+}
+
+static bool close(const std::vector<uint16_t>& got_f16, const std::vector<double>& ref, double* maxerr) {
+    bool ok = true;
+    *maxerr = 0;
+    for (size_t i = 0; i < ref.size(); ++i) {
+        const double g = orc_f16_to_f32(got_f16[i]);
+        const double e = std::fabs(g - ref[i]);
+        *maxerr = std::max(*maxerr, e);
+        if (!(e <= 2e-3 + 1e-2 * std::fabs(ref[i]))) ok = false;
+    }
+    return ok;
+}
+
+static const int Hq = 16, Hkv = 4, D = 128, BS = 16;
+
+// prefill of three requests, then one decode step, through TurboQuantBackend
+static void test_turboquant_backend(const char* method) {
+    std::printf("case: TurboQuantBackend %s\n", method);
+    std::fflush(stdout);
+    CacheConfig cc;
+    cc.kv_cache_quant_method = method;
+    KVCacheManager mgr(cc, ModelConfig{}, 1, Hkv, D);
+    mgr.allocate_gpu_blocks_for_group(0, 64);
+    TurboQuantBackend be(D, method, Hq, Hkv, 0);
+    be.ensure_workspace(512, 8, Hq, Hkv, D, 0);
+    const std::vector<int> lens = {40, 17, 300};
+    std::vector<ScheduledRequest> pre(lens.size());
+    for (size_t i = 0; i < lens.size(); ++i) {
+        pre[i].request_id = "r" + std::to_string(i);
+        pre[i].num_scheduled_tokens = lens[i];
+        pre[i].is_prefill = true;
+    }
+    HostBatchMetadata hp = build_batch_metadata(mgr, pre);
+    CHECK(hp.ok);
+    const int T = hp.num_tokens;
+    std::vector<uint16_t> K((size_t)T * Hkv * D), V(K.size()), Q((size_t)T * Hq * D);
+    orc_randn_f16(K.data(), (int64_t)K.size(), 7, 1);
+    orc_randn_f16(V.data(), (int64_t)V.size(), 7, 2);
+    orc_randn_f16(Q.data(), (int64_t)Q.size(), 7, 3);
+    Dev<uint16_t> dK(K), dV(V), dQ(Q), dO(Q.size());
+    DeviceBatchMetadata dm(8, 512, 64);
+    AttentionMetadata mp = dm.upload(hp, BS, nullptr);
+    void* pool = mgr.key_cache_ptr(0);
+    const size_t pool_n = (size_t)64 * mgr.group(0).bytes_per_block;
+    HIP_CHECK(hipMemset(pool, 0, pool_n));
+    be.store_kv(dK.p, dV.p, pool, nullptr, mp.slot_mapping, T, Hkv, D, BS, 0, nullptr);
+    const float scale = 1.0f / std::sqrt((float)D);
+    be.forward_prefill(dO.p, dQ.p, dK.p, dV.p, pool, nullptr, mp, Hq, Hkv, D, scale, BS,
+                       ScalarType::FLOAT16, nullptr);
+    HIP_CHECK(hipDeviceSynchronize());
+
+    orc_tq_layout L;
+    CHECK(orc_tq_layout_from_method(D, method, &L) == 0);
+    std::vector<float> C(L.n_centroids), M(L.n_centroids - 1);
+    orc_tq_lloyd_max(C.data(), D, L.key_quant_bits);
+    orc_tq_midpoints(C.data(), L.n_centroids, M.data());
+    std::vector<uint8_t> ref(pool_n, 0);
+    orc_tq_store(K.data(), V.data(), ref.data(), hp.slot_mapping.data(), T, Hkv, D, BS, &L, M.data(), 0);
+    CHECK(pool_bytes(pool, pool_n) == ref);
+
+    // prefill rows vs exact causal attention
+    std::vector<int64_t> toks;
+    std::vector<int32_t> heads;
+    for (int t = 0; t < T; ++t)
+        for (int h = 0; h < Hq; ++h) {
+            toks.push_back(t);
+            heads.push_back(h);
+        }
+    std::vector<double> ex(toks.size() * D);
+    orc_prefill_exact_rows(ex.data(), Q.data(), K.data(), V.data(), 0, hp.cu_seqlens.data(),
+                           (int)lens.size(), Hq, Hkv, D, scale, toks.data(), heads.data(),
+                           (int64_t)toks.size(), 0);
+    double err = 0;
+    CHECK(close(dO.get(), ex, &err));
+    std::printf("  prefill max err %.3g\n", err);
+
+    // one decode step: every request appends one token and attends its context
+    std::vector<ScheduledRequest> dec(lens.size());
+    for (size_t i = 0; i < lens.size(); ++i) {
+        dec[i].request_id = "r" + std::to_string(i);
+        dec[i].num_computed_tokens = lens[i];
+    }
+    HostBatchMetadata hd = build_batch_metadata(mgr, dec);
+    CHECK(hd.ok && hd.num_tokens == (int)lens.size());
+    std::vector<uint16_t> K1((size_t)hd.num_tokens * Hkv * D), V1(K1.size()), Q1((size_t)hd.num_reqs * Hq * D);
+    orc_randn_f16(K1.data(), (int64_t)K1.size(), 8, 1);
+    orc_randn_f16(V1.data(), (int64_t)V1.size(), 8, 2);
+    orc_randn_f16(Q1.data(), (int64_t)Q1.size(), 8, 3);
+    Dev<uint16_t> dK1(K1), dV1(V1), dQ1(Q1), dO1(Q1.size());
+    AttentionMetadata md = dm.upload(hd, BS, nullptr);
+    be.store_kv(dK1.p, dV1.p, pool, nullptr, md.slot_mapping, hd.num_tokens, Hkv, D, BS, 0, nullptr);
+    be.forward_decode(dO1.p, dQ1.p, pool, nullptr, md, Hq, Hkv, D, scale, BS, ScalarType::FLOAT16, nullptr);
+    HIP_CHECK(hipDeviceSynchronize());
+    std::vector<uint8_t> got = pool_bytes(pool, pool_n);
+    orc_tq_store(K1.data(), V1.data(), ref.data(), hd.slot_mapping.data(), hd.num_tokens, Hkv, D, BS, &L,
+                 M.data(), 0);
+    CHECK(got == ref);
+    std::vector<double> exd((size_t)hd.num_reqs * Hq * D);
+    orc_tq_decode_exact(exd.data(), Q1.data(), got.data(), hd.block_tables.data(), hd.seq_lens.data(),
+                        hd.num_reqs, Hq, Hkv, D, scale, BS, hd.max_num_blocks_per_req, &L, C.data(), 0, 0);
+    CHECK(close(dO1.get(), exd, &err));
+    std::printf("  decode max err %.3g\n", err);
+    for (size_t i = 0; i < lens.size(); ++i) mgr.free_slots("r" + std::to_string(i));
+    CHECK(mgr.num_free_gpu_blocks() == 63);
+}
+
+// append + decode of GGUF pages through PagedAttentionBackend
+static void test_paged_backend(const std::string& dtype, const std::string& layout) {
+    std::printf("case: PagedAttentionBackend %s %s\n", dtype.c_str(), layout.c_str());
+    std::fflush(stdout);
+    CacheConfig cc;
+    cc.kv_cache_dtype = dtype;
+    cc.kv_cache_layout = layout;
+    KVCacheManager mgr(cc, ModelConfig{}, 1, Hkv, D);
+    mgr.allocate_gpu_blocks_for_group(0, 96);
+    PagedAttentionBackend be(layout, dtype, ScalarType::FLOAT16);
+    be.ensure_workspace(1024, 8, Hq, Hkv, D, 0);
+    const std::vector<int> lens = {1, 700, 129};
+    std::vector<ScheduledRequest> pre(lens.size());
+    for (size_t i = 0; i < lens.size(); ++i) {
+        pre[i].request_id = "p" + std::to_string(i);
+        pre[i].num_scheduled_tokens = lens[i];
+        pre[i].is_prefill = true;
+    }
+    HostBatchMetadata hp = build_batch_metadata(mgr, pre);
+    const int T = hp.num_tokens;
+    std::vector<uint16_t> K((size_t)T * Hkv * D), V(K.size()), Q((size_t)lens.size() * Hq * D);
+    orc_randn_f16(K.data(), (int64_t)K.size(), 9, 1);
+    orc_randn_f16(V.data(), (int64_t)V.size(), 9, 2);
+    orc_randn_f16(Q.data(), (int64_t)Q.size(), 9, 3);
+    Dev<uint16_t> dK(K), dV(V), dQ(Q), dO(Q.size());
+    DeviceBatchMetadata dm(8, 1024, 96);
+    AttentionMetadata mp = dm.upload(hp, BS, nullptr);
+    const size_t pool_n = (size_t)96 * mgr.group(0).bytes_per_block;
+    HIP_CHECK(hipMemset(mgr.key_cache_ptr(0), 0, pool_n));
+    HIP_CHECK(hipMemset(mgr.value_cache_ptr(0), 0, pool_n));
+    be.store_kv(dK.p, dV.p, mgr.key_cache_ptr(0), mgr.value_cache_ptr(0), mp.slot_mapping, T, Hkv, D, BS, 0,
+                nullptr);
+    HIP_CHECK(hipDeviceSynchronize());
+    const int fmt = dtype == "q8_0" ? ORC_KV_Q8_0 : dtype == "q4_0" ? ORC_KV_Q4_0 : ORC_KV_F16;
+    std::vector<uint8_t> rk(pool_n, 0), rv(pool_n, 0);
+    orc_kv_append(K.data(), V.data(), 0, rk.data(), rv.data(), hp.slot_mapping.data(), T, Hkv, D, BS, fmt,
+                  layout == "hnd");
+    std::vector<uint8_t> gk = pool_bytes(mgr.key_cache_ptr(0), pool_n), gv = pool_bytes(mgr.value_cache_ptr(0), pool_n);
+    CHECK(gk == rk && gv == rv);
+    // decode over the appended context (seq_lens = prompt lengths)
+    AttentionMetadata md = mp;
+    md.num_reqs = hp.num_reqs;
+    be.forward_decode(dO.p, dQ.p, mgr.key_cache_ptr(0), mgr.value_cache_ptr(0), md, Hq, Hkv, D,
+                      1.0f / std::sqrt((float)D), BS, ScalarType::FLOAT16, nullptr);
+    HIP_CHECK(hipDeviceSynchronize());
+    std::vector<float> qf(Q.size());
+    orc_f16_to_f32_n(Q.data(), qf.data(), (int64_t)Q.size());
+    std::vector<double> ex(Q.size());
+    orc_paged_decode_exact(ex.data(), qf.data(), gk.data(), gv.data(), fmt, layout == "hnd",
+                           hp.block_tables.data(), hp.seq_lens.data(), hp.num_reqs, Hq, Hkv, D,
+                           1.0 / std::sqrt((double)D), BS, hp.max_num_blocks_per_req, 0);
+    double err = 0;
+    CHECK(close(dO.get(), ex, &err));
+    std::printf("  decode max err %.3g\n", err);
+}
+
+int main() {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n < 1) {
+        std::printf("FAIL no GPU\n");
+        return 2;
+    }
+    try {
+        for (const char* m : {"turboquant_3bit_nc", "turboquant_4bit_nc"}) test_turboquant_backend(m);
+        test_paged_backend("q8_0", "nhd");
+        test_paged_backend("q4_0", "hnd");
+        test_paged_backend("fp16", "hnd");
+    } catch (const std::exception& e) {
+        std::printf("FAIL exception: %s\n", e.what());
+        return 1;
+    }
+    std::printf(g_fail ? "FAIL\n" : "ok\n");
+    return g_fail ? 1 : 0;
+}

@@ -31,7 +31,7 @@ HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-ffp-contr
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-Xclang", "-target-feature", "-Xclang", "-unaligned-access-mode",
              "-I", os.path.join(ROOT, "include"), "-I", CSRC]
-CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-ffp-contract=off", "-D__HIP_PLATFORM_AMD__",
+CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-ffp-contract=off", "-D__HIP_PLATFORM_AMD__",
              "-I", os.path.join(ROOT, "include"), "-I", os.path.join(HOST, "include"),
              "-I", "/opt/rocm/include"]
 
