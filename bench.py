@@ -101,7 +101,7 @@ def bench_decode(args, torch, capi, dev):
     out = torch.empty_like(q)
     bt_d = torch.from_numpy(bt).to(dev)
     lens_d = torch.from_numpy(lens).to(dev)
-    ws = torch.empty(capi.turboquant_decode_workspace_size(B, Hq, D, bt.shape[1], BS),
+    ws = torch.empty(capi.turboquant_decode_workspace_size(B, Hq, Hkv, D, bt.shape[1], BS),
                      dtype=torch.uint8, device=dev)
     scale = 1.0 / math.sqrt(D)
     stream = torch.cuda.current_stream()

@@ -70,13 +70,18 @@ int vmc_reshape_and_cache(const void* key, const void* value, void* key_cache,
  * (num_heads / num_kv_heads).
  *   out, query    [batch][num_heads][head_dim] of q_dtype
  *   block_tables  int32 [batch][max_num_blocks_per_req]; entries < 0 are holes
- *   seq_lens      int32 [batch]; 0 writes a zero row
- *   workspace     >= vmc_paged_decode_workspace_size(...) bytes
- *   max_num_kv_splits  cap on splits per sequence (<= 0: library default)
- * Limits: head_dim == 128, num_heads / num_kv_heads <= 16, num_kv_heads <= 16.
+ *   seq_lens      int32 [batch]; <= 0 writes a zero row
+ *   workspace     >= vmc_paged_decode_workspace_size(...) bytes (device memory;
+ *                 may be NULL when that size is 0)
+ *   max_num_kv_splits  1: one pass per sequence, no workspace (paged_attention_v1);
+ *                 > 1: the batch's pages are split evenly over the GPU with at
+ *                 most batch * max_num_kv_splits pieces; <= 0: no cap
+ * Limits: head_dim == 128, num_heads / num_kv_heads <= 16, num_kv_heads <= 8.
+ * Two launches on `stream` (split pass, merge of cut sequences); no host
+ * synchronisation.  The workspace size depends on the current device's CU count.
  */
-size_t vmc_paged_decode_workspace_size(int batch_size, int num_heads, int head_dim,
-                                       int max_num_blocks_per_req, int block_size,
+size_t vmc_paged_decode_workspace_size(int batch_size, int num_heads, int num_kv_heads,
+                                       int head_dim, int max_num_blocks_per_req, int block_size,
                                        int max_num_kv_splits);
 int vmc_paged_attention_decode(void* out, const void* query, const void* key_cache,
                                const void* value_cache, const int32_t* block_tables,
@@ -134,10 +139,11 @@ int vmc_turboquant_store(const void* key, const void* value, void* kv_cache,
  * turboquant_kernels.cu:939-1007): q rotated by the Hadamard transform, K
  * reconstructed from centroids (norm-corrected, times the stored norm), V =
  * code*scale + zero, fp32 online softmax, LSE merge.  The caller provides the
- * workspace (the reference grew it inside the call).
+ * workspace (the reference grew it inside the call); max_num_kv_splits and
+ * limits as for vmc_paged_attention_decode; half_dtype must be VMC_DTYPE_F16.
  */
-size_t vmc_turboquant_decode_workspace_size(int batch_size, int num_heads, int head_dim,
-                                            int64_t max_num_blocks_per_req,
+size_t vmc_turboquant_decode_workspace_size(int batch_size, int num_heads, int num_kv_heads,
+                                            int head_dim, int64_t max_num_blocks_per_req,
                                             int64_t block_size, int max_num_kv_splits);
 int vmc_turboquant_decode_attention(void* output, const void* query, const void* kv_cache,
                                     const int32_t* block_tables, const int32_t* seq_lens,

@@ -55,7 +55,7 @@ def load():
     L.vmc_reshape_and_cache.restype = _I
     L.vmc_reshape_and_cache.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I64, _I64, _I, _I, _I, _P]
     L.vmc_paged_decode_workspace_size.restype = _SZ
-    L.vmc_paged_decode_workspace_size.argtypes = [_I, _I, _I, _I, _I, _I]
+    L.vmc_paged_decode_workspace_size.argtypes = [_I, _I, _I, _I, _I, _I, _I]
     L.vmc_paged_attention_decode.restype = _I
     L.vmc_paged_attention_decode.argtypes = [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F,
                                              _I, _I, _I, _I, _P, _SZ, _P]
@@ -66,7 +66,7 @@ def load():
     L.vmc_turboquant_store.restype = _I
     L.vmc_turboquant_store.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I64, C.POINTER(TQConfig), _I, _P]
     L.vmc_turboquant_decode_workspace_size.restype = _SZ
-    L.vmc_turboquant_decode_workspace_size.argtypes = [_I, _I, _I, _I64, _I64, _I]
+    L.vmc_turboquant_decode_workspace_size.argtypes = [_I, _I, _I, _I, _I64, _I64, _I]
     L.vmc_turboquant_decode_attention.restype = _I
     L.vmc_turboquant_decode_attention.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I64,
                                                   _I64, C.POINTER(TQConfig), _I, _I, _P, _SZ, _P]
@@ -154,10 +154,10 @@ def reshape_and_cache(key, value, key_cache, value_cache, slot_mapping, block_si
     _check(rc, "vmc_reshape_and_cache")
 
 
-def paged_decode_workspace_size(batch, num_heads, head_dim=128, max_blocks=0, block_size=16,
-                                max_splits=0):
-    return int(load().vmc_paged_decode_workspace_size(batch, num_heads, head_dim, max_blocks,
-                                                      block_size, max_splits))
+def paged_decode_workspace_size(batch, num_heads, num_kv_heads, head_dim=128, max_blocks=0,
+                                block_size=16, max_splits=0):
+    return int(load().vmc_paged_decode_workspace_size(batch, num_heads, num_kv_heads, head_dim,
+                                                      max_blocks, block_size, max_splits))
 
 
 def paged_attention_decode(out, query, key_cache, value_cache, block_tables, seq_lens,
@@ -166,9 +166,9 @@ def paged_attention_decode(out, query, key_cache, value_cache, block_tables, seq
     import torch
     B, Hq, D = query.shape
     max_blocks = block_tables.shape[1]
-    ws_bytes = paged_decode_workspace_size(B, Hq, D, max_blocks, block_size, max_splits)
+    ws_bytes = paged_decode_workspace_size(B, Hq, num_kv_heads, D, max_blocks, block_size, max_splits)
     if workspace is None:
-        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=query.device)
+        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=query.device)
     rc = load().vmc_paged_attention_decode(
         _ptr(out), _ptr(query), _ptr(key_cache), _ptr(value_cache), _ptr(block_tables),
         _ptr(seq_lens), B, Hq, num_kv_heads, D, block_size, max_blocks, scale,
@@ -186,10 +186,10 @@ def turboquant_store(key, value, kv_cache, slot_mapping, block_size, cfg, stream
     _check(rc, "vmc_turboquant_store")
 
 
-def turboquant_decode_workspace_size(batch, num_heads, head_dim=128, max_blocks=0, block_size=16,
-                                     max_splits=0):
-    return int(load().vmc_turboquant_decode_workspace_size(batch, num_heads, head_dim, max_blocks,
-                                                           block_size, max_splits))
+def turboquant_decode_workspace_size(batch, num_heads, num_kv_heads, head_dim=128, max_blocks=0,
+                                     block_size=16, max_splits=0):
+    return int(load().vmc_turboquant_decode_workspace_size(batch, num_heads, num_kv_heads, head_dim,
+                                                           max_blocks, block_size, max_splits))
 
 
 def turboquant_decode_attention(out, query, kv_cache, block_tables, seq_lens, num_kv_heads, scale,
@@ -197,9 +197,10 @@ def turboquant_decode_attention(out, query, kv_cache, block_tables, seq_lens, nu
     import torch
     B, Hq, D = query.shape
     max_blocks = block_tables.shape[1]
-    ws_bytes = turboquant_decode_workspace_size(B, Hq, D, max_blocks, block_size, max_splits)
+    ws_bytes = turboquant_decode_workspace_size(B, Hq, num_kv_heads, D, max_blocks, block_size,
+                                                max_splits)
     if workspace is None:
-        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=query.device)
+        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=query.device)
     rc = load().vmc_turboquant_decode_attention(
         _ptr(out), _ptr(query), _ptr(kv_cache), _ptr(block_tables), _ptr(seq_lens), B, Hq,
         num_kv_heads, D, scale, block_size, max_blocks, C.byref(cfg), _dtype_code(query),

@@ -6,12 +6,19 @@
 // sequence's tokens, read through the block table, GQA kv head = q head /
 // (Hq / Hkv) (ggml flash_attn_ext broadcast, ggml-cpu/ops.cpp:8260-8265).
 //
-// Work decomposition.  A work item is (sequence, split): a contiguous run of
-// pages of one sequence.  Every workgroup recomputes the same plan from
-// seq_lens (pages_b = ceil(L_b / bs); pages per split = max(pps_min,
-// ceil(total / target_items)); splits_b = min(max_splits, ...)) so no host
-// round trip or extra launch is needed; items beyond the plan exit.  The
-// workgroup has one wave per KV head; a page of the reference layout holds
+// Work decomposition ("flat").  The batch's pages are numbered sequence after
+// sequence (pages_b = ceil(L_b / bs)); workgroup w of n takes the equal share
+// [w T / n, (w+1) T / n) of the T pages, whatever sequences it crosses, so
+// every workgroup does the same work and the grid is one resident wave of
+// workgroups.  Each workgroup recomputes the layout from seq_lens (no host
+// round trip).  A sequence that lies inside one workgroup's range is written
+// directly; a sequence cut by a range boundary leaves an fp32 partial (o, m, l)
+// per piece -- at most two per workgroup, slot 2w for the piece that continues
+// from the previous range and 2w+1 for the piece that continues into the next
+// -- and a small second kernel merges them.  max_num_kv_splits == 1 instead
+// gives each sequence its own workgroup (no partials, no workspace).
+//
+// The workgroup has one wave per KV head; a page of the reference layout holds
 // all heads of 16 tokens contiguously, so the workgroup reads whole pages with
 // 16-byte loads (quantized formats stage the page in LDS; f16/bf16 pages are
 // read straight into MFMA operand registers).
@@ -31,12 +38,10 @@
 // sum(P*zero): the MFMA runs on the exact small-integer codes.
 // q_rot = H q is a Walsh-Hadamard transform done in registers (the order the
 // oracle and the store kernel share).
-//
-// Partials (multi-split sequences) are fp32 (o, m, l) per (item, head) in the
-// caller's workspace; vmc_decode_merge_kernel combines them.
 #include "vmc_common.hpp"
 #include "vmc_tq.hpp"
 
+#include <mutex>
 #include <utility>
 
 namespace vmc {
@@ -44,7 +49,7 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kBs = 16;
-constexpr int kMaxItemPages = 1024;  // block-table slice of one work item, staged in LDS
+constexpr int kChunkPages = 1024;  // pages whose block-table entries are staged in LDS at once
 constexpr float kNegInf = -__builtin_inff();
 
 enum { FMT_F16 = 0, FMT_BF16 = 1, FMT_Q8_0 = 2, FMT_Q4_0 = 3, FMT_TQ = 4 };
@@ -76,75 +81,104 @@ struct DecodeParams {
     const uint8_t* vc;
     const int32_t* bt;
     const int32_t* seq_lens;
-    float* part;       // [items][Hq][D + 2]
-    int32_t* seqinfo;  // [B][2]: first item, number of splits
+    float* part;  // [2 * grid][Hq][D + 2]: o, m, l of cut sequences
     int B, Hq, Hkv, G, max_blocks;
     float scale_log2;
     int64_t page_bytes;  // one page of one cache, all heads
     int entry_bytes;     // one (token, head) entry (TQ: the aligned slot)
     int hnd;
-    int target_items, pps_min, max_splits;
+    int per_seq;         // 1: one workgroup per sequence
+    int pps_min, max_splits;
+    int grid;            // launched decode workgroups
     int q_bf16;
     // TurboQuant
     int mse_bytes, key_packed, val_data;
     TQTables tab;
 };
 
-struct Plan {
-    int b, s, nsp, first_item, p0, p1, L;
-};
+// ------------------------------------------------------------------ layout
 
-// Identical in every workgroup (and in the merge kernel): a pure function of
-// seq_lens.  Executed by one wave; lanes stride over sequences.
-__device__ void compute_plan(const DecodeParams& p, int item, Plan* out) {
-    const int lane = threadIdx.x & 63;
+__device__ __forceinline__ int seq_pages(const DecodeParams& p, int b, int* L_out) {
+    const int L = min(p.seq_lens[b], p.max_blocks * kBs);
+    *L_out = L;
+    return L > 0 ? (L + kBs - 1) / kBs : 0;
+}
+
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        const int u = __shfl_up(v, m, 64);
+        if (lane >= m) v += u;
+    }
+    return v;
+}
+
+// total pages of the batch (one wave, result in every lane)
+__device__ int total_pages(const DecodeParams& p, int lane) {
     int total = 0;
     for (int b0 = 0; b0 < p.B; b0 += 64) {
-        const int b = b0 + lane;
-        const int L = b < p.B ? min(p.seq_lens[b], p.max_blocks * kBs) : 0;
-        int pages = L > 0 ? (L + kBs - 1) / kBs : 0;
+        int L = 0;
+        int pg = b0 + lane < p.B ? seq_pages(p, b0 + lane, &L) : 0;
 #pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) pages += __shfl_xor(pages, m, 64);
-        total += pages;
+        for (int m = 32; m >= 1; m >>= 1) pg += __shfl_xor(pg, m, 64);
+        total += pg;
     }
-    const int pps = max(p.pps_min, (total + p.target_items - 1) / p.target_items);
-    int carry = 0;
+    return total;
+}
+
+// workgroups that get pages: the launched grid, fewer when the batch is small
+__device__ __forceinline__ int effective_wgs(const DecodeParams& p, int T, int grid) {
+    int n = min(grid, max(1, (T + p.pps_min - 1) / p.pps_min));
+    return max(1, min(n, T));
+}
+
+// workgroup whose range holds global page g: floor(((g + 1) n - 1) / T)
+__device__ __forceinline__ int wg_of_page(int64_t g, int n, int T) {
+    return (int)(((g + 1) * n - 1) / T);
+}
+
+struct WGPlan {
+    int p_lo, p_hi;        // global page range
+    int first_b, last_b;   // sequences holding p_lo and p_hi - 1
+    int first_cut, last_cut;  // first piece continues from before p_lo / last past p_hi
+};
+
+// Sequences with pages in [c_lo, c_hi), in order, into LDS (one wave).  In the
+// same pass: the sequences holding p_lo and p_hi - 1.
+__device__ int collect_segments(const DecodeParams& p, int c_lo, int c_hi, int lane, int* seg_b,
+                                int* seg_ps, int* seg_L, WGPlan* plan, bool plan_ends) {
+    const int p_lo = plan->p_lo, p_hi = plan->p_hi;
+    int carry = 0, ns = 0;
     for (int b0 = 0; b0 < p.B; b0 += 64) {
         const int b = b0 + lane;
-        const int L = b < p.B ? min(p.seq_lens[b], p.max_blocks * kBs) : 0;
-        const int pages = L > 0 ? (L + kBs - 1) / kBs : 0;
-        int nsp = 0, ppsb = 0;
-        if (b < p.B) {
-            nsp = pages > 0 ? min(p.max_splits, (pages + pps - 1) / pps) : 1;
-            ppsb = pages > 0 ? min(kMaxItemPages, (pages + nsp - 1) / nsp) : 0;
-            nsp = pages > 0 ? (pages + ppsb - 1) / ppsb : 1;
+        int L = 0;
+        const int pg = b < p.B ? seq_pages(p, b, &L) : 0;
+        const int incl = wave_incl_scan(pg, lane);
+        const int ps = carry + incl - pg, pe = ps + pg;
+        const bool hit = pg > 0 && ps < c_hi && pe > c_lo;
+        const uint64_t bal = __ballot(hit);
+        if (hit) {
+            const int idx = ns + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                          __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+            seg_b[idx] = b;
+            seg_ps[idx] = ps;
+            seg_L[idx] = L;
         }
-        int incl = nsp;
-#pragma unroll
-        for (int m = 1; m < 64; m <<= 1) {
-            const int v = __shfl_up(incl, m, 64);
-            if (lane >= m) incl += v;
-        }
-        const int first = carry + incl - nsp;
-        const bool mine = b < p.B && item >= first && item < first + nsp;
-        const unsigned long long bal = __ballot(mine);
-        if (bal) {
-            const int src = __builtin_ctzll(bal);
-            if (lane == src) {
-                const int s = item - first;
-                out->b = b;
-                out->s = s;
-                out->nsp = nsp;
-                out->first_item = first;
-                out->p0 = s * ppsb;
-                out->p1 = min(pages, (s + 1) * ppsb);
-                out->L = L;
+        // at most one lane holds each end page: it writes the shared plan
+        if (plan_ends && pg > 0) {
+            if (ps <= p_lo && p_lo < pe) {
+                plan->first_b = b;
+                plan->first_cut = ps < p_lo;
             }
-            return;
+            if (ps <= p_hi - 1 && p_hi - 1 < pe) {
+                plan->last_b = b;
+                plan->last_cut = pe > p_hi;
+            }
         }
+        ns += __popcll(bal);
         carry += __shfl(incl, 63, 64);
     }
-    if (lane == 0) out->b = -1;
+    return ns;
 }
 
 // ------------------------------------------------------------------ operands
@@ -170,11 +204,6 @@ __device__ __forceinline__ uint32_t lds16(const uint8_t* p) {
     return (uint32_t)*reinterpret_cast<const uint16_t*>(p);
 }
 
-// int codes (0..15) -> exact fp16 via the 1024 + c bit trick
-__device__ __forceinline__ _Float16 code_f16(uint32_t c) {
-    return __builtin_bit_cast(_Float16, (uint16_t)(0x6400u | c)) - (_Float16)1024.0f;
-}
-
 template <int FMT>
 __device__ __forceinline__ int entry_off(int tok, int g, int Hkv, int E, int hnd) {
     return hnd ? (g * kBs + tok) * E : (tok * Hkv + g) * E;
@@ -188,128 +217,201 @@ paged_decode_kernel(DecodeParams p) {
     using AT = typename std::conditional<MBF16, bf16x8, f16x8>::type;
     using PT = typename std::conditional<MBF16, s16x4, f16x4>::type;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    __shared__ Plan plan;
+    __shared__ WGPlan plan;
+    __shared__ int n_seg;
     __shared__ __attribute__((aligned(16))) float wscr_all[8][48];  // per-wave exchange
-    __shared__ int32_t bt_lds[kMaxItemPages];
+    __shared__ int32_t bt_lds[kChunkPages];    // block of each page of the chunk
+    __shared__ int32_t info_lds[kChunkPages];  // b << 6 | valid tokens << 1 | piece ends
+    __shared__ int32_t seg_b[kChunkPages], seg_ps[kChunkPages], seg_L[kChunkPages];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int r16 = lane & 15, grp = lane >> 4;
-    const int item = blockIdx.x;
-
-    if (wave == 0) compute_plan(p, item, &plan);
+    const int w = blockIdx.x;
     constexpr bool kStaged = FMT >= FMT_Q8_0;
-    // static LDS: the LUT's address is a compile-time offset of each read
-    __shared__ uint32_t lut[FMT == FMT_TQ ? 256 : 1];
-    uint8_t* pagebuf = smem;
-    if constexpr (FMT == FMT_TQ) build_pair_lut<KB>(lut, p.tab);
-    __syncthreads();
-    const int b = __builtin_amdgcn_readfirstlane(plan.b);
-    if (b < 0) return;
-    // wave-uniform: keep them in SGPRs so block-table reads are scalar loads
-    const int s = __builtin_amdgcn_readfirstlane(plan.s);
-    const int nsp = __builtin_amdgcn_readfirstlane(plan.nsp);
-    const int L = __builtin_amdgcn_readfirstlane(plan.L);
-    const int p0 = __builtin_amdgcn_readfirstlane(plan.p0);
-    const int p1 = __builtin_amdgcn_readfirstlane(plan.p1);
-    if (s == 0 && tid == 0) {
-        p.seqinfo[2 * b] = plan.first_item;
-        p.seqinfo[2 * b + 1] = nsp;
+
+    // ---- this workgroup's page range
+    if (wave == 0) {
+        WGPlan wp;
+        if (p.per_seq) {
+            int ps = 0, pg = 0, L = 0;
+            for (int b0 = 0; b0 < p.B; b0 += 64) {  // pages before sequence w
+                const int b = b0 + lane;
+                int v = b < w ? seq_pages(p, b, &L) : 0;
+#pragma unroll
+                for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+                ps += v;
+            }
+            pg = seq_pages(p, w, &L);
+            wp = {ps, ps + pg, w, w, 0, 0};
+        } else {
+            const int T = total_pages(p, lane);
+            const int n = effective_wgs(p, T, p.grid);
+            wp.p_lo = w < n ? (int)((int64_t)w * T / n) : 0;
+            wp.p_hi = w < n ? (int)((int64_t)(w + 1) * T / n) : 0;
+            wp.first_b = wp.last_b = -1;
+            wp.first_cut = wp.last_cut = 0;
+        }
+        if (lane == 0) plan = wp;
     }
+    __syncthreads();
+    const int p_lo = __builtin_amdgcn_readfirstlane(plan.p_lo);
+    const int p_hi = __builtin_amdgcn_readfirstlane(plan.p_hi);
 
     const int g = wave;  // kv head of this wave
     float* wscr = wscr_all[wave];
     const int G = p.G;
     const int hq0 = g * G;
-    const int64_t qrow = ((int64_t)b * p.Hq + hq0 + r16) * kD;
     const bool head_ok = r16 < G;
+
+    if (p_lo >= p_hi) {
+        // no pages: per-sequence mode writes the sequence's zero rows
+        if (p.per_seq && w < p.B && head_ok) {
+            uint16_t* o = reinterpret_cast<uint16_t*>(p.out) + ((int64_t)w * p.Hq + hq0 + r16) * kD + 32 * grp;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) reinterpret_cast<u32x4*>(o)[c] = u32x4{0u, 0u, 0u, 0u};
+        }
+        return;
+    }
+
+    // static LDS: the LUT's address is a compile-time offset of each read
+    __shared__ uint32_t lut[FMT == FMT_TQ ? 256 : 1];
+    uint8_t* pagebuf = smem;
+    if constexpr (FMT == FMT_TQ) build_pair_lut<KB>(lut, p.tab);
 
     // ---- Q operand: lane (r16 = head, grp) holds dims 32*grp + 8*j + e, j = MFMA index
     AT qb[4];
-    if constexpr (FMT == FMT_TQ) {
-        float y[32];
-        if (head_ok) {
-            const u32x4* src = reinterpret_cast<const u32x4*>(p.q + qrow + 32 * grp);
+    auto load_q = [&](int b) __attribute__((always_inline)) {
+        const int64_t qrow = ((int64_t)b * p.Hq + hq0 + r16) * kD;
+        if constexpr (FMT == FMT_TQ) {
+            float y[32];
+            if (head_ok) {
+                const u32x4* src = reinterpret_cast<const u32x4*>(p.q + qrow + 32 * grp);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const u32x4 w = src[c];
+                for (int c = 0; c < 4; ++c) {
+                    const u32x4 wv = src[c];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint16_t lo = (uint16_t)(w[e] & 0xffff), hi = (uint16_t)(w[e] >> 16);
-                    y[8 * c + 2 * e] = p.q_bf16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
-                    y[8 * c + 2 * e + 1] = p.q_bf16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
+                    for (int e = 0; e < 4; ++e) {
+                        const uint16_t lo = (uint16_t)(wv[e] & 0xffff), hi = (uint16_t)(wv[e] >> 16);
+                        y[8 * c + 2 * e] = p.q_bf16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
+                        y[8 * c + 2 * e + 1] = p.q_bf16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
+                    }
                 }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 32; ++e) y[e] = 0.0f;
             }
+            // Walsh-Hadamard: half-widths 1..16 inside the lane, 32 and 64 across
+            // the lane groups (dim bit 32 = grp bit 0, dim bit 64 = grp bit 1).
+#pragma unroll
+            for (int h = 1; h < 32; h <<= 1)
+#pragma unroll
+                for (int i = 0; i < 32; i += 2 * h)
+#pragma unroll
+                    for (int j = i; j < i + h; ++j) {
+                        const float a = y[j], c = y[j + h];
+                        y[j] = a + c;
+                        y[j + h] = a - c;
+                    }
+#pragma unroll
+            for (int e = 0; e < 32; ++e) {
+                const float o = shfl_xor(y[e], 16);
+                y[e] = (grp & 1) ? o - y[e] : y[e] + o;
+            }
+#pragma unroll
+            for (int e = 0; e < 32; ++e) {
+                const float o = shfl_xor(y[e], 32);
+                y[e] = (grp & 2) ? o - y[e] : y[e] + o;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) qb[j][e] = (_Float16)__fmul_rn(y[8 * j + e], p.tab.rot_c);
         } else {
 #pragma unroll
-            for (int e = 0; e < 32; ++e) y[e] = 0.0f;
-        }
-        // Walsh-Hadamard: half-widths 1..16 inside the lane, 32 and 64 across
-        // the lane groups (dim bit 32 = grp bit 0, dim bit 64 = grp bit 1).
+            for (int j = 0; j < 4; ++j) {
+                u32x4 wv = {0u, 0u, 0u, 0u};
+                if (head_ok) wv = *reinterpret_cast<const u32x4*>(p.q + qrow + 32 * grp + 8 * j);
+                const bool qbf = p.q_bf16 != 0;
 #pragma unroll
-        for (int h = 1; h < 32; h <<= 1)
-#pragma unroll
-            for (int i = 0; i < 32; i += 2 * h)
-#pragma unroll
-                for (int j = i; j < i + h; ++j) {
-                    const float a = y[j], c = y[j + h];
-                    y[j] = a + c;
-                    y[j + h] = a - c;
-                }
-#pragma unroll
-        for (int e = 0; e < 32; ++e) {
-            const float o = shfl_xor(y[e], 16);
-            y[e] = (grp & 1) ? o - y[e] : y[e] + o;
-        }
-#pragma unroll
-        for (int e = 0; e < 32; ++e) {
-            const float o = shfl_xor(y[e], 32);
-            y[e] = (grp & 2) ? o - y[e] : y[e] + o;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) qb[j][e] = (_Float16)__fmul_rn(y[8 * j + e], p.tab.rot_c);
-    } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            u32x4 w = {0u, 0u, 0u, 0u};
-            if (head_ok) w = *reinterpret_cast<const u32x4*>(p.q + qrow + 32 * grp + 8 * j);
-            const bool qbf = p.q_bf16 != 0;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint16_t lo = (uint16_t)(w[e] & 0xffff), hi = (uint16_t)(w[e] >> 16);
-                if constexpr (MBF16) {
-                    const uint16_t l2 = qbf ? lo : f32_to_bf16_bits(f16_bits_to_f32(lo));
-                    const uint16_t h2 = qbf ? hi : f32_to_bf16_bits(f16_bits_to_f32(hi));
-                    qb[j][2 * e] = __builtin_bit_cast(__bf16, l2);
-                    qb[j][2 * e + 1] = __builtin_bit_cast(__bf16, h2);
-                } else {
-                    qb[j][2 * e] = qbf ? (_Float16)bf16_bits_to_f32(lo) : __builtin_bit_cast(_Float16, lo);
-                    qb[j][2 * e + 1] = qbf ? (_Float16)bf16_bits_to_f32(hi) : __builtin_bit_cast(_Float16, hi);
+                for (int e = 0; e < 4; ++e) {
+                    const uint16_t lo = (uint16_t)(wv[e] & 0xffff), hi = (uint16_t)(wv[e] >> 16);
+                    if constexpr (MBF16) {
+                        const uint16_t l2 = qbf ? lo : f32_to_bf16_bits(f16_bits_to_f32(lo));
+                        const uint16_t h2 = qbf ? hi : f32_to_bf16_bits(f16_bits_to_f32(hi));
+                        qb[j][2 * e] = __builtin_bit_cast(__bf16, l2);
+                        qb[j][2 * e + 1] = __builtin_bit_cast(__bf16, h2);
+                    } else {
+                        qb[j][2 * e] = qbf ? (_Float16)bf16_bits_to_f32(lo) : __builtin_bit_cast(_Float16, lo);
+                        qb[j][2 * e + 1] = qbf ? (_Float16)bf16_bits_to_f32(hi) : __builtin_bit_cast(_Float16, hi);
+                    }
                 }
             }
         }
-    }
+    };
 
-    // ---- running state
+    // ---- running state of the current piece
     f32x4 oacc[8];
+    float m_run, l_part, z_part;  // m_run per head r16 (log2 domain), l/z partial over this lane's tokens
+    auto reset_state = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int c = 0; c < 8; ++c) oacc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run = kNegInf;  // per head r16 (log2 domain), replicated over grp
-    float l_part = 0.0f;    // partial over this lane's tokens
-    float z_part = 0.0f;    // TurboQuant: partial sum of p * zero
+        for (int c = 0; c < 8; ++c) oacc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+        m_run = kNegInf;
+        l_part = 0.0f;
+        z_part = 0.0f;
+    };
+    reset_state();
+    int cur_b = -1;
 
     const int Hkv = p.Hkv, E = p.entry_bytes, hnd = p.hnd;
     const int64_t page_bytes = p.page_bytes;
-    // this item's block-table slice -> LDS, so the page loop issues no vector
-    // loads besides the page prefetch (keeps the load counter exact)
-    {
-        const int32_t* bt_row = p.bt + (int64_t)b * p.max_blocks;
-        for (int i = tid; i < p1 - p0; i += blockDim.x) bt_lds[i] = bt_row[p0 + i];
-        __syncthreads();
-    }
     const int nthreads = blockDim.x;
+
+    // ---- finish a piece of sequence b: write the rows, or the partial slot
+    auto finalize = [&](int b) __attribute__((always_inline)) {
+        const bool cut_before = b == __builtin_amdgcn_readfirstlane(plan.first_b) &&
+                                __builtin_amdgcn_readfirstlane(plan.first_cut);
+        const bool cut_after = b == __builtin_amdgcn_readfirstlane(plan.last_b) &&
+                               __builtin_amdgcn_readfirstlane(plan.last_cut);
+        const bool whole = !cut_before && !cut_after;
+        const int slot = cut_before ? 2 * w : 2 * w + 1;
+        const float l_tot = sum_over_groups(l_part);
+        const float z_tot = (FMT == FMT_TQ) ? sum_over_groups(z_part) : 0.0f;
+        const f32x4 lh4 = gather4_from_row0(l_tot, wscr, r16, grp);
+        const f32x4 zh4 = gather4_from_row0(z_tot, wscr + 16, r16, grp);
+        const f32x4 mh4 = gather4_from_row0(m_run, wscr + 32, r16, grp);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int hh = 4 * grp + i;
+            const float lh = lh4[i], zh = zh4[i], mh = mh4[i];
+            if (hh >= G) continue;
+            const int hq = hq0 + hh;
+            if (whole) {
+                const float inv = lh > 0.0f ? 1.0f / lh : 0.0f;
+                uint32_t wd[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float v0 = (oacc[2 * e][i] + zh) * inv;
+                    const float v1 = (oacc[2 * e + 1][i] + zh) * inv;
+                    const uint16_t b0 = p.q_bf16 ? f32_to_bf16_bits(v0) : f32_to_f16_bits(v0);
+                    const uint16_t b1 = p.q_bf16 ? f32_to_bf16_bits(v1) : f32_to_f16_bits(v1);
+                    wd[e] = (uint32_t)b0 | ((uint32_t)b1 << 16);
+                }
+                uint16_t* o = reinterpret_cast<uint16_t*>(p.out) + ((int64_t)b * p.Hq + hq) * kD + 8 * r16;
+                *reinterpret_cast<u32x4*>(o) = u32x4{wd[0], wd[1], wd[2], wd[3]};
+            } else {
+                float* o = p.part + ((int64_t)slot * p.Hq + hq) * (kD + 2);
+                // (D + 2) floats per row: 8-byte aligned only, store as float2
+                float* od = o + 8 * r16;
+                *reinterpret_cast<float2*>(od + 0) = make_float2(oacc[0][i] + zh, oacc[1][i] + zh);
+                *reinterpret_cast<float2*>(od + 2) = make_float2(oacc[2][i] + zh, oacc[3][i] + zh);
+                *reinterpret_cast<float2*>(od + 4) = make_float2(oacc[4][i] + zh, oacc[5][i] + zh);
+                *reinterpret_cast<float2*>(od + 6) = make_float2(oacc[6][i] + zh, oacc[7][i] + zh);
+                if (r16 == 0) *reinterpret_cast<float2*>(o + kD) = make_float2(mh, lh);
+            }
+        }
+        reset_state();
+    };
 
     // staged formats: PF pages in flight in registers -> LDS double buffer
     using SP = StagePlan<FMT, KB, VB>;
@@ -318,12 +420,12 @@ paged_decode_kernel(DecodeParams p) {
     const int n16 = (FMT == FMT_TQ) ? n16_k : 2 * n16_k;
     const int lds_page = (FMT == FMT_TQ) ? (int)page_bytes : 2 * (int)page_bytes;
     u32x4 stage[PF][SPP];
-    auto stage_load = [&](auto slot_c, int pg) __attribute__((always_inline)) {
+    auto stage_load = [&](auto slot_c, int i) __attribute__((always_inline)) {
         constexpr int S = decltype(slot_c)::value;
         // Branch-free so the compiler can count outstanding loads exactly (a
         // hole reads page 0, whose tokens are then masked; chunks past the
         // page re-read its last chunk and are not stored).
-        const int32_t blk = max(bt_lds[pg - p0], 0);
+        const int32_t blk = max(bt_lds[i], 0);
         const u32x4* ks = reinterpret_cast<const u32x4*>(p.kc + (int64_t)blk * page_bytes);
         const u32x4* vs = reinterpret_cast<const u32x4*>(p.vc + (int64_t)blk * page_bytes);
 #pragma unroll
@@ -345,9 +447,9 @@ paged_decode_kernel(DecodeParams p) {
 
     // direct formats: per-lane operand registers for one page
     u32x4 kreg[4], vreg[4];
-    auto direct_load = [&](int pg) __attribute__((always_inline)) {
-        const int32_t blk = bt_lds[pg - p0];
-        const int tok0 = pg * kBs;
+    auto direct_load = [&](int i) __attribute__((always_inline)) {
+        const int32_t blk = bt_lds[i];
+        const int nv = (info_lds[i] >> 1) & 31;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             kreg[c] = u32x4{0u, 0u, 0u, 0u};
@@ -356,22 +458,28 @@ paged_decode_kernel(DecodeParams p) {
         if (blk < 0) return;
         const uint8_t* kp = p.kc + (int64_t)blk * page_bytes;
         const uint8_t* vp = p.vc + (int64_t)blk * page_bytes;
-        if (tok0 + r16 < L) {
+        if (r16 < nv) {
             const u32x4* src = reinterpret_cast<const u32x4*>(kp + entry_off<FMT>(r16, g, Hkv, E, hnd) + 64 * grp);
 #pragma unroll
             for (int c = 0; c < 4; ++c) kreg[c] = src[c];
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int tok = 4 * grp + i;
-            if (tok0 + tok < L)
-                vreg[i] = *reinterpret_cast<const u32x4*>(vp + entry_off<FMT>(tok, g, Hkv, E, hnd) + 16 * r16);
+        for (int i2 = 0; i2 < 4; ++i2) {
+            const int tok = 4 * grp + i2;
+            if (tok < nv)
+                vreg[i2] = *reinterpret_cast<const u32x4*>(vp + entry_off<FMT>(tok, g, Hkv, E, hnd) + 16 * r16);
         }
     };
 
-    auto process = [&](int pg, const uint8_t* kpage, const uint8_t* vpage) __attribute__((always_inline)) {
-        const int32_t blk = bt_lds[pg - p0];
-        const int nv = blk < 0 ? 0 : min(kBs, L - pg * kBs);  // valid tokens in this page
+    int npc = 0;  // pages of the current chunk
+    auto process = [&](int i, const uint8_t* kpage, const uint8_t* vpage) __attribute__((always_inline)) {
+        const int info = __builtin_amdgcn_readfirstlane(info_lds[i]);
+        const int b = info >> 6;
+        const int nv = (info >> 1) & 31;  // valid tokens in this page
+        if (b != cur_b) {  // a new sequence starts on this page
+            load_q(b);
+            cur_b = b;
+        }
         AT a[4];
         float rowf = p.scale_log2;  // factor of S row r16 (token r16)
         // V operand pieces (tokens 4*grp + i, dims 8*r16 .. +7) as fp16/bf16 bits
@@ -390,9 +498,9 @@ paged_decode_kernel(DecodeParams p) {
                     const uint8_t* cb = ke + 16 * grp;  // 16 bytes, 2-byte aligned
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        const uint32_t w = lds16(cb + 4 * j) | (lds16(cb + 4 * j + 2) << 16);
+                        const uint32_t wv = lds16(cb + 4 * j) | (lds16(cb + 4 * j + 2) << 16);
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) aw[j][e] = lut[(w >> (8 * e)) & 0xffu];
+                        for (int e = 0; e < 4; ++e) aw[j][e] = lut[(wv >> (8 * e)) & 0xffu];
                     }
                 } else {
                     const uint8_t* cb = ke + 12 * grp;  // 12 bytes = four 8-code groups
@@ -421,21 +529,21 @@ paged_decode_kernel(DecodeParams p) {
                 // V: codes of tokens 4*grp + i, dims 8*r16 .. +7, scale and zero
                 uint32_t cw[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int tok = 4 * grp + i;
+                for (int i2 = 0; i2 < 4; ++i2) {
+                    const int tok = 4 * grp + i2;
                     const uint8_t* ve = kpage + entry_off<FMT>(tok, g, Hkv, E, hnd) + p.key_packed;
                     if constexpr (VB == 4) {
-                        cw[i] = lds16(ve + 4 * r16) | (lds16(ve + 4 * r16 + 2) << 16);
+                        cw[i2] = lds16(ve + 4 * r16) | (lds16(ve + 4 * r16 + 2) << 16);
                     } else {
                         // ve is even, so ve + 3*r16 is odd exactly when r16 is:
                         // read the two aligned 16-bit words around it
                         const uint8_t* al2 = ve + 3 * r16 - (r16 & 1);
-                        const uint32_t w = lds16(al2) | (lds16(al2 + 2) << 16);
-                        cw[i] = (w >> (8 * (r16 & 1))) & 0xffffffu;
+                        const uint32_t wv = lds16(al2) | (lds16(al2 + 2) << 16);
+                        cw[i2] = (wv >> (8 * (r16 & 1))) & 0xffffffu;
                     }
                     const bool ok = tok < nv;
-                    vsc[i] = ok ? f16_bits_to_f32((uint16_t)lds16(ve + p.val_data)) : 0.0f;
-                    vzr[i] = ok ? f16_bits_to_f32((uint16_t)lds16(ve + p.val_data + 2)) : 0.0f;
+                    vsc[i2] = ok ? f16_bits_to_f32((uint16_t)lds16(ve + p.val_data)) : 0.0f;
+                    vzr[i2] = ok ? f16_bits_to_f32((uint16_t)lds16(ve + p.val_data + 2)) : 0.0f;
                 }
                 // B operands {token a, token b} per dim, exact fp16 codes via 1024 + c
 #pragma unroll
@@ -470,23 +578,23 @@ paged_decode_kernel(DecodeParams p) {
                         const int jj = 8 * j + e;  // index inside the 32-block
                         float x0, x1;
                         if constexpr (FMT == FMT_Q8_0) {
-                            const uint32_t w = lds16(kb + 2 + jj);
-                            x0 = (float)(int8_t)(w & 0xff);
-                            x1 = (float)(int8_t)(w >> 8);
+                            const uint32_t wv = lds16(kb + 2 + jj);
+                            x0 = (float)(int8_t)(wv & 0xff);
+                            x1 = (float)(int8_t)(wv >> 8);
                         } else {
                             const int bi = jj & 15;
-                            const uint32_t w = lds16(kb + 2 + bi);
+                            const uint32_t wv = lds16(kb + 2 + bi);
                             const int sh = jj < 16 ? 0 : 4;
-                            x0 = (float)((int)((w >> sh) & 0xf) - 8);
-                            x1 = (float)((int)((w >> (8 + sh)) & 0xf) - 8);
+                            x0 = (float)((int)((wv >> sh) & 0xf) - 8);
+                            x1 = (float)((int)((wv >> (8 + sh)) & 0xf) - 8);
                         }
                         a[j][e] = (_Float16)(x0 * d);
                         a[j][e + 1] = (_Float16)(x1 * d);
                     }
                 }
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int tok = 4 * grp + i;
+                for (int i2 = 0; i2 < 4; ++i2) {
+                    const int tok = 4 * grp + i2;
                     const bool ok = tok < nv;
                     const uint8_t* vb = vpage + entry_off<FMT>(tok, g, Hkv, E, hnd) + BE * (r16 >> 2);
                     const float dv = ok ? f16_bits_to_f32((uint16_t)lds16(vb)) : 0.0f;
@@ -495,19 +603,19 @@ paged_decode_kernel(DecodeParams p) {
                     for (int e = 0; e < 4; ++e) {
                         float x0, x1;
                         if constexpr (FMT == FMT_Q8_0) {
-                            const uint32_t w = lds16(vb + 2 + q0 + 2 * e);
-                            x0 = (float)(int8_t)(w & 0xff);
-                            x1 = (float)(int8_t)(w >> 8);
+                            const uint32_t wv = lds16(vb + 2 + q0 + 2 * e);
+                            x0 = (float)(int8_t)(wv & 0xff);
+                            x1 = (float)(int8_t)(wv >> 8);
                         } else {
                             const int jj = q0 + 2 * e;
                             const int bi = jj & 15;
                             const int sh = jj < 16 ? 0 : 4;
-                            const uint32_t w = lds16(vb + 2 + bi);
-                            x0 = (float)((int)((w >> sh) & 0xf) - 8);
-                            x1 = (float)((int)((w >> (8 + sh)) & 0xf) - 8);
+                            const uint32_t wv = lds16(vb + 2 + bi);
+                            x0 = (float)((int)((wv >> sh) & 0xf) - 8);
+                            x1 = (float)((int)((wv >> (8 + sh)) & 0xf) - 8);
                         }
-                        vw[i][e] = (uint32_t)f32_to_f16_bits(ok ? x0 * dv : 0.0f) |
-                                   ((uint32_t)f32_to_f16_bits(ok ? x1 * dv : 0.0f) << 16);
+                        vw[i2][e] = (uint32_t)f32_to_f16_bits(ok ? x0 * dv : 0.0f) |
+                                    ((uint32_t)f32_to_f16_bits(ok ? x1 * dv : 0.0f) << 16);
                     }
                 }
             }
@@ -515,23 +623,23 @@ paged_decode_kernel(DecodeParams p) {
             // f16 / bf16: operands straight from the registers loaded last iteration
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const u32x4 w = kreg[j];
+                const u32x4 wv = kreg[j];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     if constexpr (MBF16) {
-                        a[j][2 * e] = __builtin_bit_cast(__bf16, (uint16_t)(w[e] & 0xffff));
-                        a[j][2 * e + 1] = __builtin_bit_cast(__bf16, (uint16_t)(w[e] >> 16));
+                        a[j][2 * e] = __builtin_bit_cast(__bf16, (uint16_t)(wv[e] & 0xffff));
+                        a[j][2 * e + 1] = __builtin_bit_cast(__bf16, (uint16_t)(wv[e] >> 16));
                     } else {
-                        a[j][2 * e] = __builtin_bit_cast(_Float16, (uint16_t)(w[e] & 0xffff));
-                        a[j][2 * e + 1] = __builtin_bit_cast(_Float16, (uint16_t)(w[e] >> 16));
+                        a[j][2 * e] = __builtin_bit_cast(_Float16, (uint16_t)(wv[e] & 0xffff));
+                        a[j][2 * e + 1] = __builtin_bit_cast(_Float16, (uint16_t)(wv[e] >> 16));
                     }
                 }
             }
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i2 = 0; i2 < 4; ++i2)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) vw[i][e] = vreg[i][e];
-            if (pg + 1 < p1) direct_load(pg + 1);
+                for (int e = 0; e < 4; ++e) vw[i2][e] = vreg[i2][e];
+            if (i + 1 < npc) direct_load(i + 1);
         }
 
         // ---- S^T = K . Q^T
@@ -543,9 +651,9 @@ paged_decode_kernel(DecodeParams p) {
         if constexpr (FMT == FMT_TQ) rf = gather4_from_row0(rowf, wscr, r16, grp);
         float sv[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int tok = 4 * grp + i;
-            sv[i] = tok < nv ? sacc[i] * rf[i] : kNegInf;
+        for (int i2 = 0; i2 < 4; ++i2) {
+            const int tok = 4 * grp + i2;
+            sv[i2] = tok < nv ? sacc[i2] * rf[i2] : kNegInf;
         }
         float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
         mx = max_over_groups(mx);
@@ -560,18 +668,18 @@ paged_decode_kernel(DecodeParams p) {
             if constexpr (FMT == FMT_TQ) z_part *= alpha;
             const f32x4 al = gather4_from_row0(alpha, wscr + 16, r16, grp);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i2 = 0; i2 < 4; ++i2)
 #pragma unroll
-                for (int c = 0; c < 8; ++c) oacc[c][i] *= al[i];
+                for (int c = 0; c < 8; ++c) oacc[c][i2] *= al[i2];
             m_run = m_new;
         }
         const float m_use = m_run == kNegInf ? 0.0f : m_run;
         float pv[4], psum = 0.0f, zsum = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            pv[i] = __builtin_amdgcn_exp2f(sv[i] - m_use);
-            psum += pv[i];
-            if constexpr (FMT == FMT_TQ) zsum = __builtin_fmaf(pv[i], vzr[i], zsum);
+        for (int i2 = 0; i2 < 4; ++i2) {
+            pv[i2] = __builtin_amdgcn_exp2f(sv[i2] - m_use);
+            psum += pv[i2];
+            if constexpr (FMT == FMT_TQ) zsum = __builtin_fmaf(pv[i2], vzr[i2], zsum);
         }
         l_part += psum;
         if constexpr (FMT == FMT_TQ) z_part += zsum;
@@ -579,10 +687,10 @@ paged_decode_kernel(DecodeParams p) {
         // ---- O += P . V
         PT pa;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float pw = (FMT == FMT_TQ) ? pv[i] * vsc[i] : pv[i];
-            if constexpr (MBF16) pa[i] = (short)f32_to_bf16_bits(pw);
-            else pa[i] = (_Float16)pw;
+        for (int i2 = 0; i2 < 4; ++i2) {
+            const float pw = (FMT == FMT_TQ) ? pv[i2] * vsc[i2] : pv[i2];
+            if constexpr (MBF16) pa[i2] = (short)f32_to_bf16_bits(pw);
+            else pa[i2] = (_Float16)pw;
         }
         if constexpr (FMT != FMT_TQ) {
             // {token 0,1} and {token 2,3} halves of dims (2e, 2e+1)
@@ -598,140 +706,233 @@ paged_decode_kernel(DecodeParams p) {
             const PT vb = __builtin_bit_cast(PT, u32x2{bop[c][0], bop[c][1]});
             oacc[c] = mfma16x16x16(pa, vb, oacc[c]);
         }
+        if (info & 1) finalize(b);  // last page of this sequence's piece
     };
 
-    if constexpr (kStaged) {
-        // Ring of PF register slots: slot S holds page base+S+PF while page
-        // base+S is computed from LDS.  Loads and LDS stores are unconditional
-        // (tail pages clamp to the last page), so the only branch holds no
-        // memory loads and the compiler keeps exact load counters: each LDS
-        // store waits only for its own slot, PF-1 pages stay in flight.
-        const int npg = p1 - p0;
-        if (npg > 0) {
+    // ---- chunks of up to kChunkPages pages: stage the block-table slice and
+    // the per-page sequence info in LDS, then stream the pages
+    for (int c_lo = p_lo; c_lo < p_hi; c_lo += kChunkPages) {
+        const int c_hi = min(p_hi, c_lo + kChunkPages);
+        npc = c_hi - c_lo;
+        if (wave == 0) {
+            const int ns = collect_segments(p, c_lo, c_hi, lane, seg_b, seg_ps, seg_L, &plan,
+                                            c_lo == p_lo && !p.per_seq);
+            if (lane == 0) n_seg = ns;
+        }
+        __syncthreads();
+        const int ns = n_seg;
+        for (int i = tid; i < npc; i += nthreads) {
+            const int gp = c_lo + i;
+            int lo = 0, hi = ns - 1;  // last segment with seg_ps <= gp
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (seg_ps[mid] <= gp) lo = mid;
+                else hi = mid - 1;
+            }
+            const int b = seg_b[lo], L = seg_L[lo], pp = gp - seg_ps[lo];
+            const int pages_b = (L + kBs - 1) / kBs;
+            const int32_t blk = p.bt[(int64_t)b * p.max_blocks + pp];
+            const int nv = blk < 0 ? 0 : min(kBs, L - pp * kBs);
+            const int ends = pp == pages_b - 1 || gp == p_hi - 1;
+            bt_lds[i] = blk;
+            info_lds[i] = (b << 6) | (nv << 1) | ends;
+        }
+        __syncthreads();
+
+        if constexpr (kStaged) {
+            // Ring of PF register slots: slot S holds page base+S+PF while page
+            // base+S is computed from LDS.  Loads and LDS stores are unconditional
+            // (tail pages clamp to the last page), so the only branch holds no
+            // memory loads and the compiler keeps exact load counters: each LDS
+            // store waits only for its own slot, PF-1 pages stay in flight.
             static_for<PF>([&](auto sc) __attribute__((always_inline)) {
-                stage_load(sc, p0 + min((int)decltype(sc)::value, npg - 1));
+                stage_load(sc, min((int)decltype(sc)::value, npc - 1));
             });
             stage_store(std::integral_constant<int, 0>{}, pagebuf);
             __syncthreads();
-            for (int base = 0; base < npg; base += PF) {
+            for (int base = 0; base < npc; base += PF) {
                 static_for<PF>([&](auto sc) __attribute__((always_inline)) {
                     constexpr int S = decltype(sc)::value;
                     const int i = base + S;
                     const int cur = i & 1;
-                    if (i < npg) {  // uniform over the workgroup
+                    if (i < npc) {  // uniform over the workgroup
                         const uint8_t* kp = pagebuf + cur * lds_page;
-                        process(p0 + i, kp, kp + page_bytes);
+                        process(i, kp, kp + page_bytes);
                     }
-                    stage_load(sc, p0 + min(i + PF, npg - 1));
+                    stage_load(sc, min(i + PF, npc - 1));
                     stage_store(std::integral_constant<int, (S + 1) % PF>{}, pagebuf + (cur ^ 1) * lds_page);
                     __syncthreads();
                 });
             }
-        }
-    } else {
-        if (p0 < p1) direct_load(p0);
-        for (int pg = p0; pg < p1; ++pg) process(pg, nullptr, nullptr);
-    }
-
-    // ---- finalize: per-head sums live in lanes r16 = head; O rows in 4*grp + i
-    const float l_tot = sum_over_groups(l_part);
-    const float z_tot = (FMT == FMT_TQ) ? sum_over_groups(z_part) : 0.0f;
-    const bool single = nsp == 1;
-    const f32x4 lh4 = gather4_from_row0(l_tot, wscr, r16, grp);
-    const f32x4 zh4 = gather4_from_row0(z_tot, wscr + 16, r16, grp);
-    const f32x4 mh4 = gather4_from_row0(m_run, wscr + 32, r16, grp);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int hh = 4 * grp + i;
-        const float lh = lh4[i], zh = zh4[i], mh = mh4[i];
-        if (hh >= G) continue;
-        const int hq = hq0 + hh;
-        if (single) {
-            const float inv = lh > 0.0f ? 1.0f / lh : 0.0f;
-            uint32_t w[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float v0 = (oacc[2 * e][i] + zh) * inv;
-                const float v1 = (oacc[2 * e + 1][i] + zh) * inv;
-                const uint16_t b0 = p.q_bf16 ? f32_to_bf16_bits(v0) : f32_to_f16_bits(v0);
-                const uint16_t b1 = p.q_bf16 ? f32_to_bf16_bits(v1) : f32_to_f16_bits(v1);
-                w[e] = (uint32_t)b0 | ((uint32_t)b1 << 16);
-            }
-            uint16_t* o = reinterpret_cast<uint16_t*>(p.out) + ((int64_t)b * p.Hq + hq) * kD + 8 * r16;
-            *reinterpret_cast<u32x4*>(o) = u32x4{w[0], w[1], w[2], w[3]};
         } else {
-            float* o = p.part + ((int64_t)item * p.Hq + hq) * (kD + 2);
-            f32x4 lo = {oacc[0][i] + zh, oacc[1][i] + zh, oacc[2][i] + zh, oacc[3][i] + zh};
-            f32x4 hi = {oacc[4][i] + zh, oacc[5][i] + zh, oacc[6][i] + zh, oacc[7][i] + zh};
-            // (D + 2) floats per row: 8-byte aligned only, store as float2
-            float* od = o + 8 * r16;
-            *reinterpret_cast<float2*>(od + 0) = make_float2(lo[0], lo[1]);
-            *reinterpret_cast<float2*>(od + 2) = make_float2(lo[2], lo[3]);
-            *reinterpret_cast<float2*>(od + 4) = make_float2(hi[0], hi[1]);
-            *reinterpret_cast<float2*>(od + 6) = make_float2(hi[2], hi[3]);
-            if (r16 == 0) *reinterpret_cast<float2*>(o + kD) = make_float2(mh, lh);
+            direct_load(0);
+            for (int i = 0; i < npc; ++i) process(i, nullptr, nullptr);
+            __syncthreads();  // the next chunk rewrites the page tables
         }
     }
 }
 
-// Combines the split partials of every multi-split sequence, one workgroup
-// per (sequence, head), one thread per dim:
-// out = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M)   (M = max_s m_s)
-__global__ void __launch_bounds__(kD)
-decode_merge_kernel(void* out, const float* __restrict__ part, const int32_t* __restrict__ seqinfo,
-                    int Hq, int q_bf16) {
-    const int b = blockIdx.x / Hq, h = blockIdx.x % Hq;
-    const int first = seqinfo[2 * b], nsp = seqinfo[2 * b + 1];
-    if (nsp <= 1) return;
-    const int d = threadIdx.x;
-    const float* base = part + ((int64_t)first * Hq + h) * (kD + 2);
-    const int64_t stride = (int64_t)Hq * (kD + 2);
-    float M = kNegInf;
-    for (int s = 0; s < nsp; ++s) M = fmaxf(M, base[s * stride + kD]);
-    const float Mu = M == kNegInf ? 0.0f : M;
-    float acc = 0.0f, lsum = 0.0f;
-    for (int s = 0; s < nsp; ++s) {
-        const float* r = base + s * stride;
-        const float w = exp2f(r[kD] - Mu);
-        lsum = __builtin_fmaf(r[kD + 1], w, lsum);
-        acc = __builtin_fmaf(r[d], w, acc);
+// ------------------------------------------------------------------ merge
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+// Combines the pieces of every sequence that range boundaries cut.  Grid
+// (B, Hkv), one wave per query head of the KV head.  Rows hold D + 2 floats:
+// o unnormalised, m, l (log2 domain); out = sum_s o_s 2^(m_s - M) /
+// sum_s l_s 2^(m_s - M), M = max_s m_s.  Pieces of sequence b: workgroups
+// w0..w1 (those holding its first and last page); w0 wrote slot 2 w0 + 1,
+// later ones slot 2 w.  Sequences without pages get zero rows.
+__global__ void __launch_bounds__(1024) decode_merge_kernel(DecodeParams p) {
+    const int b = blockIdx.x, g = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int hq = g * p.G + wave;
+    __shared__ int sh[3];
+    if (wave == 0) {
+        int carry = 0, ps_b = 0, pg_b = 0;
+        for (int b0 = 0; b0 < p.B; b0 += 64) {
+            int L = 0;
+            const int pg = b0 + lane < p.B ? seq_pages(p, b0 + lane, &L) : 0;
+            const int incl = wave_incl_scan(pg, lane);
+            if (b0 + lane == b) {
+                ps_b = carry + incl - pg;
+                pg_b = pg;
+            }
+            carry += __shfl(incl, 63, 64);
+        }
+        // the lane that held b publishes it
+        if (lane == (b & 63)) {
+            sh[0] = ps_b;
+            sh[1] = pg_b;
+            sh[2] = carry;
+        }
     }
-    const float v = lsum > 0.0f ? acc / lsum : 0.0f;
-    uint16_t* o = reinterpret_cast<uint16_t*>(out) + ((int64_t)b * Hq + h) * kD + d;
-    *o = q_bf16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
+    __syncthreads();
+    const int ps = sh[0], pg = sh[1], T = sh[2];
+    uint16_t* orow = reinterpret_cast<uint16_t*>(p.out) + ((int64_t)b * p.Hq + hq) * kD;
+    if (pg == 0) {
+        reinterpret_cast<uint32_t*>(orow)[lane] = 0u;
+        return;
+    }
+    const int n = effective_wgs(p, T, p.grid);
+    const int w0 = wg_of_page(ps, n, T), w1 = wg_of_page(ps + pg - 1, n, T);
+    if (w0 == w1) return;  // written by its workgroup
+    const int nseg = w1 - w0 + 1;
+    const int64_t rs = (int64_t)p.Hq * (kD + 2);
+    auto row = [&](int s) {  // piece s = workgroup w0 + s
+        const int slot = s == 0 ? 2 * w0 + 1 : 2 * (w0 + s);
+        return p.part + slot * rs + (int64_t)hq * (kD + 2);
+    };
+    float M = kNegInf;
+    for (int s0 = 0; s0 < nseg; s0 += 64)
+        M = fmaxf(M, wave_max(s0 + lane < nseg ? row(s0 + lane)[kD] : kNegInf));
+    const float Mu = M == kNegInf ? 0.0f : M;
+    const int r16 = lane & 15, grp = lane >> 4;
+    float L = 0.0f;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < nseg; s0 += 64) {
+        const int cnt = min(64, nseg - s0);
+        float wt = 0.0f;
+        if (lane < cnt) {
+            const float2 ml = *reinterpret_cast<const float2*>(row(s0 + lane) + kD);
+            wt = __builtin_amdgcn_exp2f(ml.x - Mu);
+            L = __builtin_fmaf(ml.y, wt, L);
+        }
+        // four 16-lane groups take pieces j = grp, grp + 4, ...; four in flight each
+        for (int j0 = 0; j0 < cnt; j0 += 16) {
+            float2 o[4][4];
+            float ws[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int j = j0 + 4 * u + grp;
+                const int jc = min(j, cnt - 1);
+                ws[u] = __shfl(wt, jc, 64);
+                ws[u] = j < cnt ? ws[u] : 0.0f;
+                const float2* r = reinterpret_cast<const float2*>(row(s0 + jc) + 8 * r16);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[u][e] = r[e];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    acc[2 * e] = __builtin_fmaf(o[u][e].x, ws[u], acc[2 * e]);
+                    acc[2 * e + 1] = __builtin_fmaf(o[u][e].y, ws[u], acc[2 * e + 1]);
+                }
+        }
+    }
+    L = wave_sum(L);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = sum_over_groups(acc[e]);
+    if (grp != 0) return;
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    uint32_t w4[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const uint16_t b0 = p.q_bf16 ? f32_to_bf16_bits(acc[2 * e] * inv) : f32_to_f16_bits(acc[2 * e] * inv);
+        const uint16_t b1 = p.q_bf16 ? f32_to_bf16_bits(acc[2 * e + 1] * inv) : f32_to_f16_bits(acc[2 * e + 1] * inv);
+        w4[e] = (uint32_t)b0 | ((uint32_t)b1 << 16);
+    }
+    *reinterpret_cast<u32x4*>(orow + 8 * r16) = u32x4{w4[0], w4[1], w4[2], w4[3]};
 }
 
 // ------------------------------------------------------------------ host
 
-constexpr int kTargetItems = 1024;
 constexpr int kPpsMin = 4;
-constexpr int kDefaultMaxSplits = 64;
 
-// upper bound of the plan's item count: sum_b ceil(pages_b / min(pps, cap))
-// <= target + B (+ B * ceil(max_blocks / cap) when the per-item page cap binds)
-int max_items(int B, int max_blocks) {
-    return kTargetItems + B + B * ((max_blocks + kMaxItemPages - 1) / kMaxItemPages);
+int num_cus() {
+    static std::mutex mu;
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    std::lock_guard<std::mutex> lk(mu);
+    if (!cached[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
 }
 
-size_t workspace_bytes_for(int B, int Hq, int max_blocks) {
-    const size_t seqinfo = ((size_t)B * 2 * sizeof(int32_t) + 255) / 256 * 256;
-    return seqinfo + (size_t)max_items(B, max_blocks) * Hq * (kD + 2) * sizeof(float);
+// Launched workgroups for the flat layout: one resident wave of them (a
+// workgroup of Hkv waves at 2 waves per SIMD), fewer for small batches.
+// Upper bound of the pages: B * max_blocks.
+int flat_grid(int B, int Hkv, int max_blocks, int max_splits, int cus) {
+    const int per_cu = max(1, 8 / Hkv);
+    int64_t n = (int64_t)cus * per_cu;
+    n = std::min<int64_t>(n, ((int64_t)B * max_blocks + kPpsMin - 1) / kPpsMin);
+    if (max_splits > 1) n = std::min<int64_t>(n, (int64_t)B * max_splits);
+    return (int)std::max<int64_t>(1, n);
+}
+
+size_t workspace_bytes_for(int B, int Hq, int Hkv, int max_blocks, int max_splits, int cus) {
+    if (max_splits == 1) return 0;
+    return (size_t)2 * flat_grid(B, Hkv, max_blocks, max_splits, cus) * Hq * (kD + 2) * sizeof(float);
 }
 
 template <int FMT, int KB, int VB, bool MBF16>
 int launch_decode(DecodeParams& prm, size_t lds, hipStream_t stream) {
-    const int items = max_items(prm.B, prm.max_blocks);
     auto kern = paged_decode_kernel<FMT, KB, VB, MBF16>;
     if (lds > 64 * 1024) {
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
             return VMC_EIO;
     }
-    hipLaunchKernelGGL(kern, dim3(items), dim3(64 * prm.Hkv), lds, stream, prm);
+    prm.grid = prm.per_seq ? prm.B : flat_grid(prm.B, prm.Hkv, prm.max_blocks, prm.max_splits, num_cus());
+    hipLaunchKernelGGL(kern, dim3(prm.grid), dim3(64 * prm.Hkv), lds, stream, prm);
     VMC_LAUNCH_CHECK();
-    hipLaunchKernelGGL(decode_merge_kernel, dim3(prm.B * prm.Hq), dim3(kD), 0, stream, prm.out, prm.part,
-                       prm.seqinfo, prm.Hq, prm.q_bf16);
-    VMC_LAUNCH_CHECK();
+    if (!prm.per_seq) {
+        hipLaunchKernelGGL(decode_merge_kernel, dim3(prm.B, prm.Hkv), dim3(64 * prm.G), 0, stream, prm);
+        VMC_LAUNCH_CHECK();
+    }
     return VMC_OK;
 }
 
@@ -741,8 +942,10 @@ int setup_common(DecodeParams& prm, void* out, const void* query, const int32_t*
     if (D != kD || bs != kBs) return VMC_EINVAL;
     if (B < 0 || Hq <= 0 || Hkv <= 0 || Hkv > 8 || Hq % Hkv != 0 || Hq / Hkv > 16) return VMC_EINVAL;
     if (max_blocks <= 0) return VMC_EINVAL;
-    if (B > 0 && (!out || !query || !bt || !seq_lens || !ws)) return VMC_EINVAL;
-    if (ws_bytes < workspace_bytes_for(B, Hq, max_blocks)) return VMC_ENOMEM;
+    if (B > (1 << 24)) return VMC_EINVAL;
+    if (B > 0 && (!out || !query || !bt || !seq_lens)) return VMC_EINVAL;
+    const size_t need = workspace_bytes_for(B, Hq, Hkv, max_blocks, max_splits, num_cus());
+    if (need > 0 && (!ws || ws_bytes < need)) return ws ? VMC_ENOMEM : VMC_EINVAL;
     prm.out = out;
     prm.q = reinterpret_cast<const uint16_t*>(query);
     prm.bt = bt;
@@ -753,12 +956,10 @@ int setup_common(DecodeParams& prm, void* out, const void* query, const int32_t*
     prm.G = Hq / Hkv;
     prm.max_blocks = max_blocks;
     prm.scale_log2 = scale * kLog2e;
-    const size_t seqinfo = ((size_t)B * 2 * sizeof(int32_t) + 255) / 256 * 256;
-    prm.seqinfo = reinterpret_cast<int32_t*>(ws);
-    prm.part = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(ws) + seqinfo);
-    prm.target_items = kTargetItems;
+    prm.part = reinterpret_cast<float*>(ws);
+    prm.per_seq = max_splits == 1;
     prm.pps_min = kPpsMin;
-    prm.max_splits = max_splits > 0 ? max_splits : kDefaultMaxSplits;
+    prm.max_splits = max_splits;
     return VMC_OK;
 }
 
@@ -767,22 +968,22 @@ int setup_common(DecodeParams& prm, void* out, const void* query, const int32_t*
 
 using namespace vmc;
 
-extern "C" size_t vmc_paged_decode_workspace_size(int batch_size, int num_heads, int head_dim,
-                                                  int max_num_blocks_per_req, int block_size,
-                                                  int max_num_kv_splits) {
+extern "C" size_t vmc_paged_decode_workspace_size(int batch_size, int num_heads, int num_kv_heads,
+                                                  int head_dim, int max_num_blocks_per_req,
+                                                  int block_size, int max_num_kv_splits) {
     (void)head_dim;
     (void)block_size;
-    (void)max_num_kv_splits;
-    if (batch_size < 0 || num_heads <= 0) return 0;
-    return workspace_bytes_for(batch_size, num_heads, max_num_blocks_per_req);
+    if (batch_size < 0 || num_heads <= 0 || num_kv_heads <= 0 || max_num_blocks_per_req <= 0) return 0;
+    return workspace_bytes_for(batch_size, num_heads, num_kv_heads, max_num_blocks_per_req,
+                               max_num_kv_splits, num_cus());
 }
 
-extern "C" size_t vmc_turboquant_decode_workspace_size(int batch_size, int num_heads, int head_dim,
-                                                       int64_t max_num_blocks_per_req,
+extern "C" size_t vmc_turboquant_decode_workspace_size(int batch_size, int num_heads, int num_kv_heads,
+                                                       int head_dim, int64_t max_num_blocks_per_req,
                                                        int64_t block_size, int max_num_kv_splits) {
-    return vmc_paged_decode_workspace_size(batch_size, num_heads, head_dim,
-                                           (int)max_num_blocks_per_req, (int)block_size,
-                                           max_num_kv_splits);
+    return vmc_paged_decode_workspace_size(batch_size, num_heads, num_kv_heads, head_dim,
+                                           (int)std::min<int64_t>(max_num_blocks_per_req, 0x7fffffff),
+                                           (int)block_size, max_num_kv_splits);
 }
 
 extern "C" int vmc_paged_attention_decode(void* out, const void* query, const void* key_cache,
@@ -812,8 +1013,6 @@ extern "C" int vmc_paged_attention_decode(void* out, const void* query, const vo
     prm.hnd = layout == VMC_LAYOUT_HND;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     if (kv_format == VMC_KV_Q8_0 || kv_format == VMC_KV_Q4_0) {
-        const int n16 = (int)(2 * prm.page_bytes / 16);
-        (void)n16;
         if ((prm.page_bytes % 16) != 0) return VMC_EINVAL;
     }
     const size_t lds_q = (size_t)4 * prm.page_bytes;  // K+V, double buffered
@@ -856,8 +1055,7 @@ extern "C" int vmc_turboquant_decode_attention(void* output, const void* query, 
     prm.key_packed = cfg->key_packed_size;
     prm.val_data = cfg->val_data_bytes;
     prm.tab = tq_tables(head_dim, cfg->key_quant_bits);
-    if ((prm.page_bytes % 16) != 0)
-        return VMC_EINVAL;
+    if ((prm.page_bytes % 16) != 0) return VMC_EINVAL;
     const size_t lds = (size_t)2 * prm.page_bytes;  // double-buffered page
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int kb = cfg->key_quant_bits, vb = cfg->value_quant_bits;

@@ -48,7 +48,7 @@ void reshape_and_cache(const void* key, const void* value, void* key_cache, void
                        const void* v_scale, ScalarType dtype, hipStream_t stream = nullptr,
                        const std::string& layout = "nhd");
 
-// Single pass over each sequence (no split, no workspace).
+// One pass per sequence (no split, no workspace): one workgroup per request.
 void paged_attention_v1(void* out, const void* query, const void* key_cache,
                         const void* value_cache, const AttentionParams& params,
                         const int32_t* block_tables, const int32_t* seq_lens,
@@ -56,9 +56,10 @@ void paged_attention_v1(void* out, const void* query, const void* key_cache,
                         const void* k_scale, const void* v_scale, hipStream_t stream = nullptr,
                         const std::string& layout = "nhd");
 
-// Split-KV decode.  exp_sums / max_logits are unused (the partial max and sum
-// live next to each partial output); tmp_out is the split workspace and must
-// hold paged_attention_v2_workspace_size(params) bytes.
+// Split-KV decode: the batch's pages are spread evenly over the GPU.
+// exp_sums / max_logits are unused (the partial max and sum live next to each
+// partial output); tmp_out is the split workspace and must hold
+// paged_attention_v2_workspace_size(params) bytes.
 size_t paged_attention_v2_workspace_size(const AttentionParams& params);
 void paged_attention_v2(void* out, void* exp_sums, void* max_logits, void* tmp_out,
                         const void* query, const void* key_cache, const void* value_cache,

@@ -71,7 +71,7 @@ struct TQWorkspace {
     int gpu_device = 0;
 
     // enough for batch_size x num_heads queries over max_num_blocks_per_req pages
-    void ensure_decode(int batch_size, int num_heads, int head_dim,
+    void ensure_decode(int batch_size, int num_heads, int num_kv_heads, int head_dim,
                        int64_t max_num_blocks_per_req, int64_t block_size,
                        int max_num_kv_splits, int gpu_device);
     void free_buf();

@@ -84,14 +84,13 @@ void PagedAttentionBackend::forward_decode(void* output, const void* query, cons
 }
 
 // pre-sizes the split workspace for max_num_seqs requests of up to 32768
-// tokens (longer contexts fall back to the grow-on-demand workspace)
+// tokens (a batch that needs more runs one pass per request, without it)
 void PagedAttentionBackend::ensure_workspace(int max_num_batched_tokens, int max_num_seqs,
                                              int num_attention_heads, int num_kv_heads,
                                              int head_dim, int gpu_device) {
     (void)max_num_batched_tokens;
-    (void)num_kv_heads;
-    const size_t need = vmc_paged_decode_workspace_size(max_num_seqs, num_attention_heads, head_dim,
-                                                        32768 / 16, 16, 0);
+    const size_t need = vmc_paged_decode_workspace_size(max_num_seqs, num_attention_heads, num_kv_heads,
+                                                        head_dim, 32768 / 16, 16, 0);
     if (need <= ws_bytes_) return;
     HIP_CHECK(hipSetDevice(gpu_device));
     if (ws_) HIP_CHECK(hipFree(ws_));
@@ -131,7 +130,7 @@ void TurboQuantBackend::ensure_workspace(int max_num_batched_tokens, int max_num
     num_attention_heads_ = num_attention_heads;
     num_kv_heads_ = num_kv_heads;
     head_dim_ = head_dim;
-    workspace_.ensure_decode(max_num_seqs, num_attention_heads, head_dim, 32768 / 16, 16,
+    workspace_.ensure_decode(max_num_seqs, num_attention_heads, num_kv_heads, head_dim, 32768 / 16, 16,
                              config_.max_num_kv_splits, gpu_device);
 }
 

@@ -136,12 +136,13 @@ void TQBuffers::free_buf() {
     initialized = false;
 }
 
-void TQWorkspace::ensure_decode(int batch_size, int num_heads, int head_dim,
+void TQWorkspace::ensure_decode(int batch_size, int num_heads, int num_kv_heads, int head_dim,
                                 int64_t max_num_blocks_per_req, int64_t block_size,
                                 int max_num_kv_splits, int device) {
-    const size_t need = vmc_turboquant_decode_workspace_size(
-        batch_size, num_heads, head_dim, max_num_blocks_per_req, block_size, max_num_kv_splits);
-    if (need <= decode_bytes && decode_workspace) return;
+    const size_t need = vmc_turboquant_decode_workspace_size(batch_size, num_heads, num_kv_heads,
+                                                             head_dim, max_num_blocks_per_req,
+                                                             block_size, max_num_kv_splits);
+    if (need <= decode_bytes) return;
     HIP_CHECK(hipSetDevice(device));
     if (decode_workspace) HIP_CHECK(hipFree(decode_workspace));
     decode_workspace = nullptr;
@@ -180,8 +181,8 @@ void turboquant_decode_attention(void* output, const void* query, const void* kv
     if (config.key_fp8) throw std::runtime_error("turboquant_k8v4 (fp8 keys) is not implemented");
     int dev = 0;
     HIP_CHECK(hipGetDevice(&dev));
-    workspace.ensure_decode(batch_size, num_heads, head_dim, max_num_blocks_per_req, block_size,
-                            max_num_kv_splits, dev);
+    workspace.ensure_decode(batch_size, num_heads, num_kv_heads, head_dim, max_num_blocks_per_req,
+                            block_size, max_num_kv_splits, dev);
     const vmc_tq_config c = config.to_c();
     VMC_CALL(vmc_turboquant_decode_attention(
         output, query, kv_cache, block_tables, seq_lens, batch_size, num_heads, num_kv_heads,
@@ -217,34 +218,6 @@ void reshape_and_cache(const void* key, const void* value, void* key_cache, void
 }
 
 namespace {
-// grow-only split workspace per device for paged_attention_v1 (which has no
-// workspace argument); allocation happens only when a call needs more
-struct DeviceWorkspace {
-    void* ptr = nullptr;
-    size_t bytes = 0;
-};
-std::mutex g_ws_mu;
-std::map<int, DeviceWorkspace> g_ws;
-
-void* v1_workspace(size_t need, size_t* have) {
-    int dev = 0;
-    HIP_CHECK(hipGetDevice(&dev));
-    std::lock_guard<std::mutex> lk(g_ws_mu);
-    DeviceWorkspace& w = g_ws[dev];
-    if (w.bytes < need) {
-        if (w.ptr) {
-            HIP_CHECK(hipDeviceSynchronize());
-            HIP_CHECK(hipFree(w.ptr));
-        }
-        w.ptr = nullptr;
-        w.bytes = 0;
-        HIP_CHECK(hipMalloc(&w.ptr, need));
-        w.bytes = need;
-    }
-    *have = w.bytes;
-    return w.ptr;
-}
-
 void check_params(const AttentionParams& p, const float* alibi_slopes) {
     if (alibi_slopes) throw std::runtime_error("paged attention: ALiBi is not supported");
     if (p.blocksparse_vert_stride > 1 || p.blocksparse_local_blocks > 0)
@@ -253,7 +226,7 @@ void check_params(const AttentionParams& p, const float* alibi_slopes) {
 }  // namespace
 
 size_t paged_attention_v2_workspace_size(const AttentionParams& p) {
-    return vmc_paged_decode_workspace_size(p.batch_size, p.num_heads, p.head_dim,
+    return vmc_paged_decode_workspace_size(p.batch_size, p.num_heads, p.num_kv_heads, p.head_dim,
                                            p.max_num_blocks_per_req, p.block_size, 0);
 }
 
@@ -265,13 +238,12 @@ void paged_attention_v1(void* out, const void* query, const void* key_cache,
                         const std::string& layout) {
     check_params(p, alibi_slopes);
     if (k_scale || v_scale) throw std::runtime_error("paged attention: fp8 k/v scales are not supported");
-    size_t have = 0;
-    void* ws = v1_workspace(paged_attention_v2_workspace_size(p), &have);
+    // one pass per sequence: no split, no workspace
     VMC_CALL(vmc_paged_attention_decode(out, query, key_cache, value_cache, block_tables, seq_lens,
                                         p.batch_size, p.num_heads, p.num_kv_heads, p.head_dim,
                                         p.block_size, p.max_num_blocks_per_req, p.scale,
                                         vmc_dtype_of(p.dtype), vmc_kv_format_of(kv_cache_dtype, p.dtype),
-                                        vmc_layout_of(layout), 0, ws, have, stream));
+                                        vmc_layout_of(layout), 1, nullptr, 0, stream));
 }
 
 void paged_attention_v2(void* out, void* exp_sums, void* max_logits, void* tmp_out,
