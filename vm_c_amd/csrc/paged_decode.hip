@@ -63,16 +63,38 @@ __device__ __forceinline__ void static_for(F&& f) {
     static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// Register staging of LDS-staged formats: SPP 16-byte chunks per thread per
-// page (= ceil(bytes per token-head / 64) for one wave per KV head) and PF
-// pages in flight per workgroup.
+// Compile-time geometry of a page format (head_dim 128, block 16, at most 8
+// KV heads): TurboQuant slot fields (kernels_turboquant.h:29-45), GGUF entry
+// sizes, and the register staging of LDS-staged formats -- SPP 16-byte
+// chunks per thread per page (one wave per KV head) and PF pages in flight,
+// each with its own LDS buffer of kBuf bytes (K page, then V page at kHalf).
 template <int FMT, int KB, int VB>
-struct StagePlan {
-    static constexpr int entry = FMT == FMT_TQ ? (16 * KB + 2 + 16 * VB + 4 + 1) / 2 * 2
-                                 : FMT == FMT_Q8_0 ? 2 * 136 : FMT == FMT_Q4_0 ? 2 * 72 : 0;
-    static constexpr int spp = entry > 0 ? (entry + 63) / 64 : 1;
-    static constexpr int pf = entry == 0 ? 1 : (spp <= 2 ? 4 : (spp <= 3 ? 3 : 2));
+struct Geo {
+    static constexpr int mse = 16 * KB, key_packed = mse + 2, val_data = 16 * VB;
+    static constexpr int entry = FMT == FMT_TQ ? (key_packed + val_data + 4 + 1) / 2 * 2
+                                 : FMT == FMT_Q8_0 ? 136 : FMT == FMT_Q4_0 ? 72 : 256;
+    static constexpr int per_thread = FMT == FMT_TQ ? entry : 2 * entry;  // staged bytes per token-head
+    static constexpr bool staged = FMT >= FMT_Q8_0;
+    static constexpr int spp = staged ? (per_thread + 63) / 64 : 1;
+    static constexpr int pf = !staged ? 1 : (spp <= 2 ? 4 : (spp <= 3 ? 3 : 2));
+    static constexpr int kHalf = kBs * 8 * entry;                    // one cache's page, 8 heads
+    static constexpr int kBuf = FMT == FMT_TQ ? kHalf : 2 * kHalf;  // one LDS buffer
 };
+
+// Scale of PV chunk c's accumulator: TurboQuant V codes enter the MFMA as the
+// fp16 subnormals c * 2^-24 (4-bit odd chunks keep the nibble at bit 4:
+// c * 2^-20), other formats as values.
+template <int FMT, int VB>
+__device__ __forceinline__ constexpr float kVScale(int c) {
+    return FMT != FMT_TQ ? 1.0f : (VB == 4 && (c & 1)) ? 1048576.0f : 16777216.0f;
+}
+
+// fmax without the NaN-quieting the IEEE mode adds around fmaxf
+__device__ __forceinline__ float vmax(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
 
 struct DecodeParams {
     void* out;
@@ -274,10 +296,17 @@ paged_decode_kernel(DecodeParams p) {
         return;
     }
 
-    // static LDS: the LUT's address is a compile-time offset of each read
+    // static LDS: the LUTs' addresses are compile-time offsets of each read.
+    // 3-bit keys: a 12-bit LUT of four packed fp16 centroids per entry.
     __shared__ uint32_t lut[FMT == FMT_TQ ? 256 : 1];
-    uint8_t* pagebuf = smem;
-    if constexpr (FMT == FMT_TQ) build_pair_lut<KB>(lut, p.tab);
+    __shared__ u32x2 lut4[FMT == FMT_TQ && KB == 3 ? 4096 : 1];
+    if constexpr (FMT == FMT_TQ) {
+        build_pair_lut<KB>(lut, p.tab);
+        if constexpr (KB == 3) {
+            __syncthreads();
+            for (int e = tid; e < 4096; e += blockDim.x) lut4[e] = u32x2{lut[e & 63], lut[e >> 6]};
+        }
+    }
 
     // ---- Q operand: lane (r16 = head, grp) holds dims 32*grp + 8*j + e, j = MFMA index
     AT qb[4];
@@ -363,7 +392,7 @@ paged_decode_kernel(DecodeParams p) {
     reset_state();
     int cur_b = -1;
 
-    const int Hkv = p.Hkv, E = p.entry_bytes, hnd = p.hnd;
+    const int Hkv = p.Hkv, hnd = p.hnd;
     const int64_t page_bytes = p.page_bytes;
     const int nthreads = blockDim.x;
 
@@ -391,8 +420,8 @@ paged_decode_kernel(DecodeParams p) {
                 uint32_t wd[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const float v0 = (oacc[2 * e][i] + zh) * inv;
-                    const float v1 = (oacc[2 * e + 1][i] + zh) * inv;
+                    const float v0 = __builtin_fmaf(oacc[2 * e][i], kVScale<FMT, VB>(2 * e), zh) * inv;
+                    const float v1 = __builtin_fmaf(oacc[2 * e + 1][i], kVScale<FMT, VB>(2 * e + 1), zh) * inv;
                     const uint16_t b0 = p.q_bf16 ? f32_to_bf16_bits(v0) : f32_to_f16_bits(v0);
                     const uint16_t b1 = p.q_bf16 ? f32_to_bf16_bits(v1) : f32_to_f16_bits(v1);
                     wd[e] = (uint32_t)b0 | ((uint32_t)b1 << 16);
@@ -403,10 +432,11 @@ paged_decode_kernel(DecodeParams p) {
                 float* o = p.part + ((int64_t)slot * p.Hq + hq) * (kD + 2);
                 // (D + 2) floats per row: 8-byte aligned only, store as float2
                 float* od = o + 8 * r16;
-                *reinterpret_cast<float2*>(od + 0) = make_float2(oacc[0][i] + zh, oacc[1][i] + zh);
-                *reinterpret_cast<float2*>(od + 2) = make_float2(oacc[2][i] + zh, oacc[3][i] + zh);
-                *reinterpret_cast<float2*>(od + 4) = make_float2(oacc[4][i] + zh, oacc[5][i] + zh);
-                *reinterpret_cast<float2*>(od + 6) = make_float2(oacc[6][i] + zh, oacc[7][i] + zh);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    *reinterpret_cast<float2*>(od + 2 * e) =
+                        make_float2(__builtin_fmaf(oacc[2 * e][i], kVScale<FMT, VB>(2 * e), zh),
+                                    __builtin_fmaf(oacc[2 * e + 1][i], kVScale<FMT, VB>(2 * e + 1), zh));
                 if (r16 == 0) *reinterpret_cast<float2*>(o + kD) = make_float2(mh, lh);
             }
         }
@@ -414,11 +444,10 @@ paged_decode_kernel(DecodeParams p) {
     };
 
     // staged formats: PF pages in flight in registers -> LDS double buffer
-    using SP = StagePlan<FMT, KB, VB>;
-    constexpr int SPP = SP::spp, PF = SP::pf;
+    using GE = Geo<FMT, KB, VB>;
+    constexpr int SPP = GE::spp, PF = GE::pf;
     const int n16_k = (int)(page_bytes / 16);
     const int n16 = (FMT == FMT_TQ) ? n16_k : 2 * n16_k;
-    const int lds_page = (FMT == FMT_TQ) ? (int)page_bytes : 2 * (int)page_bytes;
     u32x4 stage[PF][SPP];
     auto stage_load = [&](auto slot_c, int i) __attribute__((always_inline)) {
         constexpr int S = decltype(slot_c)::value;
@@ -435,15 +464,25 @@ paged_decode_kernel(DecodeParams p) {
             stage[S][c] = *src;
         }
     };
-    auto stage_store = [&](auto slot_c, uint8_t* dstb) __attribute__((always_inline)) {
+    // slot S of the register ring goes to LDS buffer S (V half at kHalf)
+    auto stage_store = [&](auto slot_c) __attribute__((always_inline)) {
         constexpr int S = decltype(slot_c)::value;
-        u32x4* dst = reinterpret_cast<u32x4*>(dstb);
+        uint8_t* buf = smem + S * GE::kBuf;
 #pragma unroll
         for (int c = 0; c < SPP; ++c) {
             const int idx = tid + c * nthreads;
-            if (idx < n16) dst[idx] = stage[S][c];
+            const int off = (FMT == FMT_TQ || idx < n16_k) ? 16 * idx : GE::kHalf + 16 * (idx - n16_k);
+            if (idx < n16) *reinterpret_cast<u32x4*>(buf + off) = stage[S][c];
         }
     };
+
+    // loop-invariant LDS offsets of this lane's entries inside a page
+    // (staged in LDS, or in HBM for f16/bf16):
+    // K of token r16, V of tokens 4*grp + i
+    const int k_off = entry_off<FMT>(r16, g, Hkv, GE::entry, hnd);
+    int v_off[4];
+#pragma unroll
+    for (int i2 = 0; i2 < 4; ++i2) v_off[i2] = entry_off<FMT>(4 * grp + i2, g, Hkv, GE::entry, hnd);
 
     // direct formats: per-lane operand registers for one page
     u32x4 kreg[4], vreg[4];
@@ -459,7 +498,7 @@ paged_decode_kernel(DecodeParams p) {
         const uint8_t* kp = p.kc + (int64_t)blk * page_bytes;
         const uint8_t* vp = p.vc + (int64_t)blk * page_bytes;
         if (r16 < nv) {
-            const u32x4* src = reinterpret_cast<const u32x4*>(kp + entry_off<FMT>(r16, g, Hkv, E, hnd) + 64 * grp);
+            const u32x4* src = reinterpret_cast<const u32x4*>(kp + k_off + 64 * grp);
 #pragma unroll
             for (int c = 0; c < 4; ++c) kreg[c] = src[c];
         }
@@ -467,12 +506,15 @@ paged_decode_kernel(DecodeParams p) {
         for (int i2 = 0; i2 < 4; ++i2) {
             const int tok = 4 * grp + i2;
             if (tok < nv)
-                vreg[i2] = *reinterpret_cast<const u32x4*>(vp + entry_off<FMT>(tok, g, Hkv, E, hnd) + 16 * r16);
+                vreg[i2] = *reinterpret_cast<const u32x4*>(vp + v_off[i2] + 16 * r16);
         }
     };
 
     int npc = 0;  // pages of the current chunk
-    auto process = [&](int i, const uint8_t* kpage, const uint8_t* vpage) __attribute__((always_inline)) {
+    auto process = [&](int i, auto buf_c) __attribute__((always_inline)) {
+        constexpr int BUF = decltype(buf_c)::value;
+        const uint8_t* kpage = smem + BUF * GE::kBuf;
+        const uint8_t* vpage = kpage + GE::kHalf;
         const int info = __builtin_amdgcn_readfirstlane(info_lds[i]);
         const int b = info >> 6;
         const int nv = (info >> 1) & 31;  // valid tokens in this page
@@ -489,7 +531,7 @@ paged_decode_kernel(DecodeParams p) {
 
         if constexpr (kStaged) {
             // ---- K operand for token r16
-            const uint8_t* ke = kpage + entry_off<FMT>(r16, g, Hkv, E, hnd);
+            const uint8_t* ke = kpage + k_off;
             if constexpr (FMT == FMT_TQ) {
                 // K: lane group grp owns dims 32*grp .. +31 of token r16; each
                 // code pair indexes the LUT of packed fp16 centroid pairs.
@@ -510,28 +552,30 @@ paged_decode_kernel(DecodeParams p) {
                     const uint32_t g24[4] = {h[0] | ((h[1] & 0xffu) << 16), (h[1] >> 8) | (h[2] << 8),
                                              h[3] | ((h[4] & 0xffu) << 16), (h[4] >> 8) | (h[5] << 8)};
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) aw[j][e] = lut[(g24[j] >> (6 * e)) & 63u];
+                    for (int j = 0; j < 4; ++j) {
+                        const u32x2 lo = lut4[g24[j] & 0xfffu], hi = lut4[g24[j] >> 12];
+                        aw[j] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+                    }
                 }
-                // sum of squared centroids (one mixed-precision fma per value;
-                // v_dot2 with a squared operand gave wrong sums on this toolchain)
-                float csq = 0.0f;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    a[j] = __builtin_bit_cast(AT, aw[j]);
+                for (int j = 0; j < 4; ++j) a[j] = __builtin_bit_cast(AT, aw[j]);
+                // ||C[codes]||^2 of every token: the diagonal of the Gram matrix
+                // K K^T (the A operand doubles as the B operand; fp16 products
+                // are exact, sums fp32).  Token r16's value sits in the lanes
+                // with grp == r16 / 4, element r16 % 4.
+                f32x4 gram = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) csq = __builtin_fmaf((float)a[j][e], (float)a[j][e], csq);
-                }
-                csq = sum_over_groups(csq);
-                const float nrm = f16_bits_to_f32((uint16_t)lds16(ke + p.mse_bytes));
+                for (int j = 0; j < 4; ++j) gram = mfma16x16x32(a[j], a[j], gram);
+                const int di = r16 & 3;
+                const float csq = di == 0 ? gram[0] : di == 1 ? gram[1] : di == 2 ? gram[2] : gram[3];
+                const float nrm = f16_bits_to_f32((uint16_t)lds16(ke + GE::mse));
                 rowf = p.scale_log2 * nrm * __builtin_amdgcn_rsqf(csq + 1e-16f);
                 // V: codes of tokens 4*grp + i, dims 8*r16 .. +7, scale and zero
                 uint32_t cw[4];
 #pragma unroll
                 for (int i2 = 0; i2 < 4; ++i2) {
                     const int tok = 4 * grp + i2;
-                    const uint8_t* ve = kpage + entry_off<FMT>(tok, g, Hkv, E, hnd) + p.key_packed;
+                    const uint8_t* ve = kpage + v_off[i2] + GE::key_packed;
                     if constexpr (VB == 4) {
                         cw[i2] = lds16(ve + 4 * r16) | (lds16(ve + 4 * r16 + 2) << 16);
                     } else {
@@ -541,29 +585,40 @@ paged_decode_kernel(DecodeParams p) {
                         const uint32_t wv = lds16(al2) | (lds16(al2 + 2) << 16);
                         cw[i2] = (wv >> (8 * (r16 & 1))) & 0xffffffu;
                     }
-                    const bool ok = tok < nv;
-                    vsc[i2] = ok ? f16_bits_to_f32((uint16_t)lds16(ve + p.val_data)) : 0.0f;
-                    vzr[i2] = ok ? f16_bits_to_f32((uint16_t)lds16(ve + p.val_data + 2)) : 0.0f;
+                    vsc[i2] = f16_bits_to_f32((uint16_t)lds16(ve + GE::val_data));
+                    vzr[i2] = f16_bits_to_f32((uint16_t)lds16(ve + GE::val_data + 2));
                 }
-                // B operands {token a, token b} per dim, exact fp16 codes via 1024 + c
+                if (nv < kBs) {  // tokens past the end may hold anything
 #pragma unroll
-                for (int c = 0; c < 8; ++c) {
+                    for (int i2 = 0; i2 < 4; ++i2) {
+                        const bool ok = 4 * grp + i2 < nv;
+                        vsc[i2] = ok ? vsc[i2] : 0.0f;
+                        vzr[i2] = ok ? vzr[i2] : 0.0f;
+                    }
+                }
+                // B operands {token a, token b} per dim: the integer code c as
+                // the fp16 subnormal c * 2^-24 (its bit pattern is c), so one
+                // mask per dim after a byte permute that puts both tokens'
+                // code fields in one dword; finalize scales O back (kVScale).
 #pragma unroll
-                    for (int hh = 0; hh < 2; ++hh) {
-                        uint32_t x;
+                for (int hh = 0; hh < 2; ++hh) {
+                    const uint32_t A = cw[2 * hh], Bw = cw[2 * hh + 1];
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) {
                         if constexpr (VB == 4) {
-                            const uint32_t t = __builtin_amdgcn_perm(cw[2 * hh + 1], cw[2 * hh],
+                            // byte c/2 of each token at bits 0 and 16; odd c keeps its
+                            // high nibble in place (c * 16 * 2^-24)
+                            const uint32_t t = __builtin_amdgcn_perm(Bw, A,
                                                                      (uint32_t)(c >> 1) | 0x0c00u |
                                                                          ((uint32_t)(4 + (c >> 1)) << 16) | 0x0c000000u);
-                            x = (c & 1) ? (t >> 4) : t;
-                            x = (x & 0x000f000fu) | 0x64006400u;
+                            bop[c][hh] = t & ((c & 1) ? 0x00f000f0u : 0x000f000fu);
                         } else {
-                            const uint32_t c0 = (cw[2 * hh] >> (3 * c)) & 7u;
-                            const uint32_t c1 = (cw[2 * hh + 1] >> (3 * c)) & 7u;
-                            x = (c0 | (c1 << 16)) | 0x64006400u;
+                            // codes 0-3 sit in bits 0-11 of each token, codes 4-7 in 12-23
+                            const uint32_t q = c < 4 ? __builtin_amdgcn_perm(Bw, A, 0x05040100u)
+                                                     : __builtin_amdgcn_perm(Bw, A, 0x06050201u);
+                            const int sh = c < 4 ? 3 * c : 3 * c - 8;
+                            bop[c][hh] = (q >> sh) & 0x00070007u;
                         }
-                        const f16x2 v2 = __builtin_bit_cast(f16x2, x) - f16x2{(_Float16)1024.0f, (_Float16)1024.0f};
-                        bop[c][hh] = __builtin_bit_cast(uint32_t, v2);
                     }
                 }
             } else {
@@ -596,7 +651,7 @@ paged_decode_kernel(DecodeParams p) {
                 for (int i2 = 0; i2 < 4; ++i2) {
                     const int tok = 4 * grp + i2;
                     const bool ok = tok < nv;
-                    const uint8_t* vb = vpage + entry_off<FMT>(tok, g, Hkv, E, hnd) + BE * (r16 >> 2);
+                    const uint8_t* vb = vpage + v_off[i2] + BE * (r16 >> 2);
                     const float dv = ok ? f16_bits_to_f32((uint16_t)lds16(vb)) : 0.0f;
                     const int q0 = 8 * (r16 & 3);  // index inside the block
 #pragma unroll
@@ -648,14 +703,15 @@ paged_decode_kernel(DecodeParams p) {
         for (int j = 0; j < 4; ++j) sacc = mfma16x16x32(a[j], qb[j], sacc);
 
         f32x4 rf = {rowf, rowf, rowf, rowf};
-        if constexpr (FMT == FMT_TQ) rf = gather4_from_row0(rowf, wscr, r16, grp);
+        if constexpr (FMT == FMT_TQ) rf = gather4_from_diag(rowf, wscr, r16, grp);
         float sv[4];
 #pragma unroll
-        for (int i2 = 0; i2 < 4; ++i2) {
-            const int tok = 4 * grp + i2;
-            sv[i2] = tok < nv ? sacc[i2] * rf[i2] : kNegInf;
+        for (int i2 = 0; i2 < 4; ++i2) sv[i2] = sacc[i2] * rf[i2];
+        if (nv < kBs) {
+#pragma unroll
+            for (int i2 = 0; i2 < 4; ++i2) sv[i2] = 4 * grp + i2 < nv ? sv[i2] : kNegInf;
         }
-        float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+        float mx = vmax(vmax(sv[0], sv[1]), vmax(sv[2], sv[3]));
         mx = max_over_groups(mx);
         // Lazy reference max: m_run moves only when a head's max exceeds it by
         // more than 8 (log2 units), so p <= 256 and most pages skip the O
@@ -748,25 +804,21 @@ paged_decode_kernel(DecodeParams p) {
             static_for<PF>([&](auto sc) __attribute__((always_inline)) {
                 stage_load(sc, min((int)decltype(sc)::value, npc - 1));
             });
-            stage_store(std::integral_constant<int, 0>{}, pagebuf);
+            stage_store(std::integral_constant<int, 0>{});
             __syncthreads();
             for (int base = 0; base < npc; base += PF) {
                 static_for<PF>([&](auto sc) __attribute__((always_inline)) {
                     constexpr int S = decltype(sc)::value;
                     const int i = base + S;
-                    const int cur = i & 1;
-                    if (i < npc) {  // uniform over the workgroup
-                        const uint8_t* kp = pagebuf + cur * lds_page;
-                        process(i, kp, kp + page_bytes);
-                    }
+                    if (i < npc) process(i, sc);  // uniform over the workgroup
                     stage_load(sc, min(i + PF, npc - 1));
-                    stage_store(std::integral_constant<int, (S + 1) % PF>{}, pagebuf + (cur ^ 1) * lds_page);
+                    stage_store(std::integral_constant<int, (S + 1) % PF>{});
                     __syncthreads();
                 });
             }
         } else {
             direct_load(0);
-            for (int i = 0; i < npc; ++i) process(i, nullptr, nullptr);
+            for (int i = 0; i < npc; ++i) process(i, std::integral_constant<int, 0>{});
             __syncthreads();  // the next chunk rewrites the page tables
         }
     }
@@ -919,7 +971,14 @@ size_t workspace_bytes_for(int B, int Hq, int Hkv, int max_blocks, int max_split
 }
 
 template <int FMT, int KB, int VB, bool MBF16>
-int launch_decode(DecodeParams& prm, size_t lds, hipStream_t stream) {
+int launch_decode(DecodeParams& prm, hipStream_t stream) {
+    using GE = Geo<FMT, KB, VB>;
+    // the compile-time geometry must be the one the caller described
+    if (prm.entry_bytes != GE::entry || (FMT == FMT_TQ && (prm.mse_bytes != GE::mse ||
+                                                           prm.key_packed != GE::key_packed ||
+                                                           prm.val_data != GE::val_data)))
+        return VMC_EINVAL;
+    const size_t lds = GE::staged ? (size_t)GE::pf * GE::kBuf : 0;
     auto kern = paged_decode_kernel<FMT, KB, VB, MBF16>;
     if (lds > 64 * 1024) {
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -1015,12 +1074,11 @@ extern "C" int vmc_paged_attention_decode(void* out, const void* query, const vo
     if (kv_format == VMC_KV_Q8_0 || kv_format == VMC_KV_Q4_0) {
         if ((prm.page_bytes % 16) != 0) return VMC_EINVAL;
     }
-    const size_t lds_q = (size_t)4 * prm.page_bytes;  // K+V, double buffered
     switch (kv_format) {
-        case VMC_KV_F16: return launch_decode<FMT_F16, 0, 0, false>(prm, 0, s);
-        case VMC_KV_BF16: return launch_decode<FMT_BF16, 0, 0, true>(prm, 0, s);
-        case VMC_KV_Q8_0: return launch_decode<FMT_Q8_0, 0, 0, false>(prm, lds_q, s);
-        case VMC_KV_Q4_0: return launch_decode<FMT_Q4_0, 0, 0, false>(prm, lds_q, s);
+        case VMC_KV_F16: return launch_decode<FMT_F16, 0, 0, false>(prm, s);
+        case VMC_KV_BF16: return launch_decode<FMT_BF16, 0, 0, true>(prm, s);
+        case VMC_KV_Q8_0: return launch_decode<FMT_Q8_0, 0, 0, false>(prm, s);
+        case VMC_KV_Q4_0: return launch_decode<FMT_Q4_0, 0, 0, false>(prm, s);
         default: return VMC_EINVAL;
     }
 }
@@ -1056,11 +1114,10 @@ extern "C" int vmc_turboquant_decode_attention(void* output, const void* query, 
     prm.val_data = cfg->val_data_bytes;
     prm.tab = tq_tables(head_dim, cfg->key_quant_bits);
     if ((prm.page_bytes % 16) != 0) return VMC_EINVAL;
-    const size_t lds = (size_t)2 * prm.page_bytes;  // double-buffered page
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int kb = cfg->key_quant_bits, vb = cfg->value_quant_bits;
-    if (kb == 4 && vb == 4) return launch_decode<FMT_TQ, 4, 4, false>(prm, lds, s);
-    if (kb == 3 && vb == 3) return launch_decode<FMT_TQ, 3, 3, false>(prm, lds, s);
-    if (kb == 3 && vb == 4) return launch_decode<FMT_TQ, 3, 4, false>(prm, lds, s);
+    if (kb == 4 && vb == 4) return launch_decode<FMT_TQ, 4, 4, false>(prm, s);
+    if (kb == 3 && vb == 3) return launch_decode<FMT_TQ, 3, 3, false>(prm, s);
+    if (kb == 3 && vb == 4) return launch_decode<FMT_TQ, 3, 4, false>(prm, s);
     return VMC_EINVAL;
 }

@@ -1,7 +1,7 @@
 // selftest.hip -- device check of the lane-level assumptions the kernels rely
-// on: cross-row reductions, the wave-private LDS gather, and the operand /
+// on: cross-row reductions, the wave-private LDS gathers, the operand /
 // result layouts of the MFMA shapes used (16x16x32 f16/bf16, 16x16x16 f16,
-// 32x32x16 f16/bf16).  One wave, fixed small integer inputs (exact in every
+// 32x32x16 f16/bf16), and exact fp16 subnormal operands in the 16x16x16 MFMA.  One wave, fixed small integer inputs (exact in every
 // format), every lane compares its own results with the expected values.
 #include "vmc_common.hpp"
 
@@ -10,7 +10,8 @@ namespace {
 
 enum {
     kSumGroups = 1, kMaxGroups = 2, kGather = 4, kMfma16x32 = 8, kMfma16x16 = 16,
-    kMfma32x16 = 32, kMfma16x32bf = 64, kMfma32x16bf = 128
+    kMfma32x16 = 32, kMfma16x32bf = 64, kMfma32x16bf = 128, kMfma16x16Subnormal = 256,
+    kGatherDiag = 512
 };
 
 // A[i][k] = (i + 2k) % 5 - 2, B[k][j] = (3k + j) % 7 - 3 (all exact)
@@ -30,6 +31,12 @@ __global__ void __launch_bounds__(64) selftest_kernel(int* fail) {
         const f32x4 g = gather4_from_row0((float)(100 + l), sc, r16, grp);
         for (int i = 0; i < 4; ++i)
             if (g[i] != (float)(100 + 4 * grp + i)) bad |= kGather;
+        // diagonal lanes (grp == r16 / 4) publish row r16
+        const f32x4 gd = gather4_from_diag((float)(200 + 16 * grp + r16), sc, r16, grp);
+        for (int i = 0; i < 4; ++i) {
+            const int row = 4 * grp + i;
+            if (gd[i] != (float)(200 + 16 * (row >> 2) + row)) bad |= kGatherDiag;
+        }
     }
     // 16x16x32 f16: A lane (row l%16, k = 8*(l/16) + e), D rows 4*(l/16)+i, col l%16
     {
@@ -64,6 +71,19 @@ __global__ void __launch_bounds__(64) selftest_kernel(int* fail) {
             float ref = 0.0f;
             for (int k = 0; k < 16; ++k) ref += Aval(4 * grp + i, k) * Bval(k, r16);
             if (d[i] != ref) bad |= kMfma16x16;
+        }
+        // B given as fp16 subnormals (integer codes c as c * 2^-24): the
+        // products and sums must stay exact, i.e. the unit does not flush them
+        f16x4 bs;
+        for (int e = 0; e < 4; ++e) {
+            const int k = 4 * grp + e;
+            bs[e] = __builtin_bit_cast(_Float16, (uint16_t)((3 * k + r16) % 8));
+        }
+        const f32x4 ds = mfma16x16x16(a, bs, f32x4{0.f, 0.f, 0.f, 0.f});
+        for (int i = 0; i < 4; ++i) {
+            float ref = 0.0f;
+            for (int k = 0; k < 16; ++k) ref += Aval(4 * grp + i, k) * (float)((3 * k + r16) % 8);
+            if (ds[i] * 16777216.0f != ref) bad |= kMfma16x16Subnormal;
         }
     }
     // 32x32x16: A lane (row l%32, k = 8*(l/32) + e), D col l%32, rows 8*(v/4) + 4*(l/32) + v%4

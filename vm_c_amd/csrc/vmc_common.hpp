@@ -5,7 +5,7 @@
 //   A[i][k] : lane l holds row i = l % 16, k = kpl*(l / 16) .. + kpl-1
 //   B[k][j] : lane l holds col j = l % 16, k = kpl*(l / 16) .. + kpl-1
 //   D[i][j] : lane l holds col j = l % 16, rows i = 4*(l / 16) .. + 3
-// (checked on the device by the MFMA layout self-test, vmc_selftest_mfma).
+// (checked on the device by the layout self-test, vmc_selftest).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -105,6 +105,19 @@ __device__ __forceinline__ float max_over_groups(float v) {
 // reads back the four values v[4*(l/16) .. +3] (one 16-byte LDS read).
 __device__ __forceinline__ f32x4 gather4_from_row0(float v, float* sc, int r16, int grp) {
     if (grp == 0) sc[r16] = v;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const f32x4 r = *reinterpret_cast<const f32x4*>(sc + 4 * grp);
+    __builtin_amdgcn_wave_barrier();
+    return r;
+}
+
+// Wave-private LDS exchange from the diagonal of a 16x16 D-layout tile: the
+// lane holding row r16 of column r16 (grp == r16 / 4) publishes v for row
+// r16; every lane reads back rows 4*grp .. +3 (one 16-byte LDS read).
+__device__ __forceinline__ f32x4 gather4_from_diag(float v, float* sc, int r16, int grp) {
+    if ((r16 >> 2) == grp) sc[r16] = v;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
