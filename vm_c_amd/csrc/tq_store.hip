@@ -6,8 +6,8 @@
 //   normalize_kernel          :163-175   x = k * (1/(norm + 1e-8f))
 //   cublasSgemm               :841-848   y = H x
 //   tq_store_mse_kernel       :247-351   codes, norm, V min/max codes, scale, zero
-// Here one thread owns one (token, kv-head) vector end to end with the vector
-// in VGPRs: the norm keeps the reference's sequential fmaf order, y = H x is a
+// Here 16 lanes own one (token, kv-head) vector end to end, 8 dims each in
+// VGPRs: the norm keeps the reference's sequential fmaf order, y = H x is a
 // Walsh-Hadamard transform (butterflies of half-width 1..d/2, then one multiply
 // by the reference matrix scale 1/sqrtf(d)) -- the declared rotation order the
 // CPU oracle shares -- and the codebook index is the count of midpoints <= y,
@@ -19,124 +19,155 @@
 namespace vmc {
 namespace {
 
-template <int D, bool BF16>
-__device__ __forceinline__ void load_vec(const uint16_t* src, float* x) {
-    const u32x4* p = reinterpret_cast<const u32x4*>(src);
+// One 16-lane group per (token, kv head) vector; lane j owns dims 8j .. 8j+7
+// (16 contiguous bytes of K and of V), a wave holds 4 vectors.
+constexpr int kDims = 8;
+constexpr int kGroup = 16;
+
+template <bool BF16>
+__device__ __forceinline__ void load8(const uint16_t* src, float* x) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(src);
 #pragma unroll
-    for (int c = 0; c < D / 8; ++c) {
-        const u32x4 w = p[c];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            x[8 * c + 2 * e] = half_to_f32<BF16>((uint16_t)(w[e] & 0xffffu));
-            x[8 * c + 2 * e + 1] = half_to_f32<BF16>((uint16_t)(w[e] >> 16));
-        }
+    for (int e = 0; e < 4; ++e) {
+        x[2 * e] = half_to_f32<BF16>((uint16_t)(w[e] & 0xffffu));
+        x[2 * e + 1] = half_to_f32<BF16>((uint16_t)(w[e] >> 16));
     }
 }
 
-template <int D>
-__device__ __forceinline__ void fwht(float* y) {
-#pragma unroll
-    for (int h = 1; h < D; h <<= 1) {
-#pragma unroll
-        for (int i = 0; i < D; i += 2 * h) {
-#pragma unroll
-            for (int j = i; j < i + h; ++j) {
-                const float a = y[j], b = y[j + h];
-                y[j] = a + b;
-                y[j + h] = a - b;
-            }
-        }
-    }
-}
-
-// codes q[D] -> packed bytes written as 16-bit words (dst is 2-byte aligned)
-template <int D, int BITS>
-__device__ __forceinline__ void store_codes(const int* q, uint8_t* dst) {
+// codes of this lane's 8 dims -> its bytes of the packed slot (dst 2-byte
+// aligned).  4-bit: even d in the low nibble (:291), lane j's 4 bytes at 4j.
+// 3-bit: 8 codes -> 3 bytes little endian, code i at bits 3i (:294-309);
+// lanes 2i, 2i+1 form 6 bytes at 6i, written by the even lane.
+template <int BITS>
+__device__ __forceinline__ void store_codes8(const int* q, uint8_t* dst, int j) {
     uint16_t* d16 = reinterpret_cast<uint16_t*>(dst);
     if constexpr (BITS == 4) {
-        // even d in the low nibble (:291)
+        uint32_t w = 0;
 #pragma unroll
-        for (int d = 0; d < D; d += 4)
-            d16[d / 4] = (uint16_t)((q[d] & 0xf) | ((q[d + 1] & 0xf) << 4) | ((q[d + 2] & 0xf) << 8) |
-                                    ((q[d + 3] & 0xf) << 12));
+        for (int i = 0; i < 8; ++i) w |= (uint32_t)(q[i] & 0xf) << (4 * i);
+        d16[2 * j] = (uint16_t)(w & 0xffffu);
+        d16[2 * j + 1] = (uint16_t)(w >> 16);
     } else {
-        // 8 codes -> 3 bytes little endian, code i at bits 3i (:294-309); two
-        // groups give three 16-bit words
+        uint32_t w = 0;
 #pragma unroll
-        for (int g = 0; g < D / 8; g += 2) {
-            uint32_t p0 = 0, p1 = 0;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                p0 |= (uint32_t)(q[g * 8 + i] & 7) << (3 * i);
-                p1 |= (uint32_t)(q[(g + 1) * 8 + i] & 7) << (3 * i);
-            }
-            const uint64_t w = (uint64_t)p0 | ((uint64_t)p1 << 24);
-            d16[g / 2 * 3 + 0] = (uint16_t)(w & 0xffff);
-            d16[g / 2 * 3 + 1] = (uint16_t)((w >> 16) & 0xffff);
-            d16[g / 2 * 3 + 2] = (uint16_t)((w >> 32) & 0xffff);
+        for (int i = 0; i < 8; ++i) w |= (uint32_t)(q[i] & 7) << (3 * i);
+        const uint32_t hi = (uint32_t)__shfl_xor((int)w, 1, kGroup);
+        if ((j & 1) == 0) {
+            const uint64_t w48 = (uint64_t)w | ((uint64_t)hi << 24);
+            d16[3 * (j >> 1) + 0] = (uint16_t)(w48 & 0xffff);
+            d16[3 * (j >> 1) + 1] = (uint16_t)((w48 >> 16) & 0xffff);
+            d16[3 * (j >> 1) + 2] = (uint16_t)((w48 >> 32) & 0xffff);
         }
     }
 }
 
 template <int D, int KB, int VB, bool BF16>
-__global__ void __launch_bounds__(64)
+__global__ void __launch_bounds__(256)
 tq_store_kernel(const uint16_t* __restrict__ key, const uint16_t* __restrict__ value,
                 uint8_t* __restrict__ cache, const int64_t* __restrict__ slot_mapping, int T,
                 int Hkv, int64_t bs, int SA, int mse_bytes, int key_packed, int val_data,
                 TQTables tab) {
-    const int64_t pid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (pid >= (int64_t)T * Hkv) return;
-    const int64_t t = pid / Hkv;
-    const int h = (int)(pid % Hkv);
-    const int64_t slot = slot_mapping[t];
-    if (slot < 0) return;  // :266-267
+    static_assert(D == kGroup * kDims, "one 16-lane group per 128-dim vector");
+    __shared__ __attribute__((aligned(16))) float sq[256 / kGroup][D];  // per-group K for the norm chain
+    const int lane = threadIdx.x & 63, j = lane & (kGroup - 1);
+    const int gi = threadIdx.x / kGroup;  // group in the workgroup
+    const int64_t pid = (int64_t)blockIdx.x * (blockDim.x / kGroup) + gi;
+    const bool live = pid < (int64_t)T * Hkv;
+    const int64_t pv = live ? pid : 0;  // every lane stays in the shuffles
+    const int64_t t = pv / Hkv;
+    const int h = (int)(pv % Hkv);
+    const int64_t slot = live ? slot_mapping[t] : -1;  // :266-267: slot < 0 skips
     const int64_t blk = slot / bs, off = slot % bs;
     uint8_t* sp = cache + blk * bs * Hkv * SA + off * Hkv * SA + (int64_t)h * SA;
 
-    float y[D];
-    int q[D];
-    // ---- K: norm, normalise, rotate, codebook
-    load_vec<D, BF16>(key + pid * D, y);
+    float y[kDims], vv[kDims];
+    int q[kDims];
+    // both loads up front (one HBM latency)
+    load8<BF16>(key + pv * D + kDims * j, y);
+    load8<BF16>(value + pv * D + kDims * j, vv);
+    // ---- K: norm by the reference's sequential fmaf chain over d = 0..D-1
+    // (every lane of the group runs the same chain from LDS)
+#pragma unroll
+    for (int e = 0; e < kDims; ++e) sq[gi][kDims * j + e] = y[e];
+    __syncthreads();
     float nsq = 0.0f;
 #pragma unroll
-    for (int d = 0; d < D; ++d) nsq = __builtin_fmaf(y[d], y[d], nsq);
+    for (int d = 0; d < D; d += 4) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(&sq[gi][d]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) nsq = __builtin_fmaf(v[e], v[e], nsq);
+    }
     const float norm = sqrtf(nsq);
     const float inv = 1.0f / (norm + 1e-8f);
 #pragma unroll
-    for (int d = 0; d < D; ++d) y[d] = __fmul_rn(y[d], inv);
-    fwht<D>(y);
+    for (int e = 0; e < kDims; ++e) y[e] = __fmul_rn(y[e], inv);
+    // Walsh-Hadamard, half-widths 1, 2, 4 inside the lane, 8 .. 64 across lanes
+    // (partner j ^ (h/8)); each butterfly is the same (a+b, a-b) as the
+    // sequential order
+#pragma unroll
+    for (int hw = 1; hw < kDims; hw <<= 1)
+#pragma unroll
+        for (int i = 0; i < kDims; i += 2 * hw)
+#pragma unroll
+            for (int k = i; k < i + hw; ++k) {
+                const float a = y[k], b = y[k + hw];
+                y[k] = a + b;
+                y[k + hw] = a - b;
+            }
+#pragma unroll
+    for (int m = 1; m < kGroup; m <<= 1) {
+#pragma unroll
+        for (int e = 0; e < kDims; ++e) {
+            const float o = __shfl_xor(y[e], m, kGroup);
+            y[e] = (j & m) ? o - y[e] : y[e] + o;
+        }
+    }
     constexpr int NC = 1 << KB;
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-        const float v = __fmul_rn(y[d], tab.rot_c);
+    for (int e = 0; e < kDims; ++e) {
+        const float v = __fmul_rn(y[e], tab.rot_c);
         int idx = 0;
 #pragma unroll
         for (int c = 0; c < NC - 1; ++c) idx += (v >= tab.midpoints[c]) ? 1 : 0;
-        q[d] = idx;
+        q[e] = idx;
     }
-    store_codes<D, KB>(q, sp);
-    *reinterpret_cast<uint16_t*>(sp + mse_bytes) = f32_to_half<BF16>(norm);
+    // slot is uniform over the group, so the pair shuffle of the 3-bit packing
+    // only reads lanes that take the same branch
+    if (slot >= 0) {
+        store_codes8<KB>(q, sp, j);
+        if (j == 0) *reinterpret_cast<uint16_t*>(sp + mse_bytes) = f32_to_half<BF16>(norm);
+    }
 
     // ---- V: asymmetric min/max over the whole vector (:314-347)
-    load_vec<D, BF16>(value + pid * D, y);
-    float vmin = 3.402823466e+38f, vmax = -3.402823466e+38f;
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-        vmin = fminf(vmin, y[d]);
-        vmax = fmaxf(vmax, y[d]);
+    for (int e = 0; e < kDims; ++e) y[e] = vv[e];
+    float vmin = y[0], vmax = y[0];
+#pragma unroll
+    for (int e = 1; e < kDims; ++e) {
+        vmin = fminf(vmin, y[e]);
+        vmax = fmaxf(vmax, y[e]);
+    }
+#pragma unroll
+    for (int m = 1; m < kGroup; m <<= 1) {
+        vmin = fminf(vmin, __shfl_xor(vmin, m, kGroup));
+        vmax = fmaxf(vmax, __shfl_xor(vmax, m, kGroup));
     }
     constexpr int VMAXQ = VB == 4 ? 15 : 7;
     float vscale = (vmax - vmin) / (float)VMAXQ;
     vscale = fmaxf(vscale, 1e-8f);
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-        int qq = (int)roundf((y[d] - vmin) / vscale);
-        q[d] = qq < 0 ? 0 : (qq > VMAXQ ? VMAXQ : qq);
+    for (int e = 0; e < kDims; ++e) {
+        int qq = (int)roundf((y[e] - vmin) / vscale);
+        q[e] = qq < 0 ? 0 : (qq > VMAXQ ? VMAXQ : qq);
     }
-    uint8_t* vp = sp + key_packed;
-    store_codes<D, VB>(q, vp);
-    *reinterpret_cast<uint16_t*>(vp + val_data) = f32_to_half<BF16>(vscale);
-    *reinterpret_cast<uint16_t*>(vp + val_data + 2) = f32_to_half<BF16>(vmin);
+    if (slot >= 0) {
+        uint8_t* vp = sp + key_packed;
+        store_codes8<VB>(q, vp, j);
+        if (j == 0) {
+            *reinterpret_cast<uint16_t*>(vp + val_data) = f32_to_half<BF16>(vscale);
+            *reinterpret_cast<uint16_t*>(vp + val_data + 2) = f32_to_half<BF16>(vmin);
+        }
+    }
 }
 
 template <int D, int KB, int VB>
@@ -144,8 +175,9 @@ int launch_store(const void* key, const void* value, void* cache, const int64_t*
                  int Hkv, int64_t bs, const vmc_tq_config* c, bool bf16, hipStream_t stream) {
     const TQTables& tab = tq_tables(D, KB);
     const int64_t n = (int64_t)T * Hkv;
-    const int threads = 64;
-    const int64_t grid = (n + threads - 1) / threads;
+    const int threads = 256, per_block = threads / kGroup;
+    const int64_t grid = (n + per_block - 1) / per_block;
+    if (grid > 0x7fffffff) return VMC_EINVAL;
     if (bf16)
         hipLaunchKernelGGL((tq_store_kernel<D, KB, VB, true>), dim3((unsigned)grid), dim3(threads),
                            0, stream, (const uint16_t*)key, (const uint16_t*)value,
