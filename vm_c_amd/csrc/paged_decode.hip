@@ -49,7 +49,7 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kBs = 16;
-constexpr int kChunkPages = 1024;  // pages whose block-table entries are staged in LDS at once
+constexpr int kChunkPages = 512;  // pages whose block-table entries are staged in LDS at once
 constexpr float kNegInf = -__builtin_inff();
 
 enum { FMT_F16 = 0, FMT_BF16 = 1, FMT_Q8_0 = 2, FMT_Q4_0 = 3, FMT_TQ = 4 };
@@ -65,9 +65,11 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 // Compile-time geometry of a page format (head_dim 128, block 16, at most 8
 // KV heads): TurboQuant slot fields (kernels_turboquant.h:29-45), GGUF entry
-// sizes, and the register staging of LDS-staged formats -- SPP 16-byte
-// chunks per thread per page (one wave per KV head) and PF pages in flight,
-// each with its own LDS buffer of kBuf bytes (K page, then V page at kHalf).
+// sizes, and the staging of LDS-staged formats -- SPP 16-byte chunks per
+// thread per page (one wave per KV head) and PF pages in flight.  GGUF pages
+// go through registers into one LDS buffer per ring slot (K page, then V page
+// at kHalf); TurboQuant pages go straight from HBM into LDS (load-to-LDS DMA)
+// with PF + 2 page-sized buffers: two pages are read while PF more land.
 template <int FMT, int KB, int VB>
 struct Geo {
     static constexpr int mse = 16 * KB, key_packed = mse + 2, val_data = 16 * VB;
@@ -76,17 +78,25 @@ struct Geo {
     static constexpr int per_thread = FMT == FMT_TQ ? entry : 2 * entry;  // staged bytes per token-head
     static constexpr bool staged = FMT >= FMT_Q8_0;
     static constexpr int spp = staged ? (per_thread + 63) / 64 : 1;
-    static constexpr int pf = !staged ? 1 : (spp <= 2 ? 4 : (spp <= 3 ? 3 : 2));
-    static constexpr int kHalf = kBs * 8 * entry;                    // one cache's page, 8 heads
-    static constexpr int kBuf = FMT == FMT_TQ ? kHalf : 2 * kHalf;  // one LDS buffer
+    static constexpr bool dma = FMT == FMT_TQ;
+    static constexpr int pf = !staged ? 1 : dma ? 2 : (spp <= 2 ? 4 : (spp <= 3 ? 3 : 2));
+    static constexpr int nbuf = dma ? pf + 2 : pf;
+    static constexpr int kHalf = kBs * 8 * entry;  // one cache's page, 8 heads
+    static constexpr int kBuf = dma ? kHalf : 2 * kHalf;  // one LDS buffer
 };
 
-// Scale of PV chunk c's accumulator: TurboQuant V codes enter the MFMA as the
-// fp16 subnormals c * 2^-24 (4-bit odd chunks keep the nibble at bit 4:
-// c * 2^-20), other formats as values.
+// TurboQuant V codes enter the PV MFMA as fp16 subnormals: the code field of
+// output chunk c is masked where it lies, at bit kVShift(c) of its 16-bit
+// half (at most bit 9, so the pattern stays a subnormal), i.e. the value
+// code * 2^(shift - 24).  kVScale(c) = 2^(24 - shift) undoes it; other formats
+// enter as values.
+template <int VB>
+__device__ __forceinline__ constexpr int kVShift(int c) {
+    return VB == 4 ? ((c & 1) ? 4 : 0) : (c == 0 ? 0 : c == 1 ? 3 : c == 2 ? 6 : c == 3 ? 1 : c == 4 ? 4 : c == 5 ? 7 : c == 6 ? 2 : 5);
+}
 template <int FMT, int VB>
 __device__ __forceinline__ constexpr float kVScale(int c) {
-    return FMT != FMT_TQ ? 1.0f : (VB == 4 && (c & 1)) ? 1048576.0f : 16777216.0f;
+    return FMT != FMT_TQ ? 1.0f : (float)(1 << (24 - kVShift<VB>(c)));
 }
 
 // fmax without the NaN-quieting the IEEE mode adds around fmaxf
@@ -94,6 +104,22 @@ __device__ __forceinline__ float vmax(float a, float b) {
     float r;
     asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
     return r;
+}
+// bitwise select b where m is set, else a (v_bfi_b32).  Plain C++ so the
+// compiler sees the operands: an asm consumer of an MFMA result would not get
+// the wait states the MFMA's write requires.
+__device__ __forceinline__ float sel_bits(float a, float b, uint32_t m) {
+    return __builtin_bit_cast(float, (__builtin_bit_cast(uint32_t, b) & m) | (__builtin_bit_cast(uint32_t, a) & ~m));
+}
+// max over the four lane groups of a column (every lane gets its column's)
+__device__ __forceinline__ float vmax_over_groups(float v) {
+    uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+    swap_pair16(a, b);
+    v = vmax(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+    a = __builtin_bit_cast(uint32_t, v);
+    b = a;
+    swap_pair32(a, b);
+    return vmax(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
 }
 
 struct DecodeParams {
@@ -136,7 +162,7 @@ __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
 }
 
 // total pages of the batch (one wave, result in every lane)
-__device__ int total_pages(const DecodeParams& p, int lane) {
+__device__ __forceinline__ int total_pages(const DecodeParams& p, int lane) {
     int total = 0;
     for (int b0 = 0; b0 < p.B; b0 += 64) {
         int L = 0;
@@ -167,7 +193,7 @@ struct WGPlan {
 
 // Sequences with pages in [c_lo, c_hi), in order, into LDS (one wave).  In the
 // same pass: the sequences holding p_lo and p_hi - 1.
-__device__ int collect_segments(const DecodeParams& p, int c_lo, int c_hi, int lane, int* seg_b,
+__device__ __forceinline__ int collect_segments(const DecodeParams& p, int c_lo, int c_hi, int lane, int* seg_b,
                                 int* seg_ps, int* seg_L, WGPlan* plan, bool plan_ends) {
     const int p_lo = plan->p_lo, p_hi = plan->p_hi;
     int carry = 0, ns = 0;
@@ -233,18 +259,38 @@ __device__ __forceinline__ int entry_off(int tok, int g, int Hkv, int E, int hnd
 
 // ------------------------------------------------------------------ kernel
 
+// Every LDS byte of the decode kernel in one object, the page ring first, so
+// a ring slot's reads carry compile-time offsets (below 64 KiB they fold into
+// the LDS instruction) and need no address arithmetic.
+template <int FMT, int KB, int VB>
+struct alignas(16) DecodeLds {
+    using GE = Geo<FMT, KB, VB>;
+    uint8_t ring[GE::staged ? GE::nbuf * GE::kBuf : 16];
+    u32x2 lut4[FMT == FMT_TQ && KB == 3 ? 4096 : 1];  // 3-bit keys: four fp16 centroids per 12 bits
+    uint32_t lut[FMT == FMT_TQ ? 256 : 1];              // key code pair -> two fp16 centroids
+    float wscr[8][80];                                  // per-wave exchange
+    int32_t bt[kChunkPages];                            // block of each page of the chunk
+    int32_t info[kChunkPages];                          // b << 6 | valid tokens << 1 | piece ends
+    int32_t seg_b[kChunkPages], seg_ps[kChunkPages], seg_L[kChunkPages];
+    WGPlan plan;
+    int n_seg;
+};
+
 template <int FMT, int KB, int VB, bool MBF16>
 __global__ void __launch_bounds__(512)
 paged_decode_kernel(DecodeParams p) {
     using AT = typename std::conditional<MBF16, bf16x8, f16x8>::type;
     using PT = typename std::conditional<MBF16, s16x4, f16x4>::type;
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    __shared__ WGPlan plan;
-    __shared__ int n_seg;
-    __shared__ __attribute__((aligned(16))) float wscr_all[8][48];  // per-wave exchange
-    __shared__ int32_t bt_lds[kChunkPages];    // block of each page of the chunk
-    __shared__ int32_t info_lds[kChunkPages];  // b << 6 | valid tokens << 1 | piece ends
-    __shared__ int32_t seg_b[kChunkPages], seg_ps[kChunkPages], seg_L[kChunkPages];
+    __shared__ DecodeLds<FMT, KB, VB> lds;
+    uint8_t* const smem = lds.ring;
+    WGPlan& plan = lds.plan;
+    int32_t* const bt_lds = lds.bt;
+    int32_t* const info_lds = lds.info;
+    int32_t* const seg_b = lds.seg_b;
+    int32_t* const seg_ps = lds.seg_ps;
+    int32_t* const seg_L = lds.seg_L;
+    uint32_t* const lut = lds.lut;
+    u32x2* const lut4 = lds.lut4;
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
@@ -281,7 +327,7 @@ paged_decode_kernel(DecodeParams p) {
     const int p_hi = __builtin_amdgcn_readfirstlane(plan.p_hi);
 
     const int g = wave;  // kv head of this wave
-    float* wscr = wscr_all[wave];
+    float* wscr = lds.wscr[wave];
     const int G = p.G;
     const int hq0 = g * G;
     const bool head_ok = r16 < G;
@@ -296,10 +342,8 @@ paged_decode_kernel(DecodeParams p) {
         return;
     }
 
-    // static LDS: the LUTs' addresses are compile-time offsets of each read.
-    // 3-bit keys: a 12-bit LUT of four packed fp16 centroids per entry.
-    __shared__ uint32_t lut[FMT == FMT_TQ ? 256 : 1];
-    __shared__ u32x2 lut4[FMT == FMT_TQ && KB == 3 ? 4096 : 1];
+    // key centroid tables (their addresses are compile-time offsets of each
+    // read); 3-bit keys: a 12-bit table of four packed fp16 centroids
     if constexpr (FMT == FMT_TQ) {
         build_pair_lut<KB>(lut, p.tab);
         if constexpr (KB == 3) {
@@ -443,6 +487,8 @@ paged_decode_kernel(DecodeParams p) {
         reset_state();
     };
 
+    int npc = 0;  // pages of the current chunk
+
     // staged formats: PF pages in flight in registers -> LDS double buffer
     using GE = Geo<FMT, KB, VB>;
     constexpr int SPP = GE::spp, PF = GE::pf;
@@ -473,6 +519,27 @@ paged_decode_kernel(DecodeParams p) {
             const int idx = tid + c * nthreads;
             const int off = (FMT == FMT_TQ || idx < n16_k) ? 16 * idx : GE::kHalf + 16 * (idx - n16_k);
             if (idx < n16) *reinterpret_cast<u32x4*>(buf + off) = stage[S][c];
+        }
+    };
+
+    // TurboQuant: page i of the chunk straight into LDS buffer buf: 16-byte
+    // chunk c*nthreads + tid of the page goes to the same offset of the
+    // buffer; lanes past the page issue nothing.  Past the chunk's last page
+    // (i >= npc) block 0 is re-read (every workgroup shares it, so it stays
+    // in the cache) into a buffer no step reads.
+    uint32_t dma_off[SPP];  // loop-invariant byte offset of this lane's chunks
+#pragma unroll
+    for (int c = 0; c < SPP; ++c) dma_off[c] = 16u * (uint32_t)(c * nthreads + tid);
+    auto dma_page = [&](int i, int buf) __attribute__((always_inline)) {
+        const int32_t blk = i < npc ? max(bt_lds[i], 0) : 0;
+        const uint8_t* src = p.kc + (int64_t)__builtin_amdgcn_readfirstlane(blk) * page_bytes;
+#pragma unroll
+        for (int c = 0; c < SPP; ++c) {
+            uint8_t* dst = smem + buf * GE::kBuf + 16 * (c * nthreads + 64 * wave);
+            if ((int)dma_off[c] < (int)page_bytes)
+                __builtin_amdgcn_global_load_lds(
+                    (const void __attribute__((address_space(1)))*)(src + dma_off[c]),
+                    (void __attribute__((address_space(3)))*)dst, 16, 0, 0);
         }
     };
 
@@ -510,7 +577,202 @@ paged_decode_kernel(DecodeParams p) {
         }
     };
 
-    int npc = 0;  // pages of the current chunk
+
+    // ---- TurboQuant: two pages (32 tokens) per online-softmax step.  Slot pp
+    // of a step is ring buffer BUF0 + pp (compile time); a slot without valid
+    // tokens (nv 0) contributes nothing.
+    // Per-lane loop-invariant LDS offsets inside a page: the even start of
+    // the four bytes holding token (4*grp + i)'s V code run (dims 8*r16 ..
+    // +7), which begins d = 0 or 1 bytes in (3-bit runs at odd offsets), and
+    // the byte-permute selectors that gather code bytes d .. d+2 of two tokens.
+    int vc_al[4];
+#pragma unroll
+    for (int i2 = 0; i2 < 4; ++i2) vc_al[i2] = (v_off[i2] + GE::key_packed + VB * r16) & ~1;
+    const uint32_t vd = (uint32_t)((v_off[0] + GE::key_packed + VB * r16) & 1) * 0x01010101u;
+    const uint32_t vsel0 = 0x05040100u + vd, vsel1 = 0x06050201u + vd, vsel2 = 0x07060302u + vd;
+    // Gram diagonal: lane (r16, grp) picks element r16 % 4 (two bit masks);
+    // the exchange slot of its row factor is r16 on the diagonal (grp ==
+    // r16 / 4) and 16 + r16 elsewhere (written, never read), so the write
+    // needs no branch.
+    const uint32_t odd_mask = (r16 & 1) ? ~0u : 0u, hi_mask = (r16 & 2) ? ~0u : 0u;
+    const int diag_slot = ((r16 >> 2) == grp ? 0 : 16) + r16;
+    float m_thr = kNegInf;  // m_run + 8: the lazy max moves only past it
+    auto process_tq = [&](auto buf0_c, int nv0, int nv1, auto masked_c) __attribute__((always_inline)) {
+        constexpr bool kMasked = decltype(masked_c)::value;  // a slot has fewer than 16 valid tokens
+        constexpr int BUF0 = decltype(buf0_c)::value;
+        if constexpr (FMT == FMT_TQ) {
+        const uint8_t* pg[2] = {smem + BUF0 * GE::kBuf, smem + (BUF0 + 1) * GE::kBuf};
+        const int nvp[2] = {nv0, nv1};
+        AT a[2][4];
+        float rowf[2];
+        uint16_t vsc[2][4], vzr[2][4];  // fp16 scale and zero of token 4*grp + i
+        uint32_t bop[2][8][2];  // PV B operands: dim 8*r16 + c, tokens {0,1} / {2,3}
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp) {
+            // K: lane group grp owns dims 32*grp .. +31 of token r16; the codes
+            // index LUTs of packed fp16 centroids.
+            const uint8_t* ke = pg[pp] + k_off;
+            u32x4 aw[4];
+            if constexpr (KB == 4) {
+                const uint8_t* cb = ke + 16 * grp;  // 16 bytes, 2-byte aligned
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t wv = lds16(cb + 4 * j) | (lds16(cb + 4 * j + 2) << 16);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) aw[j][e] = lut[(wv >> (8 * e)) & 0xffu];
+                }
+            } else {
+                // 12 bytes = four 8-code groups; each 12-bit half indexes the
+                // table of four packed fp16 centroids
+                const uint8_t* cb = ke + 12 * grp;
+                uint32_t h[6];
+#pragma unroll
+                for (int q = 0; q < 6; ++q) h[q] = lds16(cb + 2 * q);
+                const uint32_t g24[4] = {h[0] | ((h[1] & 0xffu) << 16), (h[1] >> 8) | (h[2] << 8),
+                                         h[3] | ((h[4] & 0xffu) << 16), (h[4] >> 8) | (h[5] << 8)};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const u32x2 lo = lut4[g24[j] & 0xfffu], hi = lut4[g24[j] >> 12];
+                    aw[j] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) a[pp][j] = __builtin_bit_cast(AT, aw[j]);
+            // ||C[codes]||^2 of every token: the diagonal of the Gram matrix
+            // K K^T (fp16 products exact, sums fp32); token r16's value sits in
+            // the lanes with grp == r16 / 4, element r16 % 4.
+            f32x4 gram = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) gram = mfma16x16x32(a[pp][j], a[pp][j], gram);
+            const float csq = sel_bits(sel_bits(gram[0], gram[1], odd_mask), sel_bits(gram[2], gram[3], odd_mask),
+                                       hi_mask);
+            const float nrm = f16_bits_to_f32((uint16_t)lds16(ke + GE::mse));
+            rowf[pp] = p.scale_log2 * nrm * __builtin_amdgcn_rsqf(csq + 1e-16f);
+            // V: the four bytes around token 4*grp + i's code run, its scale
+            // and zero
+            uint32_t cw[4];
+#pragma unroll
+            for (int i2 = 0; i2 < 4; ++i2) {
+                const uint8_t* cr = pg[pp] + vc_al[i2];
+                cw[i2] = lds16(cr) | (lds16(cr + 2) << 16);
+                const uint8_t* ve = pg[pp] + v_off[i2] + GE::key_packed + GE::val_data;
+                vsc[pp][i2] = (uint16_t)lds16(ve);
+                vzr[pp][i2] = (uint16_t)lds16(ve + 2);
+            }
+            if constexpr (kMasked) {  // tokens past the end may hold anything
+#pragma unroll
+                for (int i2 = 0; i2 < 4; ++i2) {
+                    const bool ok = 4 * grp + i2 < nvp[pp];
+                    vsc[pp][i2] = ok ? vsc[pp][i2] : (uint16_t)0;
+                    vzr[pp][i2] = ok ? vzr[pp][i2] : (uint16_t)0;
+                }
+            }
+            // B operands {token a, token b} per dim: byte permutes put both
+            // tokens' code bytes in the two halves of a dword, then each
+            // chunk's field is masked where it lies (kVShift).
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const uint32_t A = cw[2 * hh], Bw = cw[2 * hh + 1];
+                const uint32_t w0 = __builtin_amdgcn_perm(Bw, A, vsel0);  // run bytes 0-1
+                const uint32_t w1 = __builtin_amdgcn_perm(Bw, A, vsel1);  // run bytes 1-2
+                const uint32_t w2 = __builtin_amdgcn_perm(Bw, A, vsel2);  // run bytes 2-3 (4-bit)
+                if constexpr (VB == 4) {
+                    const uint32_t w3 = __builtin_amdgcn_perm(Bw, A, 0x0c070c03u);  // run byte 3
+                    bop[pp][0][hh] = w0 & 0x000f000fu;
+                    bop[pp][1][hh] = w0 & 0x00f000f0u;
+                    bop[pp][2][hh] = w1 & 0x000f000fu;
+                    bop[pp][3][hh] = w1 & 0x00f000f0u;
+                    bop[pp][4][hh] = w2 & 0x000f000fu;
+                    bop[pp][5][hh] = w2 & 0x00f000f0u;
+                    bop[pp][6][hh] = w3 & 0x000f000fu;
+                    bop[pp][7][hh] = w3 & 0x00f000f0u;
+                } else {
+                    bop[pp][0][hh] = w0 & 0x00070007u;  // code bits 0-2 of the run
+                    bop[pp][1][hh] = w0 & 0x00380038u;  // 3-5
+                    bop[pp][2][hh] = w0 & 0x01c001c0u;  // 6-8
+                    bop[pp][3][hh] = w1 & 0x000e000eu;  // 9-11
+                    bop[pp][4][hh] = w1 & 0x00700070u;  // 12-14
+                    bop[pp][5][hh] = w1 & 0x03800380u;  // 15-17
+                    bop[pp][6][hh] = w2 & 0x001c001cu;  // 18-20 (w2's high bytes unused)
+                    bop[pp][7][hh] = w2 & 0x00e000e0u;  // 21-23
+                }
+            }
+        }
+        // ---- S^T = K . Q^T per page, times the per-token factor
+        f32x4 sacc[2];
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp) {
+            sacc[pp] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sacc[pp] = mfma16x16x32(a[pp][j], qb[j], sacc[pp]);
+        }
+        wscr[diag_slot] = rowf[0];
+        wscr[32 + diag_slot] = rowf[1];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const f32x4 rf0 = *reinterpret_cast<const f32x4*>(wscr + 4 * grp);
+        const f32x4 rf1 = *reinterpret_cast<const f32x4*>(wscr + 32 + 4 * grp);
+        __builtin_amdgcn_wave_barrier();
+        float sv[2][4];
+#pragma unroll
+        for (int i2 = 0; i2 < 4; ++i2) {
+            sv[0][i2] = sacc[0][i2] * rf0[i2];
+            sv[1][i2] = sacc[1][i2] * rf1[i2];
+        }
+        if constexpr (kMasked) {
+#pragma unroll
+            for (int pp = 0; pp < 2; ++pp)
+#pragma unroll
+                for (int i2 = 0; i2 < 4; ++i2) sv[pp][i2] = 4 * grp + i2 < nvp[pp] ? sv[pp][i2] : kNegInf;
+        }
+        // Lazy reference max: m_run moves only when a head's max exceeds it by
+        // more than 8 (log2 units), so p <= 256 and most steps skip the O
+        // rescale.  Every term of l, z and O uses the same reference: exact.
+        // The cross-group max is taken only when some lane's own max passes
+        // the threshold.
+        const float mloc = vmax(vmax(vmax(sv[0][0], sv[0][1]), vmax(sv[0][2], sv[0][3])),
+                                vmax(vmax(sv[1][0], sv[1][1]), vmax(sv[1][2], sv[1][3])));
+        if (__ballot(mloc > m_thr)) {  // wave-uniform
+            const float mx = vmax_over_groups(mloc);
+            const bool upd = mx > m_thr;  // the same in every lane of head r16
+            const float m_new = upd ? mx : m_run;
+            const float alpha = upd ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;  // 0 when m_run = -inf
+            l_part *= alpha;
+            z_part *= alpha;
+            const f32x4 al = gather4_from_row0(alpha, wscr + 64, r16, grp);
+#pragma unroll
+            for (int i2 = 0; i2 < 4; ++i2)
+#pragma unroll
+                for (int c = 0; c < 8; ++c) oacc[c][i2] *= al[i2];
+            m_run = m_new;
+            m_thr = m_run + 8.0f;
+        }
+        const float m_use = m_run == kNegInf ? 0.0f : m_run;
+        float psum = 0.0f, zsum = 0.0f;
+        AT pa;  // A operand of the PV MFMA: k = 8*grp + 4*pp + i <-> page pp, token 4*grp + i
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp)
+#pragma unroll
+            for (int i2 = 0; i2 < 4; ++i2) {
+                const float pv = __builtin_amdgcn_exp2f(sv[pp][i2] - m_use);
+                const float sc = (float)__builtin_bit_cast(_Float16, vsc[pp][i2]);
+                const float zr = (float)__builtin_bit_cast(_Float16, vzr[pp][i2]);
+                psum += pv;
+                zsum = __builtin_fmaf(pv, zr, zsum);
+                pa[4 * pp + i2] = (_Float16)__builtin_fmaf(pv, sc, 0.0f);
+            }
+        l_part += psum;
+        z_part += zsum;
+        // ---- O += P . V over the 32 tokens of both pages
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const AT vb = __builtin_bit_cast(AT, u32x4{bop[0][c][0], bop[0][c][1], bop[1][c][0], bop[1][c][1]});
+            oacc[c] = mfma16x16x32(pa, vb, oacc[c]);
+        }
+        }
+    };
+
     auto process = [&](int i, auto buf_c) __attribute__((always_inline)) {
         constexpr int BUF = decltype(buf_c)::value;
         const uint8_t* kpage = smem + BUF * GE::kBuf;
@@ -523,105 +785,14 @@ paged_decode_kernel(DecodeParams p) {
             cur_b = b;
         }
         AT a[4];
-        float rowf = p.scale_log2;  // factor of S row r16 (token r16)
         // V operand pieces (tokens 4*grp + i, dims 8*r16 .. +7) as fp16/bf16 bits
         uint32_t vw[4][4];  // [token i][dword e] = dims (2e, 2e+1)
         uint32_t bop[8][2];  // PV B operands: dim 8*r16 + c, tokens {0,1} / {2,3}
-        float vsc[4] = {1.f, 1.f, 1.f, 1.f}, vzr[4] = {0.f, 0.f, 0.f, 0.f};
 
         if constexpr (kStaged) {
             // ---- K operand for token r16
             const uint8_t* ke = kpage + k_off;
-            if constexpr (FMT == FMT_TQ) {
-                // K: lane group grp owns dims 32*grp .. +31 of token r16; each
-                // code pair indexes the LUT of packed fp16 centroid pairs.
-                u32x4 aw[4];
-                if constexpr (KB == 4) {
-                    const uint8_t* cb = ke + 16 * grp;  // 16 bytes, 2-byte aligned
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const uint32_t wv = lds16(cb + 4 * j) | (lds16(cb + 4 * j + 2) << 16);
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) aw[j][e] = lut[(wv >> (8 * e)) & 0xffu];
-                    }
-                } else {
-                    const uint8_t* cb = ke + 12 * grp;  // 12 bytes = four 8-code groups
-                    uint32_t h[6];
-#pragma unroll
-                    for (int q = 0; q < 6; ++q) h[q] = lds16(cb + 2 * q);
-                    const uint32_t g24[4] = {h[0] | ((h[1] & 0xffu) << 16), (h[1] >> 8) | (h[2] << 8),
-                                             h[3] | ((h[4] & 0xffu) << 16), (h[4] >> 8) | (h[5] << 8)};
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const u32x2 lo = lut4[g24[j] & 0xfffu], hi = lut4[g24[j] >> 12];
-                        aw[j] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-                    }
-                }
-#pragma unroll
-                for (int j = 0; j < 4; ++j) a[j] = __builtin_bit_cast(AT, aw[j]);
-                // ||C[codes]||^2 of every token: the diagonal of the Gram matrix
-                // K K^T (the A operand doubles as the B operand; fp16 products
-                // are exact, sums fp32).  Token r16's value sits in the lanes
-                // with grp == r16 / 4, element r16 % 4.
-                f32x4 gram = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) gram = mfma16x16x32(a[j], a[j], gram);
-                const int di = r16 & 3;
-                const float csq = di == 0 ? gram[0] : di == 1 ? gram[1] : di == 2 ? gram[2] : gram[3];
-                const float nrm = f16_bits_to_f32((uint16_t)lds16(ke + GE::mse));
-                rowf = p.scale_log2 * nrm * __builtin_amdgcn_rsqf(csq + 1e-16f);
-                // V: codes of tokens 4*grp + i, dims 8*r16 .. +7, scale and zero
-                uint32_t cw[4];
-#pragma unroll
-                for (int i2 = 0; i2 < 4; ++i2) {
-                    const int tok = 4 * grp + i2;
-                    const uint8_t* ve = kpage + v_off[i2] + GE::key_packed;
-                    if constexpr (VB == 4) {
-                        cw[i2] = lds16(ve + 4 * r16) | (lds16(ve + 4 * r16 + 2) << 16);
-                    } else {
-                        // ve is even, so ve + 3*r16 is odd exactly when r16 is:
-                        // read the two aligned 16-bit words around it
-                        const uint8_t* al2 = ve + 3 * r16 - (r16 & 1);
-                        const uint32_t wv = lds16(al2) | (lds16(al2 + 2) << 16);
-                        cw[i2] = (wv >> (8 * (r16 & 1))) & 0xffffffu;
-                    }
-                    vsc[i2] = f16_bits_to_f32((uint16_t)lds16(ve + GE::val_data));
-                    vzr[i2] = f16_bits_to_f32((uint16_t)lds16(ve + GE::val_data + 2));
-                }
-                if (nv < kBs) {  // tokens past the end may hold anything
-#pragma unroll
-                    for (int i2 = 0; i2 < 4; ++i2) {
-                        const bool ok = 4 * grp + i2 < nv;
-                        vsc[i2] = ok ? vsc[i2] : 0.0f;
-                        vzr[i2] = ok ? vzr[i2] : 0.0f;
-                    }
-                }
-                // B operands {token a, token b} per dim: the integer code c as
-                // the fp16 subnormal c * 2^-24 (its bit pattern is c), so one
-                // mask per dim after a byte permute that puts both tokens'
-                // code fields in one dword; finalize scales O back (kVScale).
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const uint32_t A = cw[2 * hh], Bw = cw[2 * hh + 1];
-#pragma unroll
-                    for (int c = 0; c < 8; ++c) {
-                        if constexpr (VB == 4) {
-                            // byte c/2 of each token at bits 0 and 16; odd c keeps its
-                            // high nibble in place (c * 16 * 2^-24)
-                            const uint32_t t = __builtin_amdgcn_perm(Bw, A,
-                                                                     (uint32_t)(c >> 1) | 0x0c00u |
-                                                                         ((uint32_t)(4 + (c >> 1)) << 16) | 0x0c000000u);
-                            bop[c][hh] = t & ((c & 1) ? 0x00f000f0u : 0x000f000fu);
-                        } else {
-                            // codes 0-3 sit in bits 0-11 of each token, codes 4-7 in 12-23
-                            const uint32_t q = c < 4 ? __builtin_amdgcn_perm(Bw, A, 0x05040100u)
-                                                     : __builtin_amdgcn_perm(Bw, A, 0x06050201u);
-                            const int sh = c < 4 ? 3 * c : 3 * c - 8;
-                            bop[c][hh] = (q >> sh) & 0x00070007u;
-                        }
-                    }
-                }
-            } else {
+            {
                 // GGUF blocks: lane group grp owns block grp (dims 32*grp .. +31)
                 constexpr int BE = FMT == FMT_Q8_0 ? 34 : 18;
                 const uint8_t* kb = ke + BE * grp;
@@ -702,11 +873,9 @@ paged_decode_kernel(DecodeParams p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) sacc = mfma16x16x32(a[j], qb[j], sacc);
 
-        f32x4 rf = {rowf, rowf, rowf, rowf};
-        if constexpr (FMT == FMT_TQ) rf = gather4_from_diag(rowf, wscr, r16, grp);
         float sv[4];
 #pragma unroll
-        for (int i2 = 0; i2 < 4; ++i2) sv[i2] = sacc[i2] * rf[i2];
+        for (int i2 = 0; i2 < 4; ++i2) sv[i2] = sacc[i2] * p.scale_log2;
         if (nv < kBs) {
 #pragma unroll
             for (int i2 = 0; i2 < 4; ++i2) sv[i2] = 4 * grp + i2 < nv ? sv[i2] : kNegInf;
@@ -721,7 +890,6 @@ paged_decode_kernel(DecodeParams p) {
             const float m_new = upd ? mx : m_run;
             const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 when m_run = -inf
             l_part *= alpha;
-            if constexpr (FMT == FMT_TQ) z_part *= alpha;
             const f32x4 al = gather4_from_row0(alpha, wscr + 16, r16, grp);
 #pragma unroll
             for (int i2 = 0; i2 < 4; ++i2)
@@ -730,32 +898,27 @@ paged_decode_kernel(DecodeParams p) {
             m_run = m_new;
         }
         const float m_use = m_run == kNegInf ? 0.0f : m_run;
-        float pv[4], psum = 0.0f, zsum = 0.0f;
+        float pv[4], psum = 0.0f;
 #pragma unroll
         for (int i2 = 0; i2 < 4; ++i2) {
             pv[i2] = __builtin_amdgcn_exp2f(sv[i2] - m_use);
             psum += pv[i2];
-            if constexpr (FMT == FMT_TQ) zsum = __builtin_fmaf(pv[i2], vzr[i2], zsum);
         }
         l_part += psum;
-        if constexpr (FMT == FMT_TQ) z_part += zsum;
 
         // ---- O += P . V
         PT pa;
 #pragma unroll
         for (int i2 = 0; i2 < 4; ++i2) {
-            const float pw = (FMT == FMT_TQ) ? pv[i2] * vsc[i2] : pv[i2];
-            if constexpr (MBF16) pa[i2] = (short)f32_to_bf16_bits(pw);
-            else pa[i2] = (_Float16)pw;
+            if constexpr (MBF16) pa[i2] = (short)f32_to_bf16_bits(pv[i2]);
+            else pa[i2] = (_Float16)pv[i2];
         }
-        if constexpr (FMT != FMT_TQ) {
-            // {token 0,1} and {token 2,3} halves of dims (2e, 2e+1)
+        // {token 0,1} and {token 2,3} halves of dims (2e, 2e+1)
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
-                bop[c][0] = __builtin_amdgcn_perm(vw[1][c >> 1], vw[0][c >> 1], sel);
-                bop[c][1] = __builtin_amdgcn_perm(vw[3][c >> 1], vw[2][c >> 1], sel);
-            }
+        for (int c = 0; c < 8; ++c) {
+            const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+            bop[c][0] = __builtin_amdgcn_perm(vw[1][c >> 1], vw[0][c >> 1], sel);
+            bop[c][1] = __builtin_amdgcn_perm(vw[3][c >> 1], vw[2][c >> 1], sel);
         }
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
@@ -773,10 +936,10 @@ paged_decode_kernel(DecodeParams p) {
         if (wave == 0) {
             const int ns = collect_segments(p, c_lo, c_hi, lane, seg_b, seg_ps, seg_L, &plan,
                                             c_lo == p_lo && !p.per_seq);
-            if (lane == 0) n_seg = ns;
+            if (lane == 0) lds.n_seg = ns;
         }
         __syncthreads();
-        const int ns = n_seg;
+        const int ns = lds.n_seg;
         for (int i = tid; i < npc; i += nthreads) {
             const int gp = c_lo + i;
             int lo = 0, hi = ns - 1;  // last segment with seg_ps <= gp
@@ -795,7 +958,78 @@ paged_decode_kernel(DecodeParams p) {
         }
         __syncthreads();
 
-        if constexpr (kStaged) {
+        if constexpr (GE::dma) {
+            // Ring of NB = PF + 2 LDS buffers fed by load-to-LDS.  Steps take the
+            // aligned page pairs (2k, 2k+1) of the chunk; step k reads buffers
+            // 2k % NB and 2k % NB + 1 (compile-time: the loop is unrolled over
+            // the NB / 2 ring phases).  Pages 2k .. 2k+PF-1 are in flight when
+            // step k starts: each wave waits until only its transfers of the
+            // PF - 2 pages after the pair are outstanding (a wave issues nw
+            // transfers per page; vmcnt retires loads in issue order and later
+            // stores only make the wait stricter), the barrier makes every
+            // wave's share visible and shows that every wave is done with the
+            // previous step's buffers, which then receive pages 2k+PF and
+            // 2k+PF+1.  The barrier is the raw instruction and the asm's memory
+            // clobber keeps LDS reads below it.  A pair that a piece boundary
+            // splits runs twice, each time with one slot masked.
+            constexpr int NB = GE::nbuf, NPH = NB / 2;
+            static_assert(NB == PF + 2 && NB % 2 == 0 && PF <= 4 && SPP <= 3, "pair steps over an even ring");
+            // transfers this wave issues per page (its first lane decides)
+            int nw = 0;
+#pragma unroll
+            for (int c = 0; c < SPP; ++c) nw += (int)dma_off[c] - 16 * lane < (int)page_bytes;
+            nw = __builtin_amdgcn_readfirstlane(nw);
+#pragma unroll
+            for (int s2 = 0; s2 < PF; ++s2) dma_page(s2, s2);
+            for (int i0 = 0; i0 < npc; i0 += NB) {
+                static_for<NPH>([&](auto ph) __attribute__((always_inline)) {
+                    constexpr int S0 = 2 * decltype(ph)::value;
+                    const int i = i0 + S0;
+                    if (i < npc) {  // uniform over the workgroup
+                        // at most SPP * (PF - 2) <= 6 of this wave's transfers may stay
+                        switch (nw * (PF - 2)) {
+                        case 0: asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory"); break;
+                        case 1: asm volatile("s_waitcnt vmcnt(1)\n\ts_barrier" ::: "memory"); break;
+                        case 2: asm volatile("s_waitcnt vmcnt(2)\n\ts_barrier" ::: "memory"); break;
+                        case 3: asm volatile("s_waitcnt vmcnt(3)\n\ts_barrier" ::: "memory"); break;
+                        case 4: asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory"); break;
+                        default: asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory"); break;
+                        }
+                        dma_page(i + PF, (S0 + PF) % NB);
+                        dma_page(i + PF + 1, (S0 + PF + 1) % NB);
+                        const int info0 = __builtin_amdgcn_readfirstlane(info_lds[i]);
+                        const bool has1 = i + 1 < npc;
+                        const int info1 = has1 ? __builtin_amdgcn_readfirstlane(info_lds[i + 1]) : info0;
+                        const bool split = (info0 & 1) && has1;  // page i ends its piece, i + 1 starts one
+                        int b = info0 >> 6;
+                        int nva = (info0 >> 1) & 31, nvb = has1 && !split ? (info1 >> 1) & 31 : 0;
+                        int ends = split ? info0 : info1;
+                        for (int part = 0;; ++part) {
+                            if (b != cur_b) {  // a new sequence starts here
+                                load_q(b);
+                                cur_b = b;
+                            }
+                            if (nva == kBs && nvb == kBs)
+                                process_tq(std::integral_constant<int, S0>{}, nva, nvb, std::false_type{});
+                            else
+                                process_tq(std::integral_constant<int, S0>{}, nva, nvb, std::true_type{});
+                            if (ends & 1) {  // last page of this sequence's piece
+                                finalize(b);
+                                m_thr = kNegInf;
+                            }
+                            if (!split || part == 1) break;
+                            b = info1 >> 6;
+                            nva = 0;
+                            nvb = (info1 >> 1) & 31;
+                            ends = info1;
+                        }
+                    }
+                });
+            }
+            // no transfer may still target LDS when the buffers are reused or the
+            // workgroup ends
+            asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        } else if constexpr (kStaged) {
             // Ring of PF register slots: slot S holds page base+S+PF while page
             // base+S is computed from LDS.  Loads and LDS stores are unconditional
             // (tail pages clamp to the last page), so the only branch holds no
@@ -978,15 +1212,9 @@ int launch_decode(DecodeParams& prm, hipStream_t stream) {
                                                            prm.key_packed != GE::key_packed ||
                                                            prm.val_data != GE::val_data)))
         return VMC_EINVAL;
-    const size_t lds = GE::staged ? (size_t)GE::pf * GE::kBuf : 0;
     auto kern = paged_decode_kernel<FMT, KB, VB, MBF16>;
-    if (lds > 64 * 1024) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-            return VMC_EIO;
-    }
     prm.grid = prm.per_seq ? prm.B : flat_grid(prm.B, prm.Hkv, prm.max_blocks, prm.max_splits, num_cus());
-    hipLaunchKernelGGL(kern, dim3(prm.grid), dim3(64 * prm.Hkv), lds, stream, prm);
+    hipLaunchKernelGGL(kern, dim3(prm.grid), dim3(64 * prm.Hkv), 0, stream, prm);
     VMC_LAUNCH_CHECK();
     if (!prm.per_seq) {
         hipLaunchKernelGGL(decode_merge_kernel, dim3(prm.B, prm.Hkv), dim3(64 * prm.G), 0, stream, prm);

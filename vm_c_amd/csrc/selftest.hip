@@ -11,7 +11,7 @@ namespace {
 enum {
     kSumGroups = 1, kMaxGroups = 2, kGather = 4, kMfma16x32 = 8, kMfma16x16 = 16,
     kMfma32x16 = 32, kMfma16x32bf = 64, kMfma32x16bf = 128, kMfma16x16Subnormal = 256,
-    kGatherDiag = 512
+    kGatherDiag = 512, kMfma16x32Subnormal = 1024
 };
 
 // A[i][k] = (i + 2k) % 5 - 2, B[k][j] = (3k + j) % 7 - 3 (all exact)
@@ -56,6 +56,21 @@ __global__ void __launch_bounds__(64) selftest_kernel(int* fail) {
             for (int k = 0; k < 32; ++k) ref += Aval(4 * grp + i, k) * Bval(k, r16);
             if (d[i] != ref) bad |= kMfma16x32;
             if (db[i] != ref) bad |= kMfma16x32bf;
+        }
+        // B as fp16 subnormals holding a 3-bit code shifted left by 0..7
+        // (column r16 uses shift r16 % 8, so bit 9 is the highest set): the
+        // value is code * 2^(shift - 24), products and sums exact
+        f16x8 bs;
+        const int sh = r16 & 7;
+        for (int e = 0; e < 8; ++e) {
+            const int k = 8 * grp + e;
+            bs[e] = __builtin_bit_cast(_Float16, (uint16_t)(((3 * k + r16) % 8) << sh));
+        }
+        const f32x4 ds = mfma16x16x32(a, bs, f32x4{0.f, 0.f, 0.f, 0.f});
+        for (int i = 0; i < 4; ++i) {
+            float ref = 0.0f;
+            for (int k = 0; k < 32; ++k) ref += Aval(4 * grp + i, k) * (float)((3 * k + r16) % 8);
+            if (ds[i] * (float)(1 << (24 - sh)) != ref) bad |= kMfma16x32Subnormal;
         }
     }
     // 16x16x16 f16: k = 4*(l/16) + e
