@@ -133,6 +133,8 @@ TQ_CASES = {
     "cfg3_small": dict(seq_lens=[1024, 1024], Hq=32, Hkv=8),
     "cfg5_small": dict(seq_lens=[1024, 4000, 32], Hq=64, Hkv=8),
     "ragged": dict(seq_lens=[1, 17, 0, 300], Hq=16, Hkv=4),
+    # 16 query heads per KV head: the S tile's columns all hold heads of one page
+    "gqa16": dict(seq_lens=[300, 1024, 17, 33], Hq=32, Hkv=2),
 }
 
 

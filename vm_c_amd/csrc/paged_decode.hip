@@ -49,7 +49,7 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kBs = 16;
-constexpr int kChunkPages = 512;  // pages whose block-table entries are staged in LDS at once
+constexpr int kChunkPages = 256;  // pages whose block-table entries are staged in LDS at once
 constexpr float kNegInf = -__builtin_inff();
 
 enum { FMT_F16 = 0, FMT_BF16 = 1, FMT_Q8_0 = 2, FMT_Q4_0 = 3, FMT_TQ = 4 };
@@ -69,7 +69,8 @@ __device__ __forceinline__ void static_for(F&& f) {
 // thread per page (one wave per KV head) and PF pages in flight.  GGUF pages
 // go through registers into one LDS buffer per ring slot (K page, then V page
 // at kHalf); TurboQuant pages go straight from HBM into LDS (load-to-LDS DMA)
-// with PF + 2 page-sized buffers: two pages are read while PF more land.
+// with PF + 2 buffers, each one head group's share of a page: two pages are
+// read while PF more land.
 template <int FMT, int KB, int VB>
 struct Geo {
     static constexpr int mse = 16 * KB, key_packed = mse + 2, val_data = 16 * VB;
@@ -82,7 +83,14 @@ struct Geo {
     static constexpr int pf = !staged ? 1 : dma ? 2 : (spp <= 2 ? 4 : (spp <= 3 ? 3 : 2));
     static constexpr int nbuf = dma ? pf + 2 : pf;
     static constexpr int kHalf = kBs * 8 * entry;  // one cache's page, 8 heads
-    static constexpr int kBuf = dma ? kHalf : 2 * kHalf;  // one LDS buffer
+    // TurboQuant: a head group (<= 4 heads) of 16 tokens, each token's run
+    // fetched as a window of whole 16-byte chunks (at most nc_max of them)
+    static constexpr int nc_of(int h) { return (h * entry + 30) / 16; }
+    static constexpr int spt_of(int h) { return (kBs * nc_of(h) + 64 * h - 1) / (64 * h); }
+    static constexpr int nc_max = nc_of(4);
+    // chunks per lane per page for any group size (1..4 heads, one wave each)
+    static constexpr int spt = std::max(std::max(spt_of(1), spt_of(2)), std::max(spt_of(3), spt_of(4)));
+    static constexpr int kBuf = dma ? kBs * nc_max * 16 : 2 * kHalf;  // one LDS buffer
 };
 
 // TurboQuant V codes enter the PV MFMA as fp16 subnormals: the code field of
@@ -99,12 +107,10 @@ __device__ __forceinline__ constexpr float kVScale(int c) {
     return FMT != FMT_TQ ? 1.0f : (float)(1 << (24 - kVShift<VB>(c)));
 }
 
-// fmax without the NaN-quieting the IEEE mode adds around fmaxf
-__device__ __forceinline__ float vmax(float a, float b) {
-    float r;
-    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-    return r;
-}
+// fmax of scores (products, so never signalling NaNs: no quieting is added).
+// Plain C++ rather than asm: the hazard checks that guard cross-lane reads
+// (DPP, permlane) of a VGPR must see the instruction that wrote it.
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_fmaxf(a, b); }
 // bitwise select b where m is set, else a (v_bfi_b32).  Plain C++ so the
 // compiler sees the operands: an asm consumer of an MFMA result would not get
 // the wait states the MFMA's write requires.
@@ -137,7 +143,10 @@ struct DecodeParams {
     int hnd;
     int per_seq;         // 1: one workgroup per sequence
     int pps_min, max_splits;
-    int grid;            // launched decode workgroups
+    int grid;            // page ranges (flat) or sequences (per-sequence mode)
+    int hgroups, hpw;    // KV-head groups per page (one workgroup each), heads per group
+    int row_bytes;       // TurboQuant: one token's entries, all KV heads (Hkv * slot)
+    int tq_nc;           // TurboQuant: 16-byte chunks fetched per token for one head group
     int q_bf16;
     // TurboQuant
     int mse_bytes, key_packed, val_data;
@@ -276,7 +285,14 @@ struct alignas(16) DecodeLds {
     int n_seg;
 };
 
-template <int FMT, int KB, int VB, bool MBF16>
+// HALF (TurboQuant, at most 8 query heads per KV head): the 16 columns of
+// the S tile hold the heads for the step's first page (columns 0-7) and for
+// its second page (columns 8-15): K of both pages runs against a
+// block-diagonal Q^T, so every lane's four scores are real and the softmax
+// works on 4 values per lane instead of 8.  The PV product keeps the page of
+// each row apart (rows 0-7 first page, 8-15 second) and the halves are added
+// when the piece ends.
+template <int FMT, int KB, int VB, bool MBF16, bool HALF>
 __global__ void __launch_bounds__(512)
 paged_decode_kernel(DecodeParams p) {
     using AT = typename std::conditional<MBF16, bf16x8, f16x8>::type;
@@ -295,7 +311,11 @@ paged_decode_kernel(DecodeParams p) {
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int r16 = lane & 15, grp = lane >> 4;
-    const int w = blockIdx.x;
+    // workgroup = (KV-head group hg, page range or sequence w); the groups of
+    // one range are p.grid ids apart, so with p.grid a multiple of 8 they
+    // share an XCD (and its L2)
+    const int hg = (int)blockIdx.x / p.grid;
+    const int w = (int)blockIdx.x - hg * p.grid;
     constexpr bool kStaged = FMT >= FMT_Q8_0;
 
     // ---- this workgroup's page range
@@ -326,11 +346,13 @@ paged_decode_kernel(DecodeParams p) {
     const int p_lo = __builtin_amdgcn_readfirstlane(plan.p_lo);
     const int p_hi = __builtin_amdgcn_readfirstlane(plan.p_hi);
 
-    const int g = wave;  // kv head of this wave
+    const int g = hg * p.hpw + wave;  // kv head of this wave
     float* wscr = lds.wscr[wave];
     const int G = p.G;
     const int hq0 = g * G;
     const bool head_ok = r16 < G;
+    const int qh = HALF ? (r16 & 7) : r16;  // query head of S column r16
+    const bool q_ok = qh < G;
 
     if (p_lo >= p_hi) {
         // no pages: per-sequence mode writes the sequence's zero rows
@@ -353,12 +375,14 @@ paged_decode_kernel(DecodeParams p) {
     }
 
     // ---- Q operand: lane (r16 = head, grp) holds dims 32*grp + 8*j + e, j = MFMA index
-    AT qb[4];
+    // HALF: qb[0..3] hold the heads in columns 0-7 (zero in 8-15), qb[4..7]
+    // the heads in columns 8-15 (zero in 0-7)
+    AT qb[HALF ? 8 : 4];
     auto load_q = [&](int b) __attribute__((always_inline)) {
-        const int64_t qrow = ((int64_t)b * p.Hq + hq0 + r16) * kD;
+        const int64_t qrow = ((int64_t)b * p.Hq + hq0 + qh) * kD;
         if constexpr (FMT == FMT_TQ) {
             float y[32];
-            if (head_ok) {
+            if (q_ok) {
                 const u32x4* src = reinterpret_cast<const u32x4*>(p.q + qrow + 32 * grp);
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
@@ -400,6 +424,15 @@ paged_decode_kernel(DecodeParams p) {
             for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int e = 0; e < 8; ++e) qb[j][e] = (_Float16)__fmul_rn(y[8 * j + e], p.tab.rot_c);
+            if constexpr (HALF) {
+                const uint32_t lo_m = r16 < 8 ? ~0u : 0u;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const u32x4 v = __builtin_bit_cast(u32x4, qb[j]);
+                    qb[4 + j] = __builtin_bit_cast(AT, u32x4{v[0] & ~lo_m, v[1] & ~lo_m, v[2] & ~lo_m, v[3] & ~lo_m});
+                    qb[j] = __builtin_bit_cast(AT, u32x4{v[0] & lo_m, v[1] & lo_m, v[2] & lo_m, v[3] & lo_m});
+                }
+            }
         } else {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -448,8 +481,20 @@ paged_decode_kernel(DecodeParams p) {
                                __builtin_amdgcn_readfirstlane(plan.last_cut);
         const bool whole = !cut_before && !cut_after;
         const int slot = cut_before ? 2 * w : 2 * w + 1;
-        const float l_tot = sum_over_groups(l_part);
-        const float z_tot = (FMT == FMT_TQ) ? sum_over_groups(z_part) : 0.0f;
+        float l_tot = sum_over_groups(l_part);
+        float z_tot = (FMT == FMT_TQ) ? sum_over_groups(z_part) : 0.0f;
+        if constexpr (HALF) {
+            // columns r16 and r16 ^ 8 hold the same head; O rows m and m + 8
+            // (lane groups grp and grp + 2) too
+            l_tot += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, l_tot), 0x128, 0xf, 0xf, false));
+            z_tot += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, z_tot), 0x128, 0xf, 0xf, false));
+            // (a lane-permute read per element: a loop of permlane32 swaps is
+            // miscompiled by this toolchain, which reuses one swap's result)
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) oacc[c][i] += __shfl_xor(oacc[c][i], 32, 64);
+        }
         const f32x4 lh4 = gather4_from_row0(l_tot, wscr, r16, grp);
         const f32x4 zh4 = gather4_from_row0(z_tot, wscr + 16, r16, grp);
         const f32x4 mh4 = gather4_from_row0(m_run, wscr + 32, r16, grp);
@@ -527,16 +572,32 @@ paged_decode_kernel(DecodeParams p) {
     // buffer; lanes past the page issue nothing.  Past the chunk's last page
     // (i >= npc) block 0 is re-read (every workgroup shares it, so it stays
     // in the cache) into a buffer no step reads.
-    uint32_t dma_off[SPP];  // loop-invariant byte offset of this lane's chunks
+    // TurboQuant (NHD pages: token rows of Hkv slots): the buffer holds this
+    // group's run of every token row, [t*row + hg*run, +run), as a window of
+    // NC 16-byte chunks starting at the run's 16-byte-aligned start; window
+    // chunk j of token t sits at LDS offset 16 * (t*NC + j).  The run starts
+    // mis(t) = (t*row + hg*run) % 16 bytes into its window.  Chunks past the
+    // page end (the last window's tail) re-read the page's last chunk; they
+    // are never read back.
+    constexpr int SPT = GE::spt;
+    const int tq_nc = p.tq_nc, run_bytes = p.hpw * GE::entry;
+    auto run_mis = [&](int t) { return (t * p.row_bytes + hg * run_bytes) & 15; };
+    uint32_t dma_off[SPT];  // loop-invariant source offset of this lane's chunks in the page
+    bool dma_on[SPT];
 #pragma unroll
-    for (int c = 0; c < SPP; ++c) dma_off[c] = 16u * (uint32_t)(c * nthreads + tid);
+    for (int c = 0; c < SPT; ++c) {
+        const int q = c * nthreads + tid, t = q / max(tq_nc, 1), j = q - t * tq_nc;
+        const int a = ((t * p.row_bytes + hg * run_bytes) & ~15) + 16 * j;
+        dma_on[c] = FMT == FMT_TQ && t < kBs;
+        dma_off[c] = (uint32_t)min(a, (int)page_bytes - 16);
+    }
     auto dma_page = [&](int i, int buf) __attribute__((always_inline)) {
         const int32_t blk = i < npc ? max(bt_lds[i], 0) : 0;
         const uint8_t* src = p.kc + (int64_t)__builtin_amdgcn_readfirstlane(blk) * page_bytes;
 #pragma unroll
-        for (int c = 0; c < SPP; ++c) {
+        for (int c = 0; c < SPT; ++c) {
             uint8_t* dst = smem + buf * GE::kBuf + 16 * (c * nthreads + 64 * wave);
-            if ((int)dma_off[c] < (int)page_bytes)
+            if (dma_on[c])
                 __builtin_amdgcn_global_load_lds(
                     (const void __attribute__((address_space(1)))*)(src + dma_off[c]),
                     (void __attribute__((address_space(3)))*)dst, 16, 0, 0);
@@ -546,10 +607,15 @@ paged_decode_kernel(DecodeParams p) {
     // loop-invariant LDS offsets of this lane's entries inside a page
     // (staged in LDS, or in HBM for f16/bf16):
     // K of token r16, V of tokens 4*grp + i
-    const int k_off = entry_off<FMT>(r16, g, Hkv, GE::entry, hnd);
+    // (TurboQuant: this group's window layout, local head = wave)
+    auto lds_entry = [&](int t) {
+        return FMT == FMT_TQ ? t * tq_nc * 16 + run_mis(t) + wave * GE::entry
+                             : entry_off<FMT>(t, g, Hkv, GE::entry, hnd);
+    };
+    const int k_off = lds_entry(r16);
     int v_off[4];
 #pragma unroll
-    for (int i2 = 0; i2 < 4; ++i2) v_off[i2] = entry_off<FMT>(4 * grp + i2, g, Hkv, GE::entry, hnd);
+    for (int i2 = 0; i2 < 4; ++i2) v_off[i2] = lds_entry(4 * grp + i2);
 
     // direct formats: per-lane operand registers for one page
     u32x4 kreg[4], vreg[4];
@@ -655,11 +721,13 @@ paged_decode_kernel(DecodeParams p) {
             for (int i2 = 0; i2 < 4; ++i2) {
                 const uint8_t* cr = pg[pp] + vc_al[i2];
                 cw[i2] = lds16(cr) | (lds16(cr + 2) << 16);
-                const uint8_t* ve = pg[pp] + v_off[i2] + GE::key_packed + GE::val_data;
-                vsc[pp][i2] = (uint16_t)lds16(ve);
-                vzr[pp][i2] = (uint16_t)lds16(ve + 2);
+                if constexpr (!HALF) {
+                    const uint8_t* ve = pg[pp] + v_off[i2] + GE::key_packed + GE::val_data;
+                    vsc[pp][i2] = (uint16_t)lds16(ve);
+                    vzr[pp][i2] = (uint16_t)lds16(ve + 2);
+                }
             }
-            if constexpr (kMasked) {  // tokens past the end may hold anything
+            if constexpr (kMasked && !HALF) {  // tokens past the end may hold anything
 #pragma unroll
                 for (int i2 = 0; i2 < 4; ++i2) {
                     const bool ok = 4 * grp + i2 < nvp[pp];
@@ -698,6 +766,85 @@ paged_decode_kernel(DecodeParams p) {
                 }
             }
         }
+        if constexpr (HALF) {
+        // ---- S^T: column c < 8 is head c on the first page, c >= 8 head c - 8
+        // on the second (block-diagonal Q^T, one accumulator)
+        f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sacc = mfma16x16x32(a[0][j], qb[j], sacc);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sacc = mfma16x16x32(a[1][j], qb[4 + j], sacc);
+        // this lane's page: scale and zero of its tokens 4*grp + i, valid count
+        const uint8_t* vpg = smem + BUF0 * GE::kBuf + (r16 >= 8 ? GE::kBuf : 0);
+        uint16_t hs[4], hz[4];
+#pragma unroll
+        for (int i2 = 0; i2 < 4; ++i2) {
+            const uint8_t* ve = vpg + v_off[i2] + GE::key_packed + GE::val_data;
+            hs[i2] = (uint16_t)lds16(ve);
+            hz[i2] = (uint16_t)lds16(ve + 2);
+        }
+        wscr[diag_slot] = rowf[0];
+        wscr[32 + diag_slot] = rowf[1];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const f32x4 rf = *reinterpret_cast<const f32x4*>(wscr + (r16 >= 8 ? 32 : 0) + 4 * grp);
+        __builtin_amdgcn_wave_barrier();
+        float sv[4];
+#pragma unroll
+        for (int i2 = 0; i2 < 4; ++i2) sv[i2] = sacc[i2] * rf[i2];
+        if constexpr (kMasked) {
+            const int nvl = r16 >= 8 ? nv1 : nv0;
+#pragma unroll
+            for (int i2 = 0; i2 < 4; ++i2) {
+                const bool ok = 4 * grp + i2 < nvl;
+                sv[i2] = ok ? sv[i2] : kNegInf;
+                hs[i2] = ok ? hs[i2] : (uint16_t)0;
+                hz[i2] = ok ? hz[i2] : (uint16_t)0;
+            }
+        }
+        // Lazy reference max (see below); a head's max spans columns c, c ^ 8
+        const float mloc = vmax(vmax(sv[0], sv[1]), vmax(sv[2], sv[3]));
+        if (__ballot(mloc > m_thr)) {  // wave-uniform
+            float mx = vmax_over_groups(mloc);
+            mx = vmax(mx, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, mx), 0x128, 0xf, 0xf, false)));
+            const bool upd = mx > m_thr;  // the same in every lane of the head
+            const float m_new = upd ? mx : m_run;
+            const float alpha = upd ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;  // 0 when m_run = -inf
+            l_part *= alpha;
+            z_part *= alpha;
+            // O row m belongs to the head of column m
+            const f32x4 al = gather4_from_row0(alpha, wscr + 64, r16, grp);
+#pragma unroll
+            for (int i2 = 0; i2 < 4; ++i2)
+#pragma unroll
+                for (int c = 0; c < 8; ++c) oacc[c][i2] *= al[i2];
+            m_run = m_new;
+            m_thr = m_run + 8.0f;
+        }
+        const float m_use = m_run == kNegInf ? 0.0f : m_run;
+        float psum = 0.0f, zsum = 0.0f;
+        f16x4 pw;
+#pragma unroll
+        for (int i2 = 0; i2 < 4; ++i2) {
+            const float pv = __builtin_amdgcn_exp2f(sv[i2] - m_use);
+            psum += pv;
+            zsum = __builtin_fmaf(pv, (float)__builtin_bit_cast(_Float16, hz[i2]), zsum);
+            pw[i2] = (_Float16)__builtin_fmaf(pv, (float)__builtin_bit_cast(_Float16, hs[i2]), 0.0f);
+        }
+        l_part += psum;
+        z_part += zsum;
+        // ---- O += P . V: rows 0-7 take k = 8*grp + i (first page, token
+        // 4*grp + i), rows 8-15 k = 8*grp + 4 + i (second page)
+        const u32x2 pw2 = __builtin_bit_cast(u32x2, pw);
+        const uint32_t lo_m = r16 < 8 ? ~0u : 0u;
+        const AT pa = __builtin_bit_cast(AT, u32x4{pw2[0] & lo_m, pw2[1] & lo_m, pw2[0] & ~lo_m, pw2[1] & ~lo_m});
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const AT vb = __builtin_bit_cast(AT, u32x4{bop[0][c][0], bop[0][c][1], bop[1][c][0], bop[1][c][1]});
+            oacc[c] = mfma16x16x32(pa, vb, oacc[c]);
+        }
+        } else {
         // ---- S^T = K . Q^T per page, times the per-token factor
         f32x4 sacc[2];
 #pragma unroll
@@ -769,6 +916,7 @@ paged_decode_kernel(DecodeParams p) {
         for (int c = 0; c < 8; ++c) {
             const AT vb = __builtin_bit_cast(AT, u32x4{bop[0][c][0], bop[0][c][1], bop[1][c][0], bop[1][c][1]});
             oacc[c] = mfma16x16x32(pa, vb, oacc[c]);
+        }
         }
         }
     };
@@ -973,11 +1121,11 @@ paged_decode_kernel(DecodeParams p) {
             // clobber keeps LDS reads below it.  A pair that a piece boundary
             // splits runs twice, each time with one slot masked.
             constexpr int NB = GE::nbuf, NPH = NB / 2;
-            static_assert(NB == PF + 2 && NB % 2 == 0 && PF <= 4 && SPP <= 3, "pair steps over an even ring");
+            static_assert(NB == PF + 2 && NB % 2 == 0 && PF <= 4 && SPT <= 3, "pair steps over an even ring");
             // transfers this wave issues per page (its first lane decides)
             int nw = 0;
 #pragma unroll
-            for (int c = 0; c < SPP; ++c) nw += (int)dma_off[c] - 16 * lane < (int)page_bytes;
+            for (int c = 0; c < SPT; ++c) nw += c * nthreads + 64 * wave < kBs * tq_nc;
             nw = __builtin_amdgcn_readfirstlane(nw);
 #pragma unroll
             for (int s2 = 0; s2 < PF; ++s2) dma_page(s2, s2);
@@ -1199,12 +1347,28 @@ int flat_grid(int B, int Hkv, int max_blocks, int max_splits, int cus) {
     return (int)std::max<int64_t>(1, n);
 }
 
+// TurboQuant: KV heads per workgroup (one wave each) -- at most 4, so two
+// workgroups fit a CU (LDS) and the two waves on each SIMD belong to
+// different workgroups; 0 when Hkv cannot be split that way
+int tq_heads_per_group(int Hkv) { return Hkv <= 4 ? Hkv : (Hkv % 2 == 0 && Hkv / 2 <= 4 ? Hkv / 2 : 1); }
+
+// TurboQuant page ranges: two resident workgroups per CU, fewer for small
+// batches; never more than flat_grid's count (the workspace is sized by it)
+int tq_ranges(int B, int Hkv, int max_blocks, int max_splits, int cus) {
+    const int hgroups = Hkv / tq_heads_per_group(Hkv);
+    int64_t n = std::max<int64_t>(1, (int64_t)cus * 2 / hgroups);
+    n = std::min<int64_t>(n, ((int64_t)B * max_blocks + kPpsMin - 1) / kPpsMin);
+    if (max_splits > 1) n = std::min<int64_t>(n, (int64_t)B * max_splits);
+    n = std::min<int64_t>(n, flat_grid(B, Hkv, max_blocks, max_splits, cus));
+    return (int)std::max<int64_t>(1, n);
+}
+
 size_t workspace_bytes_for(int B, int Hq, int Hkv, int max_blocks, int max_splits, int cus) {
     if (max_splits == 1) return 0;
     return (size_t)2 * flat_grid(B, Hkv, max_blocks, max_splits, cus) * Hq * (kD + 2) * sizeof(float);
 }
 
-template <int FMT, int KB, int VB, bool MBF16>
+template <int FMT, int KB, int VB, bool MBF16, bool HALF = false>
 int launch_decode(DecodeParams& prm, hipStream_t stream) {
     using GE = Geo<FMT, KB, VB>;
     // the compile-time geometry must be the one the caller described
@@ -1212,9 +1376,19 @@ int launch_decode(DecodeParams& prm, hipStream_t stream) {
                                                            prm.key_packed != GE::key_packed ||
                                                            prm.val_data != GE::val_data)))
         return VMC_EINVAL;
-    auto kern = paged_decode_kernel<FMT, KB, VB, MBF16>;
-    prm.grid = prm.per_seq ? prm.B : flat_grid(prm.B, prm.Hkv, prm.max_blocks, prm.max_splits, num_cus());
-    hipLaunchKernelGGL(kern, dim3(prm.grid), dim3(64 * prm.Hkv), 0, stream, prm);
+    auto kern = paged_decode_kernel<FMT, KB, VB, MBF16, HALF>;
+    if constexpr (FMT == FMT_TQ) {
+        prm.hpw = tq_heads_per_group(prm.Hkv);
+        prm.hgroups = prm.Hkv / prm.hpw;
+        prm.row_bytes = prm.Hkv * GE::entry;
+        prm.tq_nc = GE::nc_of(prm.hpw);
+        prm.grid = prm.per_seq ? prm.B : tq_ranges(prm.B, prm.Hkv, prm.max_blocks, prm.max_splits, num_cus());
+    } else {
+        prm.hpw = prm.Hkv;
+        prm.hgroups = 1;
+        prm.grid = prm.per_seq ? prm.B : flat_grid(prm.B, prm.Hkv, prm.max_blocks, prm.max_splits, num_cus());
+    }
+    hipLaunchKernelGGL(kern, dim3(prm.grid * prm.hgroups), dim3(64 * prm.hpw), 0, stream, prm);
     VMC_LAUNCH_CHECK();
     if (!prm.per_seq) {
         hipLaunchKernelGGL(decode_merge_kernel, dim3(prm.B, prm.Hkv), dim3(64 * prm.G), 0, stream, prm);
@@ -1344,8 +1518,13 @@ extern "C" int vmc_turboquant_decode_attention(void* output, const void* query, 
     if ((prm.page_bytes % 16) != 0) return VMC_EINVAL;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int kb = cfg->key_quant_bits, vb = cfg->value_quant_bits;
-    if (kb == 4 && vb == 4) return launch_decode<FMT_TQ, 4, 4, false>(prm, s);
-    if (kb == 3 && vb == 3) return launch_decode<FMT_TQ, 3, 3, false>(prm, s);
-    if (kb == 3 && vb == 4) return launch_decode<FMT_TQ, 3, 4, false>(prm, s);
+    // at most 8 query heads per KV head: two pages share the S tile's columns
+    const bool half = prm.G <= 8;
+    if (kb == 4 && vb == 4)
+        return half ? launch_decode<FMT_TQ, 4, 4, false, true>(prm, s) : launch_decode<FMT_TQ, 4, 4, false>(prm, s);
+    if (kb == 3 && vb == 3)
+        return half ? launch_decode<FMT_TQ, 3, 3, false, true>(prm, s) : launch_decode<FMT_TQ, 3, 3, false>(prm, s);
+    if (kb == 3 && vb == 4)
+        return half ? launch_decode<FMT_TQ, 3, 4, false, true>(prm, s) : launch_decode<FMT_TQ, 3, 4, false>(prm, s);
     return VMC_EINVAL;
 }
