@@ -54,15 +54,6 @@ constexpr float kNegInf = -__builtin_inff();
 
 enum { FMT_F16 = 0, FMT_BF16 = 1, FMT_Q8_0 = 2, FMT_Q4_0 = 3, FMT_TQ = 4 };
 
-template <typename F, int... I>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
-    (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-    static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
 // Compile-time geometry of a page format (head_dim 128, block 16, at most 8
 // KV heads): TurboQuant slot fields (kernels_turboquant.h:29-45), GGUF entry
 // sizes, and the staging of LDS-staged formats -- SPP 16-byte chunks per

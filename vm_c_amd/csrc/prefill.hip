@@ -30,11 +30,9 @@ namespace vmc {
 namespace {
 
 constexpr int kD = 128;
-constexpr int BM = 128;    // query rows per workgroup
+constexpr int NW = 8;      // waves per workgroup (32 query rows each)
 constexpr int BN = 64;     // kv rows per tile
-constexpr int PITCH = 272; // LDS bytes per K/V row
-constexpr int TILE_BYTES = BN * PITCH;
-constexpr int LDS_BYTES = 4 * TILE_BYTES + 2 * 4 * 32 * 4;
+constexpr int NSLOT = 3;   // K/V tile slots in LDS
 constexpr float kNegInf = -__builtin_inff();
 
 struct PrefillParams {
@@ -45,7 +43,9 @@ struct PrefillParams {
     const int32_t* pos;
     int T, Hq, Hkv, G;
     float scale_log2;
-    int ntiles;
+    int ntiles;          // query blocks of qb rows
+    int hw, rb, qb;      // heads per workgroup, 32-row blocks per head, rows per block
+    int hgroups;         // workgroups per KV head and query block (G / hw)
     // fused append
     uint8_t* kc;
     uint8_t* vc;
@@ -80,42 +80,63 @@ __device__ __forceinline__ V8 as_v8(u32x4 w) {
     return __builtin_bit_cast(V8, w);
 }
 
+// All LDS of the kernel: two K/V tile slots (rows of 256 B, 16-byte chunk
+// ch of row r stored at chunk position ch ^ swz(r)), then the per-wave
+// exchange.  swz(r) rotates the low 4 row bits by two: a bijection on 16
+// consecutive rows (the 32-row K operand reads spread over all banks) whose
+// bits 2-3 differ for 4 consecutive rows (a transpose read of 4 rows x 4
+// chunks spreads too).
+struct PrefillLds {
+    uint8_t tile[NSLOT][2][BN * 256];  // [slot][K, V][row][position]
+    float scratch[2][NW][32];          // [alpha, l][wave][row]
+};
+
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+// Workgroup = 8 waves = hw query heads of one KV head x rb blocks of 32
+// query rows (hw * rb = 8): every K/V tile in LDS serves 256 query rows,
+// which halves the tile traffic from L2 against 4-wave, one-head
+// workgroups.  Grid: query block (largest first) x KV head x head group.
 template <bool BF16, int APPEND_FMT>
-__global__ void __launch_bounds__(256, 2)
+__global__ void __launch_bounds__(512, 1)
 prefill_kernel(PrefillParams p) {
     using M = MT<BF16>;
     using V8 = typename M::v8;
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    uint8_t* kbuf = smem;                      // [2][BN][PITCH]
-    uint8_t* vbuf = smem + 2 * TILE_BYTES;     // [2][BN][PITCH]
-    float* scratch = reinterpret_cast<float*>(smem + 4 * TILE_BYTES);  // [4 waves][32]
+    __shared__ PrefillLds lds;
 
     const int tid = threadIdx.x;
     const int w = tid >> 6, lane = tid & 63;
     const int c32 = lane & 31, h = lane >> 5;
-    const int hq = blockIdx.x % p.Hq;
-    const int tile = p.ntiles - 1 - (int)(blockIdx.x / p.Hq);
-    const int g = hq / p.G;
+    const int per_blk = p.Hkv * p.hgroups;
+    const int qblk = p.ntiles - 1 - (int)(blockIdx.x / per_blk);
+    const int gi = (int)blockIdx.x % per_blk;
+    const int g = gi / p.hgroups, hgrp = gi % p.hgroups;
+    const int hq = g * p.G + hgrp * p.hw + w / p.rb;  // this wave's query head
     const int T = p.T;
-    const int q0 = tile * BM;
+    const int q0 = qblk * p.qb;
 
     // kv range of the whole workgroup
     const int kv_lo = max(0, q0 - p.pos[q0]);
-    const int kv_end = min(q0 + BM, T);
+    const int kv_end = min(q0 + p.qb, T);
     const int ntile = (kv_end - kv_lo + BN - 1) / BN;
 
     // this lane's query row and its key window [lo, row]
-    const int row = q0 + 32 * w + c32;
+    const int wr = 32 * (w % p.rb);  // this wave's rows: q0 + wr .. +31
+    const int row = q0 + wr + c32;
     const bool row_ok = row < T;
     const int lo = row_ok ? row - p.pos[row] : 0;
     // wave-uniform bounds
-    const int wrow0 = q0 + 32 * w;
+    const int wrow0 = q0 + wr;
     const bool wave_ok = wrow0 < T;
     const int wrow1 = min(wrow0 + 31, T - 1);
     const int wlo0 = wave_ok ? wrow0 - p.pos[wrow0] : 0;
     const int wlo1 = wave_ok ? wrow1 - p.pos[wrow1] : 0;
 
-    // ---- Q^T operand: lane (col = row, half h) holds dims 16s + 8h .. +7
+    // ---- Q^T operand: lane (col = row, half h) holds dims 16s + 8h .. +7.
+    // A negative scale flips Q's sign bits (exact) so that c = |scale| log2 e
+    // is positive and the largest raw score is the largest scaled one.
+    const float csc = fabsf(p.scale_log2);
+    const uint32_t qflip = p.scale_log2 < 0.0f ? 0x80008000u : 0u;
     V8 qb[8];
     {
         const uint16_t* qp = p.q + ((int64_t)row * p.Hq + hq) * kD + 8 * h;
@@ -123,7 +144,7 @@ prefill_kernel(PrefillParams p) {
         for (int s = 0; s < 8; ++s) {
             u32x4 wv = {0u, 0u, 0u, 0u};
             if (row_ok) wv = *reinterpret_cast<const u32x4*>(qp + 16 * s);
-            qb[s] = as_v8<V8>(wv);
+            qb[s] = as_v8<V8>(u32x4{wv[0] ^ qflip, wv[1] ^ qflip, wv[2] ^ qflip, wv[3] ^ qflip});
         }
     }
 
@@ -132,109 +153,105 @@ prefill_kernel(PrefillParams p) {
     for (int m = 0; m < 4; ++m)
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[m][i] = 0.0f;
-    float m_run = kNegInf, l_part = 0.0f;
+    // m_run: the row's reference max (log2 units); it moves only when a score
+    // exceeds it by more than 8, so P <= 256 and most tiles skip the rescale
+    float m_run = kNegInf, m_thr = kNegInf, l_part = 0.0f;
 
-    // ---- staging: 1024 16-byte chunks per tensor per tile, 4 per thread
-    u32x4 stk[4], stv[4];
-    auto stage_load = [&](int t) {
+    // ---- tile loads: load-to-LDS, 2 rounds of 32 rows per tensor; lane
+    // (wave w, lane L) of round i fills row 32 i + 4 w + L / 16 at chunk
+    // position L % 16, i.e. source chunk (L % 16) ^ swz(row)
+    const int ld_row = 4 * w + (lane >> 4);
+    const uint32_t ld_col = 16u * (uint32_t)((lane & 15) ^ swz(ld_row));
+    const int64_t row_stride = (int64_t)p.Hkv * kD * 2;  // bytes between kv rows
+    const uint8_t* kg = reinterpret_cast<const uint8_t*>(p.k) + (int64_t)g * kD * 2 + ld_col;
+    const uint8_t* vg = reinterpret_cast<const uint8_t*>(p.v) + (int64_t)g * kD * 2 + ld_col;
+    auto load_tile = [&](int t, auto slot_c) __attribute__((always_inline)) {
+        constexpr int SL = decltype(slot_c)::value;
         const int k0 = kv_lo + t * BN;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = tid + 256 * i;
-            const int r = c >> 4, ch = c & 15;
-            const int kk = k0 + r;
-            stk[i] = u32x4{0u, 0u, 0u, 0u};
-            stv[i] = u32x4{0u, 0u, 0u, 0u};
-            if (kk < kv_end) {
-                const int64_t off = ((int64_t)kk * p.Hkv + g) * kD + ch * 8;
-                stk[i] = *reinterpret_cast<const u32x4*>(p.k + off);
-                stv[i] = *reinterpret_cast<const u32x4*>(p.v + off);
-                if constexpr (BF16) {
-                    // PV runs in fp16 (P keeps 11 mantissa bits): V bf16 -> fp16,
-                    // exact for |v| in [2^-14, 65504]
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const uint32_t x = stv[i][e];
-                        stv[i][e] = (uint32_t)f32_to_f16_bits(bf16_bits_to_f32((uint16_t)(x & 0xffff))) |
-                                    ((uint32_t)f32_to_f16_bits(bf16_bits_to_f32((uint16_t)(x >> 16))) << 16);
-                    }
-                }
-            }
-        }
-    };
-    auto stage_store = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = tid + 256 * i;
-            const int r = c >> 4, ch = c & 15;
-            *reinterpret_cast<u32x4*>(kbuf + buf * TILE_BYTES + r * PITCH + ch * 16) = stk[i];
-            *reinterpret_cast<u32x4*>(vbuf + buf * TILE_BYTES + r * PITCH + ch * 16) = stv[i];
+        for (int i = 0; i < 2; ++i) {
+            // rows past the range re-read the last row (masked later)
+            const int kk = min(k0 + 32 * i + ld_row, kv_end - 1);
+            const int64_t off = (int64_t)kk * row_stride;
+            __builtin_amdgcn_global_load_lds(
+                (const void __attribute__((address_space(1)))*)(kg + off),
+                (void __attribute__((address_space(3)))*)(&lds.tile[SL][0][1024 * (8 * i + w)]), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(
+                (const void __attribute__((address_space(1)))*)(vg + off),
+                (void __attribute__((address_space(3)))*)(&lds.tile[SL][1][1024 * (8 * i + w)]), 16, 0, 0);
         }
     };
 
-    stage_load(0);
-    stage_store(0);
-    __syncthreads();
+    // ---- loop-invariant LDS read offsets
+    // K (S^T A operand): lane reads row 32 kb + c32, chunk 2 s + h
+    int k_rd[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) k_rd[s] = c32 * 256 + 16 * ((2 * s + h) ^ swz(c32));
+    // V (PV B operand) by transpose reads: lane group G = lane / 16 covers kv
+    // rows 16 c + 8 s + 4 (G / 2) + e (e = 0..3, one per lane quad) and dims
+    // 32 m + 16 (G % 2) + 4 q; the lane then holds dim 32 m + lane % 32 of
+    // those 4 rows.  One offset per (m, s): the chunk position depends on both
+    // through the swizzle.
+    const int G = lane >> 4, jq = lane & 15, e4 = jq >> 2, q4 = jq & 3;
+    const int hv = G >> 1;
+    int v_rd[4][2];
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const int r = 8 * s + 4 * hv + e4;                     // row within 16
+            const int chunk = 4 * m + 2 * (G & 1) + (q4 >> 1);
+            v_rd[m][s] = r * 256 + 16 * (chunk ^ swz(r)) + 8 * (q4 & 1);
+        }
 
-    for (int t = 0; t < ntile; ++t) {
-        const int buf = t & 1;
-        if (t + 1 < ntile) stage_load(t + 1);
+    auto process = [&](int t, auto slot_c) __attribute__((always_inline)) {
+        constexpr int SL = decltype(slot_c)::value;
         const int k0 = kv_lo + t * BN;
         // skip: tile entirely after this wave's last row, or before its first window
         const bool active = wave_ok && k0 <= wrow1 && k0 + BN - 1 >= wlo0;
-        if (active) {
-            const uint8_t* kt = kbuf + buf * TILE_BYTES;
-            const uint8_t* vt = vbuf + buf * TILE_BYTES;
-            const bool need_mask = (k0 + BN - 1 > wrow0) || (k0 < wlo1);
-            // ---- S^T = K Q^T, two 32-row kv blocks
-            f32x16 sacc[2];
+        if (!active) return;
+        const uint8_t* kt = lds.tile[SL][0];
+        const uint8_t* vt = lds.tile[SL][1];
+        const bool need_mask = (k0 + BN - 1 > wrow0) || (k0 < wlo1);
+        // ---- S^T = K Q^T, two 32-row kv blocks
+        f32x16 sacc[2];
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+        for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-                for (int i = 0; i < 16; ++i) sacc[kb][i] = 0.0f;
-                const uint8_t* kr = kt + (kb * 32 + c32) * PITCH + 16 * h;
+            for (int i = 0; i < 16; ++i) sacc[kb][i] = 0.0f;
 #pragma unroll
-                for (int s = 0; s < 8; ++s) {
-                    const u32x4 a = *reinterpret_cast<const u32x4*>(kr + 32 * s);
-                    sacc[kb] = M::mma(as_v8<V8>(a), qb[s], sacc[kb]);
-                }
+            for (int s = 0; s < 8; ++s) {
+                const u32x4 a = *reinterpret_cast<const u32x4*>(kt + kb * 32 * 256 + k_rd[s]);
+                sacc[kb] = M::mma(as_v8<V8>(a), qb[s], sacc[kb]);
             }
-            // ---- online softmax (log2 domain), one query row per lane column
-            float mx = kNegInf;
+        }
+        // ---- online softmax (log2 domain), one query row per lane column;
+        // masked scores become -inf (only tiles that cross a window edge)
+        if (need_mask) {
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int j = 0; j < 16; ++j) {
-                    float sv = sacc[kb][j] * p.scale_log2;
-                    if (need_mask) {
-                        const int kv = k0 + kb * 32 + 8 * (j >> 2) + 4 * h + (j & 3);
-                        sv = (kv <= row && kv >= lo && row_ok) ? sv : kNegInf;
-                    }
-                    sacc[kb][j] = sv;
-                    mx = fmaxf(mx, sv);
+                    const int kv = k0 + kb * 32 + 8 * (j >> 2) + 4 * h + (j & 3);
+                    const bool ok = kv <= row && kv >= lo && row_ok;
+                    sacc[kb][j] = ok ? sacc[kb][j] : kNegInf;
                 }
-            mx = fmaxf(mx, shfl_xor(mx, 32));
-            const float m_new = fmaxf(m_run, mx);
-            const float m_use = m_new == kNegInf ? 0.0f : m_new;
-            const float alpha = exp2f(m_run - m_use);
+        }
+        float mloc = kNegInf;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) mloc = fmaxf(mloc, sacc[kb][j]);
+        if (__ballot(mloc * csc > m_thr)) {  // wave-uniform; rare after the first tiles
+            const float mrow = fmaxf(mloc, shfl_xor(mloc, 32)) * csc;
+            const bool upd = mrow > m_thr;  // the same in both halves of the row
+            const float m_new = upd ? mrow : m_run;
+            const float alpha = upd ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;  // 0 from -inf
+            l_part *= alpha;
             m_run = m_new;
-            // P as MFMA A operands, chunk c = kv rows 16c .. 16c+15
-            uint32_t pw[4][4];
-            float psum = 0.0f;
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-#pragma unroll
-                for (int e = 0; e < 8; e += 2) {
-                    const int kb = c >> 1;
-                    const int j0 = 4 * (2 * (c & 1) + (e >> 2)) + (e & 3);
-                    const uint16_t b0 = f32_to_f16_bits(exp2f(sacc[kb][j0] - m_use));
-                    const uint16_t b1 = f32_to_f16_bits(exp2f(sacc[kb][j0 + 1] - m_use));
-                    psum += f16_bits_to_f32(b0) + f16_bits_to_f32(b1);
-                    pw[c][e >> 1] = (uint32_t)b0 | ((uint32_t)b1 << 16);
-                }
-            l_part = __builtin_fmaf(l_part, alpha, psum);
-            // ---- rescale O rows by their query rows' alpha (rows 8b + 4h + i)
-            float* sc = scratch + w * 32;
+            m_thr = m_run + 8.0f;
+            // rescale O rows by their query rows' alpha (rows 8b + 4h + i)
+            float* sc = lds.scratch[0][w];
             if (h == 0) sc[c32] = alpha;
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
@@ -251,37 +268,95 @@ prefill_kernel(PrefillParams p) {
             for (int m = 0; m < 4; ++m)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) o[m][i] *= al[i];
-            // ---- O += P V
+        }
+        const float m_use = m_run == kNegInf ? 0.0f : m_run;
+        // P = 2^(s c - m) in fp16 (11 bits, also for bf16 inputs) as MFMA A
+        // operands, chunk c = kv rows 16c .. 16c+15; the row sum adds the
+        // rounded values the MFMA uses
+        uint32_t pw[4][4];
+        float psum = 0.0f;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const f16x8 pa = as_v8<f16x8>(u32x4{pw[c][0], pw[c][1], pw[c][2], pw[c][3]});
-                u32x2 vv[8];
+        for (int c = 0; c < 4; ++c)
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int kv = 16 * c + 8 * (e >> 2) + 4 * h + (e & 3);
-                    vv[e] = *reinterpret_cast<const u32x2*>(vt + kv * PITCH + 8 * c32);
-                }
+            for (int e = 0; e < 8; e += 2) {
+                const int kb = c >> 1;
+                const int j0 = 4 * (2 * (c & 1) + (e >> 2)) + (e & 3);
+                const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][j0], csc, -m_use));
+                const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][j0 + 1], csc, -m_use));
+                const f16x2 ph = {(_Float16)p0, (_Float16)p1};
+                psum = __builtin_amdgcn_fdot2(ph, f16x2{(_Float16)1.0f, (_Float16)1.0f}, psum, false);
+                pw[c][e >> 1] = __builtin_bit_cast(uint32_t, ph);
+            }
+        l_part += psum;
+        // ---- O += P V (fp16): k = 8h + e <-> kv 16c + 8(e/4) + 4h + e%4 (the
+        // S^T registers' order); V arrives transposed, output column n = dim 32m + n
 #pragma unroll
-                for (int m = 0; m < 4; ++m) {
-                    u32x4 bw;
+        for (int c = 0; c < 4; ++c) {
+            const f16x8 pa = as_v8<f16x8>(u32x4{pw[c][0], pw[c][1], pw[c][2], pw[c][3]});
 #pragma unroll
-                    for (int e2 = 0; e2 < 4; ++e2) {
-                        const uint32_t lo16 = (vv[2 * e2][m >> 1] >> (16 * (m & 1))) & 0xffffu;
-                        const uint32_t hi16 = (vv[2 * e2 + 1][m >> 1] >> (16 * (m & 1))) & 0xffffu;
-                        bw[e2] = lo16 | (hi16 << 16);
-                    }
-                    o[m] = MT<false>::mma(pa, as_v8<f16x8>(bw), o[m]);
-                }
+            for (int m = 0; m < 4; ++m) {
+                const int off0 = v_rd[m][0] + c * 16 * 256;
+                const int off1 = v_rd[m][1] + c * 16 * 256;
+                const s16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4*)(vt + off0));
+                const s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4*)(vt + off1));
+                const u32x2 l2 = __builtin_bit_cast(u32x2, lo4), h2 = __builtin_bit_cast(u32x2, hi4);
+                o[m] = MT<false>::mma(pa, as_v8<f16x8>(u32x4{l2[0], l2[1], h2[0], h2[1]}), o[m]);
             }
         }
-        if (t + 1 < ntile) stage_store(buf ^ 1);
-        __syncthreads();
-    }
+    };
 
-    // ---- normalise and store: lane holds rows 8b + 4h + i, dims 4*c32 .. +3
+    // bf16 inputs: PV runs in fp16, so each wave converts the V chunks its
+    // own transfers wrote (exact for |v| in [2^-14, 65504]) before the barrier
+    auto v_to_f16 = [&](auto slot_c) __attribute__((always_inline)) {
+        constexpr int SL = decltype(slot_c)::value;
+        if constexpr (BF16) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                u32x4* pv = reinterpret_cast<u32x4*>(&lds.tile[SL][1][1024 * (8 * i + w) + 16 * lane]);
+                const u32x4 x = *pv;
+                u32x4 y;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const f16x2 hh = {(_Float16)__builtin_bit_cast(float, x[e] << 16),
+                                      (_Float16)__builtin_bit_cast(float, x[e] & 0xffff0000u)};
+                    y[e] = __builtin_bit_cast(uint32_t, hh);
+                }
+                *pv = y;
+            }
+        }
+    };
+
+    // ---- NSLOT LDS slots: tile t in slot t % NSLOT; the next NSLOT - 1 tiles
+    // are in flight while t runs.  Before tile t each wave waits until only
+    // the transfers of tiles t+1 .. t+NSLOT-2 are outstanding (4 per tile:
+    // vmcnt retires loads in order), converts its own V chunks, and the
+    // barrier makes the tile visible and shows slot (t-1) % NSLOT free, which
+    // then receives tile t + NSLOT - 1.
+    static_assert(NSLOT == 3, "wait counts below assume three slots");
+    load_tile(0, std::integral_constant<int, 0>{});
+    if (1 < ntile) load_tile(1, std::integral_constant<int, 1>{});
+    for (int t0 = 0; t0 < ntile; t0 += NSLOT) {
+        static_for<NSLOT>([&](auto sc) __attribute__((always_inline)) {
+            constexpr int S = decltype(sc)::value;
+            const int t = t0 + S;
+            if (t < ntile) {  // uniform over the workgroup
+                if (t + 1 < ntile) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+                else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                v_to_f16(sc);
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                if (t + 2 < ntile) load_tile(t + 2, std::integral_constant<int, (S + 2) % NSLOT>{});
+                process(t, sc);
+            }
+        });
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    // ---- normalise and store: lane holds rows 8b + 4h + i, dims 32m + c32
     {
         const float l_tot = l_part + shfl_xor(l_part, 32);
-        float* sc = scratch + 4 * 32 + w * 32;
+        float* sc = lds.scratch[1][w];
         if (h == 0) sc[c32] = l_tot;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -294,23 +369,20 @@ prefill_kernel(PrefillParams p) {
                 const int r = wrow0 + 8 * b + 4 * h + i;
                 if (r >= T) continue;
                 const float inv = l4[i] > 0.0f ? 1.0f / l4[i] : 0.0f;
-                const uint32_t d0 = M::cvt(o[0][4 * b + i] * inv), d1 = M::cvt(o[1][4 * b + i] * inv);
-                const uint32_t d2 = M::cvt(o[2][4 * b + i] * inv), d3 = M::cvt(o[3][4 * b + i] * inv);
-                uint16_t* op = p.out + ((int64_t)r * p.Hq + hq) * kD + 4 * c32;
-                *reinterpret_cast<u32x2*>(op) = u32x2{d0 | (d1 << 16), d2 | (d3 << 16)};
+                uint16_t* op = p.out + ((int64_t)r * p.Hq + hq) * kD + c32;
+#pragma unroll
+                for (int m = 0; m < 4; ++m) op[32 * m] = M::cvt(o[m][4 * b + i] * inv);
             }
         }
     }
 
     // ---- fused quantize-on-append of this tile's K/V rows (once per KV head)
     if constexpr (APPEND_FMT >= 0) {
-        if (hq % p.G == 0) {
-            const int nrow = min(BM, T - q0);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int item = tid + 256 * j;  // [tensor][row][block]
-                const int tensor = item >> 9;
-                const int r = (item >> 2) & 127;
+        if (hgrp == 0) {
+            const int nrow = min(p.qb, T - q0);
+            for (int item = tid; item < 2 * p.qb * 4; item += NW * 64) {  // [tensor][row][block]
+                const int tensor = item / (p.qb * 4);
+                const int r = (item >> 2) % p.qb;
                 const int blk = item & 3;
                 if (r >= nrow) continue;
                 const int64_t slot = p.slots[q0 + r];
@@ -327,11 +399,8 @@ prefill_kernel(PrefillParams p) {
 template <bool BF16, int FMT>
 int launch_prefill(PrefillParams& prm, hipStream_t stream) {
     auto kern = prefill_kernel<BF16, FMT>;
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES) != hipSuccess)
-        return VMC_EIO;
-    const int64_t grid = (int64_t)prm.ntiles * prm.Hq;
-    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), LDS_BYTES, stream, prm);
+    const int64_t grid = (int64_t)prm.ntiles * prm.Hkv * prm.hgroups;
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * NW), 0, stream, prm);
     VMC_LAUNCH_CHECK();
     return VMC_OK;
 }
@@ -377,7 +446,12 @@ extern "C" int vmc_flash_attention_prefill(void* output, const void* query, cons
     prm.Hkv = num_kv_heads;
     prm.G = num_heads / num_kv_heads;
     prm.scale_log2 = scale * kLog2e;
-    prm.ntiles = (num_tokens + BM - 1) / BM;
+    // heads per workgroup: 4, 2 or 1, dividing G; 32-row blocks per head fill 8 waves
+    prm.hw = prm.G % 4 == 0 ? 4 : (prm.G % 2 == 0 ? 2 : 1);
+    prm.rb = NW / prm.hw;
+    prm.qb = 32 * prm.rb;
+    prm.hgroups = prm.G / prm.hw;
+    prm.ntiles = (num_tokens + prm.qb - 1) / prm.qb;
     int fmt = -1;
     if (key_cache) {
         const int64_t E = vmc_kv_entry_bytes(kv_format, head_dim);
@@ -392,7 +466,7 @@ extern "C" int vmc_flash_attention_prefill(void* output, const void* query, cons
         prm.hnd = layout == VMC_LAYOUT_HND;
         fmt = kv_format;
     }
-    if ((int64_t)prm.ntiles * prm.Hq > 0x7fffffffLL) return VMC_EINVAL;
+    if ((int64_t)prm.ntiles * prm.Hkv * prm.hgroups > 0x7fffffffLL) return VMC_EINVAL;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     return dtype == VMC_DTYPE_BF16 ? dispatch_fmt<true>(prm, fmt, s) : dispatch_fmt<false>(prm, fmt, s);
 }
