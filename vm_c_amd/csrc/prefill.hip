@@ -8,22 +8,25 @@
 // [t - pos(t), t]; GQA kv head = q head / (Hq / Hkv).
 //
 // Tiling (gfx950, wave64, v_mfma_f32_32x32x16_{bf16,f16}):
-//   workgroup = 4 waves = 128 query rows of one query head; K/V tiles of 64
-//   rows, double-buffered in LDS (row pitch 272 B: 16-byte aligned reads hit
-//   distinct banks).
-//   S^T[64 kv x 32 q] = K . Q^T  per wave: 2 x 8 MFMAs, Q^T held in registers.
-//     The output layout puts one query row per lane column, so the row max /
-//     sum of the online softmax are in-lane plus one cross-half shuffle.
-//   O[32 q x 128] += P . V       per wave: 4 dim-blocks x 4 kv-chunks MFMAs.
-//     P is fed straight from the S^T registers: the contraction index k of an
-//     MFMA may be any permutation of the 16 kv rows as long as A and B agree,
-//     so logical k = 8h + e maps to kv 16c + 8(e/4) + 4h + e%4, which is what
-//     lane half h already holds.  V output columns are permuted (block m,
-//     column n -> dim 4n + m) so each lane reads 8 contiguous bytes per kv row.
-//   Per-row rescale factors reach the O rows through a 128-byte LDS scratch.
-// Fused append: the workgroup of the first query head of each KV group writes
-// its 128 K/V rows into the paged cache with the same block encoders as
-// vmc_reshape_and_cache (bit-identical pages).
+//   workgroup = 8 waves = up to 4 query heads of one KV head x 32-row query
+//   blocks, so every K/V tile of 64 keys in LDS serves 256 query rows.  Tiles
+//   arrive by load-to-LDS transfers in a 3-slot ring (rows of 256 B, 16-byte
+//   chunk ch of row r at position ch ^ swz(r)); before a tile is published
+//   each wave transposes the V rows it loaded into an fp16 V^T tile.
+//   S^T[64 kv x 32 q] = K . Q^T per wave: 16 MFMAs, Q^T held in registers,
+//     the two 32-key chains interleaved with K operand reads two steps
+//     ahead.  One query row per lane column: the row max / sum of the online
+//     softmax are in-lane plus one cross-half shuffle.
+//   O[32 q x 128] += P . V per wave: 16 fp16 MFMAs.  P is fed straight from
+//     the S^T registers: the contraction index k of an MFMA may be any
+//     permutation of the 16 keys as long as A and B agree, so logical k =
+//     8h + e maps to kv 16c + 8(e/4) + 4h + e%4, which is what lane half h
+//     already holds; V^T stores each 16-key block in that order, so a B
+//     operand is one 16-byte read.
+//   Per-row rescale factors reach the O rows through a small LDS scratch.
+// Fused append: head group 0 of each KV head writes the block's K/V rows into
+// the paged cache with the same block encoders as vmc_reshape_and_cache
+// (bit-identical pages).
 #include "kv_quant.hpp"
 
 namespace vmc {
@@ -80,14 +83,26 @@ __device__ __forceinline__ V8 as_v8(u32x4 w) {
     return __builtin_bit_cast(V8, w);
 }
 
-// All LDS of the kernel: two K/V tile slots (rows of 256 B, 16-byte chunk
-// ch of row r stored at chunk position ch ^ swz(r)), then the per-wave
-// exchange.  swz(r) rotates the low 4 row bits by two: a bijection on 16
-// consecutive rows (the 32-row K operand reads spread over all banks) whose
-// bits 2-3 differ for 4 consecutive rows (a transpose read of 4 rows x 4
-// chunks spreads too).
+// One 16-byte-per-lane load-to-LDS transfer: lane L's 16 bytes from src land
+// at dst + 16 L.  Issued from asm so the compiler does not track it: it
+// would otherwise make every later LDS read wait for all transfers in
+// flight (it cannot tell the slots apart); the kernel waits for them itself.
+__device__ __forceinline__ void dma16(const void* src, const void* dst) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)dst);
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+}
+
+// All LDS of the kernel: the K / raw V tile ring (rows of 256 B, 16-byte
+// chunk ch of row r stored at chunk position ch ^ swz(r)), the fp16 V^T
+// tiles (128 rows of 64 keys, 16-byte chunk i of row d at position
+// i ^ ((d >> 1) & 7)), then the per-wave exchange.  swz(r) rotates the low
+// 4 row bits by two: a bijection on 16 consecutive rows (the 32-row K
+// operand reads spread over all banks) whose bits 2-3 differ for 4
+// consecutive rows (the transpose reads of 4 rows x 16 dims spread too).
 struct PrefillLds {
     uint8_t tile[NSLOT][2][BN * 256];  // [slot][K, V][row][position]
+    uint8_t vtr[NSLOT][kD * BN * 2];   // [slot][dim][kv position] fp16 V^T
     float scratch[2][NW][32];          // [alpha, l][wave][row]
 };
 
@@ -173,12 +188,8 @@ prefill_kernel(PrefillParams p) {
             // rows past the range re-read the last row (masked later)
             const int kk = min(k0 + 32 * i + ld_row, kv_end - 1);
             const int64_t off = (int64_t)kk * row_stride;
-            __builtin_amdgcn_global_load_lds(
-                (const void __attribute__((address_space(1)))*)(kg + off),
-                (void __attribute__((address_space(3)))*)(&lds.tile[SL][0][1024 * (8 * i + w)]), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(
-                (const void __attribute__((address_space(1)))*)(vg + off),
-                (void __attribute__((address_space(3)))*)(&lds.tile[SL][1][1024 * (8 * i + w)]), 16, 0, 0);
+            dma16(kg + off, &lds.tile[SL][0][1024 * (8 * i + w)]);
+            dma16(vg + off, &lds.tile[SL][1][1024 * (8 * i + w)]);
         }
     };
 
@@ -187,22 +198,12 @@ prefill_kernel(PrefillParams p) {
     int k_rd[8];
 #pragma unroll
     for (int s = 0; s < 8; ++s) k_rd[s] = c32 * 256 + 16 * ((2 * s + h) ^ swz(c32));
-    // V (PV B operand) by transpose reads: lane group G = lane / 16 covers kv
-    // rows 16 c + 8 s + 4 (G / 2) + e (e = 0..3, one per lane quad) and dims
-    // 32 m + 16 (G % 2) + 4 q; the lane then holds dim 32 m + lane % 32 of
-    // those 4 rows.  One offset per (m, s): the chunk position depends on both
-    // through the swizzle.
-    const int G = lane >> 4, jq = lane & 15, e4 = jq >> 2, q4 = jq & 3;
-    const int hv = G >> 1;
-    int v_rd[4][2];
+    // V^T (PV B operand): lane (n = c32, h) reads dim 32 m + n, kv positions
+    // 16 c + 8 h .. +7 = 16-byte chunk 2 c + h of the 128-byte row, stored at
+    // chunk (2 c + h) ^ ((dim >> 1) & 7); m enters as an immediate offset
+    int vt_rd[4];
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            const int r = 8 * s + 4 * hv + e4;                     // row within 16
-            const int chunk = 4 * m + 2 * (G & 1) + (q4 >> 1);
-            v_rd[m][s] = r * 256 + 16 * (chunk ^ swz(r)) + 8 * (q4 & 1);
-        }
+    for (int c = 0; c < 4; ++c) vt_rd[c] = c32 * 128 + 16 * ((2 * c + h) ^ ((c32 >> 1) & 7));
 
     auto process = [&](int t, auto slot_c) __attribute__((always_inline)) {
         constexpr int SL = decltype(slot_c)::value;
@@ -211,18 +212,32 @@ prefill_kernel(PrefillParams p) {
         const bool active = wave_ok && k0 <= wrow1 && k0 + BN - 1 >= wlo0;
         if (!active) return;
         const uint8_t* kt = lds.tile[SL][0];
-        const uint8_t* vt = lds.tile[SL][1];
+        const uint8_t* vtt = lds.vtr[SL];
         const bool need_mask = (k0 + BN - 1 > wrow0) || (k0 < wlo1);
         // ---- S^T = K Q^T, two 32-row kv blocks
         f32x16 sacc[2];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int i = 0; i < 16; ++i) sacc[kb][i] = 0.0f;
+        {
+            // the two kv blocks' chains interleaved; K operands read two
+            // steps ahead of their MFMAs
+            u32x4 ka[8][2];
+#pragma unroll
+            for (int s = 0; s < 8; ++s)
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+                    ka[s][kb] = *reinterpret_cast<const u32x4*>(kt + kb * 32 * 256 + k_rd[s]);
+#pragma unroll
+            for (int s = 0; s < 8; ++s)
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) sacc[kb] = M::mma(as_v8<V8>(ka[s][kb]), qb[s], sacc[kb]);
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
-                const u32x4 a = *reinterpret_cast<const u32x4*>(kt + kb * 32 * 256 + k_rd[s]);
-                sacc[kb] = M::mma(as_v8<V8>(a), qb[s], sacc[kb]);
+                if (s < 6) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
             }
         }
         // ---- online softmax (log2 domain), one query row per lane column;
@@ -290,41 +305,59 @@ prefill_kernel(PrefillParams p) {
         l_part += psum;
         // ---- O += P V (fp16): k = 8h + e <-> kv 16c + 8(e/4) + 4h + e%4 (the
         // S^T registers' order); V arrives transposed, output column n = dim 32m + n
+        {
+            u32x4 vb[4][4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const f16x8 pa = as_v8<f16x8>(u32x4{pw[c][0], pw[c][1], pw[c][2], pw[c][3]});
+            for (int c = 0; c < 4; ++c)
 #pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                const int off0 = v_rd[m][0] + c * 16 * 256;
-                const int off1 = v_rd[m][1] + c * 16 * 256;
-                const s16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (__attribute__((address_space(3))) s16x4*)(vt + off0));
-                const s16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (__attribute__((address_space(3))) s16x4*)(vt + off1));
-                const u32x2 l2 = __builtin_bit_cast(u32x2, lo4), h2 = __builtin_bit_cast(u32x2, hi4);
-                o[m] = MT<false>::mma(pa, as_v8<f16x8>(u32x4{l2[0], l2[1], h2[0], h2[1]}), o[m]);
+                for (int m = 0; m < 4; ++m)
+                    vb[c][m] = *reinterpret_cast<const u32x4*>(vtt + m * 32 * 128 + vt_rd[c]);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const f16x8 pa = as_v8<f16x8>(u32x4{pw[c][0], pw[c][1], pw[c][2], pw[c][3]});
+#pragma unroll
+                for (int m = 0; m < 4; ++m) o[m] = MT<false>::mma(pa, as_v8<f16x8>(vb[c][m]), o[m]);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                if (i < 14) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             }
         }
     };
 
-    // bf16 inputs: PV runs in fp16, so each wave converts the V chunks its
-    // own transfers wrote (exact for |v| in [2^-14, 65504]) before the barrier
-    auto v_to_f16 = [&](auto slot_c) __attribute__((always_inline)) {
+    // V^T pass: each wave transposes the 8 V rows its own transfers wrote
+    // (rows 32 rs + 4 w + 0..3, rs = 0, 1) into the fp16 V^T tile, by
+    // transpose reads (16-lane group: 4 rows x 16 dims) and 8-byte writes.
+    // Within each 16-key block, kv 8a + 4h + e sits at position 8h + 4a + e,
+    // so the PV B operand of lane half h is one contiguous 16-byte chunk.
+    // bf16 inputs are converted to fp16 here (exact for |v| in [2^-14, 65504]).
+    const int tq_e = (lane >> 2) & 3, tq_q = lane & 3, tq_j = lane & 15;
+    auto v_transpose = [&](auto slot_c) __attribute__((always_inline)) {
         constexpr int SL = decltype(slot_c)::value;
-        if constexpr (BF16) {
+        const uint8_t* vr = lds.tile[SL][1];
+        uint8_t* vtt = lds.vtr[SL];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                u32x4* pv = reinterpret_cast<u32x4*>(&lds.tile[SL][1][1024 * (8 * i + w) + 16 * lane]);
-                const u32x4 x = *pv;
-                u32x4 y;
+        for (int i = 0; i < 4; ++i) {
+            const int combo = 4 * i + (lane >> 4);
+            const int rs = combo & 1, dblk = combo >> 1;
+            const int r = 32 * rs + 4 * w + tq_e;
+            const int chunk = 2 * dblk + (tq_q >> 1);
+            const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) s16x4*)(vr + r * 256 + 16 * (chunk ^ swz(r)) + 8 * (tq_q & 1)));
+            u32x2 y = __builtin_bit_cast(u32x2, x);
+            if constexpr (BF16) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const f16x2 hh = {(_Float16)__builtin_bit_cast(float, x[e] << 16),
-                                      (_Float16)__builtin_bit_cast(float, x[e] & 0xffff0000u)};
+                for (int e = 0; e < 2; ++e) {
+                    const f16x2 hh = {(_Float16)__builtin_bit_cast(float, y[e] << 16),
+                                      (_Float16)__builtin_bit_cast(float, y[e] & 0xffff0000u)};
                     y[e] = __builtin_bit_cast(uint32_t, hh);
                 }
-                *pv = y;
             }
+            const int dim = 16 * dblk + tq_j;
+            const int ci = 2 * (2 * rs + (w >> 2)) + (w & 1);
+            *reinterpret_cast<u32x2*>(vtt + dim * 128 + 16 * (ci ^ ((dim >> 1) & 7)) + 8 * ((w >> 1) & 1)) = y;
         }
     };
 
@@ -344,7 +377,7 @@ prefill_kernel(PrefillParams p) {
             if (t < ntile) {  // uniform over the workgroup
                 if (t + 1 < ntile) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
                 else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-                v_to_f16(sc);
+                v_transpose(sc);
                 asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
                 if (t + 2 < ntile) load_tile(t + 2, std::integral_constant<int, (S + 2) % NSLOT>{});
                 process(t, sc);
