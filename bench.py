@@ -11,6 +11,9 @@ page pool is replicated into >= 2 GiB of distinct copies and the steps rotate
 through them so the 256 MB last-level cache cannot serve the pages.
 
 Also measured in the same run (extra fields of the same line):
+  * variant_g32: the same decode step with the configuration text's KV
+    format, turboquant_3bit_g32 (random-sign Walsh-Hadamard, 3-bit codes and
+    a 16-bit scale per 32 values, 112-byte slots);
   * causal prefill: batch 4 x 4096 tokens, 32/8 heads, bf16, fused q8_0
     quantize-on-append into the paged cache -> TFLOP/s;
   * cpu_baseline: the CPU restatement of the TurboQuant decode (OpenMP over
@@ -68,14 +71,14 @@ def slots_for(bt, lens, positions_of):
 
 # ------------------------------------------------------------------ decode
 
-def bench_decode(args, torch, capi, dev):
+def bench_decode(args, torch, capi, dev, method="turboquant_3bit_nc", sign_seed=0):
     w = decode_workload()
     B, Hq, Hkv, lens, bt = w["B"], w["Hq"], w["Hkv"], w["lens"], w["bt"]
-    cfg = capi.tq_config(D, "turboquant_3bit_nc")
+    cfg = capi.tq_config(D, method, sign_seed=sign_seed)
     slot_bytes = cfg.slot_size_aligned
     pool_bytes = w["nblk"] * BS * Hkv * slot_bytes
     npool = max(2, math.ceil(2 * 1024 ** 3 / pool_bytes))
-    log(f"decode: B={B} Hq={Hq} Hkv={Hkv} sum(L)={int(lens.sum())} max(L)={int(lens.max())} "
+    log(f"decode {method}: B={B} Hq={Hq} Hkv={Hkv} sum(L)={int(lens.sum())} max(L)={int(lens.max())} "
         f"pool={pool_bytes / 1e6:.1f} MB x {npool} copies")
     pools = [torch.empty(pool_bytes, dtype=torch.uint8, device=dev) for _ in range(npool)]
     gen = torch.Generator(device=dev)
@@ -250,6 +253,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-prefill", action="store_true")
+    ap.add_argument("--skip-variant", action="store_true",
+                    help="skip the per-32-group 3-bit variant's decode (turboquant_3bit_g32)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy 5 times (the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -274,6 +279,19 @@ def main():
         print(json.dumps({"copy_calibration_bytes": n, "launches": 5}), flush=True)
         return
     dec = bench_decode(args, torch, capi, dev)
+    var = None
+    if not args.skip_variant:
+        # the configuration text's format: random-sign WHT (seed 4) + 3-bit
+        # codes with a scale per 32 values, same workload
+        v = bench_decode(args, torch, capi, dev, method="turboquant_3bit_g32", sign_seed=4)
+        var = {"kv": "turboquant_3bit_g32 (112 B slot, signs seed 4)",
+               "ms_step": round(v["ms_step"], 4), "ms_attn": round(v["ms_attn"], 4),
+               "attn_gbs": round(v["attn_bytes"] / (v["ms_attn"] * 1e-3) / 1e9, 1),
+               "attn_frac_hbm": round(v["attn_bytes"] / (v["ms_attn"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+               "attn_bytes": v["attn_bytes"],
+               "tokens_per_s": round(v["w"]["B"] / (v["ms_step"] * 1e-3), 1)}
+        del v
+        torch.cuda.empty_cache()
     pre = None if args.skip_prefill else bench_prefill(args, torch, capi, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline(dec, torch)
 
@@ -309,6 +327,8 @@ def main():
                      "ms": round(dec["ms_attn"], 4), "bytes": dec["attn_bytes"]},
         "cpu_baseline": cpu,
     }
+    if var is not None:
+        line["variant_g32"] = var
     if pre is not None:
         line["prefill"] = {"workload": "causal prefill B=4 S=4096 Hq=32 Hkv=8 bf16, fused q8_0 append",
                            "ms": round(pre["ms"], 4), "tflops": round(pre["tflops"], 1),

@@ -109,11 +109,31 @@ typedef struct vmc_tq_config {
     int slot_size_aligned;
     int n_centroids;
     int max_num_kv_splits;
+    /* The two fields below have no counterpart in vm_c::TQConfig: they select
+     * the per-32-group variant the benchmark configurations describe
+     * ("seeded random-sign Walsh-Hadamard, 4-bit / 3-bit codes with a 16-bit
+     * scale (+zero) per 32-value group"), for which the reference has no
+     * code.  group_size 0 is the reference layout above. */
+    int group_size;              /* 0, or 32 */
+    unsigned long long sign_seed; /* rotation signs (0: all +1) */
 } vmc_tq_config;
 
 /* TQConfig::from_method: "turboquant_4bit_nc" (default), "turboquant_3bit_nc",
  * "turboquant_k3v4_nc".  Returns VMC_EINVAL for an unknown method or for
- * "turboquant_k8v4" (fp8 keys, not implemented). */
+ * "turboquant_k8v4" (fp8 keys, not implemented).
+ * The per-32-group variant (no reference counterpart): "turboquant_4bit_g32"
+ * and "turboquant_3bit_g32".  For both K and V, y = H (s * x) / sqrt(128)
+ * (s = +-1 signs from sign_seed), then per 32 values of y:
+ *   4-bit: {fp16 d, fp16 m, 16 bytes, byte j = code j | code j+16 << 4},
+ *          y ~ code * d + m, d = (max - min) / 15;
+ *   3-bit: {fp16 d, 12 bytes of codes, 8 codes per 3 bytes little endian,
+ *          code i at bits 3i}, y ~ (code - 4) * d, d = v / -4 with v the
+ *          first value of largest magnitude.
+ * A slot is the K part then the V part: 2 x 80 = 160 bytes (4-bit) or
+ * 2 x 56 = 112 bytes (3-bit); the fields above describe one part (mse_bytes
+ * = code bytes, key_packed_size = value_packed_size = part bytes,
+ * n_centroids = 0, norm_correction = 0).  sign_seed starts at 0; the caller
+ * sets it, identically for the store and the decode. */
 int vmc_tq_config_from_method(int head_dim, const char* method, vmc_tq_config* out);
 
 /* Host-side constant tables (Lloyd-Max centroids for N(0, 1/d), midpoints),

@@ -670,6 +670,187 @@ void orc_tq_decode_exact(double* out, const uint16_t* query, const uint8_t* kv_c
 }
 
 /* ------------------------------------------------------------------------ */
+/* TurboQuant per-32-group variant (configuration text; no reference code)  */
+/* ------------------------------------------------------------------------ */
+/* Defined here (the configuration asks for "seeded random-sign Walsh-Hadamard
+ * + 4-bit / 3-bit codes with a 16-bit scale (+zero) per 32-value group"):
+ *   y = H (s * x) / sqrt(d), in orc_tq_rotate's declared order, for K and V;
+ *   s[i] = -1 where bit i % 64 of orc_rand_u64(seed, ORC_G32_SIGN_STREAM,
+ *   i / 64) is set (seed 0: all +1);
+ *   slot = K part then V part, each four 32-value blocks of y:
+ *     4-bit: {fp16 d, fp16 m, qs[16]}, qs[j] = q[j] | q[j+16] << 4, y ~ q d + m,
+ *            d = (max - min) / 15, q = min(15, (int)((y - min) / d + 0.5));
+ *     3-bit: {fp16 d, qs[12]}, codes 8k .. 8k+7 in bytes 3k .. 3k+2 little
+ *            endian (code i at bits 3i), y ~ (q - 4) d, d = v / -4 with v the
+ *            first value of largest magnitude, q = min(7, (int)(y / d + 4.5));
+ *   the divisions are y * (1/d) (0 when d = 0) in fp32, no contraction. */
+#define ORC_G32_SIGN_STREAM 0x5349474eULL
+
+void orc_g32_signs(uint64_t seed, float* s, int d) {
+    for (int i = 0; i < d; ++i) {
+        const uint64_t w = seed ? orc_rand_u64(seed, ORC_G32_SIGN_STREAM, (uint64_t)(i / 64)) : 0;
+        s[i] = ((w >> (i % 64)) & 1) ? -1.0f : 1.0f;
+    }
+}
+
+int orc_g32_part_bytes(int bits) { return bits == 4 ? 80 : 56; }
+
+static void g32_put_f16(uint8_t* p, float v) {
+    const uint16_t b = orc_f32_to_f16(v);
+    p[0] = (uint8_t)(b & 0xff);
+    p[1] = (uint8_t)(b >> 8);
+}
+static float g32_get_f16(const uint8_t* p) { return orc_f16_to_f32((uint16_t)(p[0] | (p[1] << 8))); }
+
+void orc_g32_quantize_part(const float* y, int bits, uint8_t* dst) {
+    for (int g = 0; g < 4; ++g) {
+        const float* x = y + 32 * g;
+        int q[32];
+        if (bits == 4) {
+            uint8_t* blk = dst + 20 * g;
+            float mn = x[0], mx = x[0];
+            for (int j = 1; j < 32; ++j) {
+                mn = fminf(mn, x[j]);
+                mx = fmaxf(mx, x[j]);
+            }
+            const float d = (mx - mn) / 15.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+            g32_put_f16(blk, d);
+            g32_put_f16(blk + 2, mn);
+            for (int j = 0; j < 32; ++j) {
+                float t = x[j] - mn;
+                t = t * id;
+                t = t + 0.5f;
+                const int c = (int)t;
+                q[j] = c > 15 ? 15 : c;
+            }
+            for (int j = 0; j < 16; ++j) blk[4 + j] = (uint8_t)(q[j] | (q[j + 16] << 4));
+        } else {
+            uint8_t* blk = dst + 14 * g;
+            float amax = 0.0f, v = 0.0f;
+            for (int j = 0; j < 32; ++j) {
+                const float a = fabsf(x[j]);
+                if (a > amax) {
+                    amax = a;
+                    v = x[j];
+                }
+            }
+            const float d = v / -4.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+            g32_put_f16(blk, d);
+            for (int j = 0; j < 32; ++j) {
+                float t = x[j] * id;
+                t = t + 4.5f;
+                const int c = (int)t;
+                q[j] = c > 7 ? 7 : c;
+            }
+            for (int k = 0; k < 4; ++k) {
+                uint32_t w = 0;
+                for (int i = 0; i < 8; ++i) w |= (uint32_t)q[8 * k + i] << (3 * i);
+                blk[2 + 3 * k] = (uint8_t)(w & 0xff);
+                blk[3 + 3 * k] = (uint8_t)((w >> 8) & 0xff);
+                blk[4 + 3 * k] = (uint8_t)((w >> 16) & 0xff);
+            }
+        }
+    }
+}
+
+void orc_g32_dequant_part(const uint8_t* src, int bits, float* y) {
+    for (int g = 0; g < 4; ++g) {
+        if (bits == 4) {
+            const uint8_t* blk = src + 20 * g;
+            const float d = g32_get_f16(blk), m = g32_get_f16(blk + 2);
+            for (int j = 0; j < 16; ++j) {
+                y[32 * g + j] = (float)(blk[4 + j] & 0xf) * d + m;
+                y[32 * g + j + 16] = (float)(blk[4 + j] >> 4) * d + m;
+            }
+        } else {
+            const uint8_t* blk = src + 14 * g;
+            const float d = g32_get_f16(blk);
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t w = blk[2 + 3 * k] | (blk[3 + 3 * k] << 8) | (blk[4 + 3 * k] << 16);
+                for (int i = 0; i < 8; ++i) y[32 * g + 8 * k + i] = (float)((int)((w >> (3 * i)) & 7) - 4) * d;
+            }
+        }
+    }
+}
+
+void orc_g32_store(const uint16_t* key, const uint16_t* value, uint8_t* kv_cache,
+                   const int64_t* slot_mapping, int T, int Hkv, int D, int64_t bs, int bits,
+                   uint64_t seed, int bf16) {
+    const int P = orc_g32_part_bytes(bits), S = 2 * P;
+    float sg[128];
+    orc_g32_signs(seed, sg, D);
+#pragma omp parallel for schedule(static)
+    for (int t = 0; t < T; ++t) {
+        const int64_t slot = slot_mapping[t];
+        if (slot < 0) continue;
+        float x[128], y[128];
+        for (int h = 0; h < Hkv; ++h) {
+            const int64_t pid = (int64_t)t * Hkv + h;
+            uint8_t* sp = kv_cache + (slot / bs) * bs * Hkv * S + (slot % bs) * Hkv * S + (int64_t)h * S;
+            for (int part = 0; part < 2; ++part) {
+                const uint16_t* src = (part ? value : key) + pid * D;
+                for (int d = 0; d < D; ++d) x[d] = half_to_f32(src[d], bf16);
+                orc_tq_rotate(x, sg, y, D);
+                orc_g32_quantize_part(y, bits, sp + part * P);
+            }
+        }
+    }
+}
+
+/* Exact fp64 attention over the dequantized pages, in the rotated domain:
+ * q_r = H (s q) / sqrt(d), O = s (H O_r) / sqrt(d) (exact H, fp64). */
+void orc_g32_decode_exact(double* out, const uint16_t* query, const uint8_t* kv_cache,
+                          const int32_t* block_tables, const int32_t* seq_lens, int B, int Hq,
+                          int Hkv, int D, double scale, int64_t bs, int64_t max_blocks, int bits,
+                          uint64_t seed, int q_bf16, int nthreads) {
+    const int kv_group = Hq / Hkv;
+    const int P = orc_g32_part_bytes(bits), S = 2 * P;
+    const double c = 1.0 / sqrt((double)D);
+    float sg[128];
+    orc_g32_signs(seed, sg, D);
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel for schedule(dynamic)
+#endif
+    for (int bh = 0; bh < B * Hq; ++bh) {
+        const int b = bh / Hq, h = bh % Hq, kvh = h / kv_group;
+        const int n = seq_lens[b] > 0 ? seq_lens[b] : 0;
+        double* K = (double*)malloc(sizeof(double) * (size_t)(n + 1) * (size_t)D);
+        double* V = (double*)malloc(sizeof(double) * (size_t)(n + 1) * (size_t)D);
+        double qs[128], qr[128], orr[128];
+        float y[128];
+        int cnt = 0;
+        for (int pos = 0; pos < n; ++pos) {
+            const int32_t blk = block_tables[(int64_t)b * max_blocks + pos / bs];
+            if (blk < 0) continue;
+            const uint8_t* sp = kv_cache + (int64_t)blk * bs * Hkv * S + (pos % bs) * Hkv * S +
+                                (int64_t)kvh * S;
+            orc_g32_dequant_part(sp, bits, y);
+            for (int d = 0; d < D; ++d) K[(int64_t)cnt * D + d] = y[d];
+            orc_g32_dequant_part(sp + P, bits, y);
+            for (int d = 0; d < D; ++d) V[(int64_t)cnt * D + d] = y[d];
+            cnt++;
+        }
+        for (int d = 0; d < D; ++d) qs[d] = half_to_f32(query[(int64_t)bh * D + d], q_bf16) * sg[d];
+        for (int i = 0; i < D; ++i) {
+            double acc = 0.0;
+            for (int j = 0; j < D; ++j) acc += ((__builtin_popcount((unsigned)(i & j)) & 1) ? -c : c) * qs[j];
+            qr[i] = acc;
+        }
+        softmax_av_exact(qr, K, V, cnt, D, scale, orr);
+        for (int i = 0; i < D; ++i) {
+            double acc = 0.0;
+            for (int j = 0; j < D; ++j) acc += ((__builtin_popcount((unsigned)(i & j)) & 1) ? -c : c) * orr[j];
+            out[(int64_t)bh * D + i] = acc * sg[i];
+        }
+        free(K);
+        free(V);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
 /* paged decode over f16 / bf16 / q8_0 / q4_0 pages                         */
 /* ------------------------------------------------------------------------ */
 

@@ -110,6 +110,22 @@ void orc_tq_decode_exact(double* out, const uint16_t* query, const uint8_t* kv_c
                          const orc_tq_layout* L, const float* centroids,
                          int half_is_bf16, int nthreads);
 
+/* ---- TurboQuant per-32-group variant (configuration text, no reference
+ * code; format defined in vmc_oracle.c) ---- */
+void orc_g32_signs(uint64_t seed, float* s, int d);
+int  orc_g32_part_bytes(int bits);
+void orc_g32_quantize_part(const float* y, int bits, uint8_t* dst);
+void orc_g32_dequant_part(const uint8_t* src, int bits, float* y);
+void orc_g32_store(const uint16_t* key, const uint16_t* value, uint8_t* kv_cache,
+                   const int64_t* slot_mapping, int num_tokens, int num_kv_heads,
+                   int head_dim, int64_t block_size, int bits, uint64_t seed,
+                   int half_is_bf16);
+void orc_g32_decode_exact(double* out, const uint16_t* query, const uint8_t* kv_cache,
+                          const int32_t* block_tables, const int32_t* seq_lens,
+                          int batch, int num_heads, int num_kv_heads, int head_dim,
+                          double scale, int64_t block_size, int64_t max_blocks_per_req,
+                          int bits, uint64_t seed, int q_is_bf16, int nthreads);
+
 /* ---- paged decode over f16/bf16/q8_0/q4_0 pages ---- */
 /* exact fp64 softmax attention over the dequantized pages; q is fp32 */
 void orc_paged_decode_exact(double* out, const float* q,

@@ -141,6 +141,16 @@ static void test_layouts() {
     auto l8 = TurboQuantLayout::create(128, "turboquant_k8v4");
     CHECK(l4.slot_size_aligned == 134 && l3.slot_size_aligned == 102);
     CHECK(lk.slot_size_aligned == 118 && l8.slot_size_aligned == 196);
+    // per-32-group variant (not in vm_c): K + V parts of four blocks
+    auto g4 = TurboQuantLayout::create(128, "turboquant_4bit_g32");
+    auto g3 = TurboQuantLayout::create(128, "turboquant_3bit_g32");
+    CHECK(g4.slot_size_aligned == 160 && g3.slot_size_aligned == 112);
+    CHECK(g4.group_size == 32 && g3.group_size == 32 && g3.key_quant_bits == 3);
+    {
+        const TQConfig c4 = TQConfig::from_method(128, "turboquant_4bit_g32");
+        const vmc_tq_config cc = c4.to_c();
+        CHECK(cc.group_size == 32 && cc.slot_size_aligned == 160 && cc.key_packed_size == 80);
+    }
     for (const char* meth : {"turboquant_4bit_nc", "turboquant_3bit_nc", "turboquant_k3v4_nc"}) {
         TQConfig a = TQConfig::from_method(128, meth);
         vmc_tq_config b;

@@ -97,13 +97,22 @@ static void test_turboquant_backend(const char* method) {
                        ScalarType::FLOAT16, nullptr);
     HIP_CHECK(hipDeviceSynchronize());
 
+    // the per-32-group variant ("*_g32", signs of seed 0) or the reference layout
+    const bool g32 = std::string(method).find("_g32") != std::string::npos;
+    const int gbits = std::string(method).find("4bit") != std::string::npos ? 4 : 3;
     orc_tq_layout L;
-    CHECK(orc_tq_layout_from_method(D, method, &L) == 0);
-    std::vector<float> C(L.n_centroids), M(L.n_centroids - 1);
-    orc_tq_lloyd_max(C.data(), D, L.key_quant_bits);
-    orc_tq_midpoints(C.data(), L.n_centroids, M.data());
+    std::vector<float> C(16), M(15);
+    if (!g32) {
+        CHECK(orc_tq_layout_from_method(D, method, &L) == 0);
+        orc_tq_lloyd_max(C.data(), D, L.key_quant_bits);
+        orc_tq_midpoints(C.data(), L.n_centroids, M.data());
+    }
+    auto ref_store = [&](const uint16_t* k, const uint16_t* v, uint8_t* dst, const int64_t* slots, int n) {
+        if (g32) orc_g32_store(k, v, dst, slots, n, Hkv, D, BS, gbits, 0, 0);
+        else orc_tq_store(k, v, dst, slots, n, Hkv, D, BS, &L, M.data(), 0);
+    };
     std::vector<uint8_t> ref(pool_n, 0);
-    orc_tq_store(K.data(), V.data(), ref.data(), hp.slot_mapping.data(), T, Hkv, D, BS, &L, M.data(), 0);
+    ref_store(K.data(), V.data(), ref.data(), hp.slot_mapping.data(), T);
     CHECK(pool_bytes(pool, pool_n) == ref);
 
     // prefill rows vs exact causal attention
@@ -140,12 +149,15 @@ static void test_turboquant_backend(const char* method) {
     be.forward_decode(dO1.p, dQ1.p, pool, nullptr, md, Hq, Hkv, D, scale, BS, ScalarType::FLOAT16, nullptr);
     HIP_CHECK(hipDeviceSynchronize());
     std::vector<uint8_t> got = pool_bytes(pool, pool_n);
-    orc_tq_store(K1.data(), V1.data(), ref.data(), hd.slot_mapping.data(), hd.num_tokens, Hkv, D, BS, &L,
-                 M.data(), 0);
+    ref_store(K1.data(), V1.data(), ref.data(), hd.slot_mapping.data(), hd.num_tokens);
     CHECK(got == ref);
     std::vector<double> exd((size_t)hd.num_reqs * Hq * D);
-    orc_tq_decode_exact(exd.data(), Q1.data(), got.data(), hd.block_tables.data(), hd.seq_lens.data(),
-                        hd.num_reqs, Hq, Hkv, D, scale, BS, hd.max_num_blocks_per_req, &L, C.data(), 0, 0);
+    if (g32)
+        orc_g32_decode_exact(exd.data(), Q1.data(), got.data(), hd.block_tables.data(), hd.seq_lens.data(),
+                             hd.num_reqs, Hq, Hkv, D, scale, BS, hd.max_num_blocks_per_req, gbits, 0, 0, 0);
+    else
+        orc_tq_decode_exact(exd.data(), Q1.data(), got.data(), hd.block_tables.data(), hd.seq_lens.data(),
+                            hd.num_reqs, Hq, Hkv, D, scale, BS, hd.max_num_blocks_per_req, &L, C.data(), 0, 0);
     CHECK(close(dO1.get(), exd, &err));
     std::printf("  decode max err %.3g\n", err);
     for (size_t i = 0; i < lens.size(); ++i) mgr.free_slots("r" + std::to_string(i));
@@ -215,7 +227,9 @@ int main() {
         return 2;
     }
     try {
-        for (const char* m : {"turboquant_3bit_nc", "turboquant_4bit_nc"}) test_turboquant_backend(m);
+        for (const char* m : {"turboquant_3bit_nc", "turboquant_4bit_nc", "turboquant_3bit_g32",
+                              "turboquant_4bit_g32"})
+            test_turboquant_backend(m);
         test_paged_backend("q8_0", "nhd");
         test_paged_backend("q4_0", "hnd");
         test_paged_backend("fp16", "hnd");

@@ -72,6 +72,16 @@ def lib():
         L.orc_tq_decode_exact.argtypes = [_P, _P, _P, _P, _P, C.c_int, C.c_int, C.c_int,
                                           C.c_int, C.c_double, C.c_int64, C.c_int64,
                                           C.POINTER(TQLayout), _P, C.c_int, C.c_int]
+        L.orc_g32_signs.argtypes = [C.c_uint64, _P, C.c_int]
+        L.orc_g32_part_bytes.restype = C.c_int
+        L.orc_g32_part_bytes.argtypes = [C.c_int]
+        L.orc_g32_quantize_part.argtypes = [_P, C.c_int, _P]
+        L.orc_g32_dequant_part.argtypes = [_P, C.c_int, _P]
+        L.orc_g32_store.argtypes = [_P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int64, C.c_int,
+                                    C.c_uint64, C.c_int]
+        L.orc_g32_decode_exact.argtypes = [_P, _P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int,
+                                           C.c_double, C.c_int64, C.c_int64, C.c_int, C.c_uint64,
+                                           C.c_int, C.c_int]
         L.orc_paged_decode_exact.argtypes = [_P, _P, _P, _P, C.c_int, C.c_int, _P, _P,
                                              C.c_int, C.c_int, C.c_int, C.c_int, C.c_double,
                                              C.c_int64, C.c_int64, C.c_int]
@@ -199,6 +209,49 @@ def tq_decode_exact(q_bits, cache, block_tables, seq_lens, Hkv, scale, block_siz
                               _ptr(bt), _ptr(np.ascontiguousarray(seq_lens, dtype=np.int32)),
                               B, Hq, Hkv, D, scale, block_size, bt.shape[1], C.byref(L),
                               _ptr(centroids), int(bf16), nthreads)
+    return out
+
+
+def g32_signs(seed, d=128):
+    out = np.zeros(d, dtype=np.float32)
+    lib().orc_g32_signs(seed, _ptr(out), d)
+    return out
+
+
+def g32_part_bytes(bits):
+    return int(lib().orc_g32_part_bytes(bits))
+
+
+def g32_quantize_part(y, bits):
+    y = np.ascontiguousarray(y, dtype=np.float32)
+    assert y.size == 128
+    out = np.zeros(g32_part_bytes(bits), dtype=np.uint8)
+    lib().orc_g32_quantize_part(_ptr(y), bits, _ptr(out))
+    return out
+
+
+def g32_dequant_part(part, bits):
+    part = np.ascontiguousarray(part, dtype=np.uint8)
+    out = np.zeros(128, dtype=np.float32)
+    lib().orc_g32_dequant_part(_ptr(part), bits, _ptr(out))
+    return out
+
+
+def g32_store(key_bits, value_bits, slot_mapping, cache, block_size, bits, seed, bf16=False):
+    T, H, D = key_bits.shape
+    lib().orc_g32_store(_ptr(np.ascontiguousarray(key_bits)), _ptr(np.ascontiguousarray(value_bits)),
+                        _ptr(cache), _ptr(np.ascontiguousarray(slot_mapping, dtype=np.int64)),
+                        T, H, D, block_size, bits, seed, int(bf16))
+
+
+def g32_decode_exact(q_bits, cache, block_tables, seq_lens, Hkv, scale, block_size, bits, seed,
+                     bf16=False, nthreads=0):
+    B, Hq, D = q_bits.shape
+    out = np.zeros((B, Hq, D), dtype=np.float64)
+    bt = np.ascontiguousarray(block_tables, dtype=np.int32)
+    lib().orc_g32_decode_exact(_ptr(out), _ptr(np.ascontiguousarray(q_bits)), _ptr(cache), _ptr(bt),
+                               _ptr(np.ascontiguousarray(seq_lens, dtype=np.int32)), B, Hq, Hkv, D,
+                               scale, block_size, bt.shape[1], bits, seed, int(bf16), nthreads)
     return out
 
 

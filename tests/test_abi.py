@@ -55,6 +55,22 @@ def test_tq_config_layouts():
         capi.tq_config(128, "turboquant_k8v4")
 
 
+def test_g32_config_layouts():
+    """The per-32-group variant (no reference counterpart): K and V parts of
+    four blocks, 2 x 80 B (4-bit: fp16 scale + fp16 min + 16 B) and 2 x 56 B
+    (3-bit: fp16 scale + 12 B), matching the oracle's part sizes."""
+    from vm_c_amd import capi
+    for m, bits, part in (("turboquant_4bit_g32", 4, 80), ("turboquant_3bit_g32", 3, 56)):
+        c = capi.tq_config(128, m, sign_seed=7)
+        assert (c.group_size, c.key_quant_bits, c.value_quant_bits) == (32, bits, bits)
+        assert (c.key_packed_size, c.value_packed_size, c.slot_size_aligned) == (part, part, 2 * part)
+        assert c.sign_seed == 7 and c.n_centroids == 0
+        assert O.g32_part_bytes(bits) == part
+    import pytest
+    with pytest.raises(capi.VmcError):
+        capi.tq_config(64, "turboquant_4bit_g32")
+
+
 def test_tq_host_tables_match_oracle():
     from vm_c_amd import capi
     for bits in (3, 4):

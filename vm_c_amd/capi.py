@@ -30,7 +30,8 @@ class TQConfig(C.Structure):
     _fields_ = [(n, C.c_int) for n in (
         "head_dim", "key_quant_bits", "value_quant_bits", "norm_correction", "key_fp8",
         "fp8_e4b15", "mse_bytes", "key_packed_size", "val_data_bytes", "value_packed_size",
-        "slot_size", "slot_size_aligned", "n_centroids", "max_num_kv_splits")]
+        "slot_size", "slot_size_aligned", "n_centroids", "max_num_kv_splits",
+        "group_size")] + [("sign_seed", C.c_ulonglong)]
 
 
 class VmcError(RuntimeError):
@@ -130,10 +131,13 @@ def kv_entry_bytes(kv_format, head_dim):
     return int(load().vmc_kv_entry_bytes(kv_format, head_dim))
 
 
-def tq_config(head_dim=128, method="turboquant_4bit_nc"):
+def tq_config(head_dim=128, method="turboquant_4bit_nc", sign_seed=0):
+    """vmc_tq_config_from_method; sign_seed sets the rotation signs of the
+    per-32-group methods ("turboquant_4bit_g32", "turboquant_3bit_g32")."""
     cfg = TQConfig()
     _check(load().vmc_tq_config_from_method(head_dim, method.encode(), C.byref(cfg)),
            f"vmc_tq_config_from_method({method})")
+    cfg.sign_seed = int(sign_seed)
     return cfg
 
 

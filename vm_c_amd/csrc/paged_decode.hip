@@ -52,7 +52,11 @@ constexpr int kBs = 16;
 constexpr int kChunkPages = 256;  // pages whose block-table entries are staged in LDS at once
 constexpr float kNegInf = -__builtin_inff();
 
-enum { FMT_F16 = 0, FMT_BF16 = 1, FMT_Q8_0 = 2, FMT_Q4_0 = 3, FMT_TQ = 4 };
+// FMT_G4 / FMT_G3: the per-32-group variant (no reference counterpart): one
+// slot per (token, head) holds the K part then the V part, each four 32-value
+// blocks {fp16 d, fp16 m, 16 B of nibbles} (4-bit) or {fp16 d, 12 B of 3-bit
+// codes} (3-bit) of the rotated vector
+enum { FMT_F16 = 0, FMT_BF16 = 1, FMT_Q8_0 = 2, FMT_Q4_0 = 3, FMT_TQ = 4, FMT_G4 = 5, FMT_G3 = 6 };
 
 // Compile-time geometry of a page format (head_dim 128, block 16, at most 8
 // KV heads): TurboQuant slot fields (kernels_turboquant.h:29-45), GGUF entry
@@ -65,9 +69,12 @@ enum { FMT_F16 = 0, FMT_BF16 = 1, FMT_Q8_0 = 2, FMT_Q4_0 = 3, FMT_TQ = 4 };
 template <int FMT, int KB, int VB>
 struct Geo {
     static constexpr int mse = 16 * KB, key_packed = mse + 2, val_data = 16 * VB;
+    // K and V in one slot per (token, head), one pool
+    static constexpr bool combined = FMT == FMT_TQ || FMT == FMT_G4 || FMT == FMT_G3;
     static constexpr int entry = FMT == FMT_TQ ? (key_packed + val_data + 4 + 1) / 2 * 2
+                                 : FMT == FMT_G4 ? 160 : FMT == FMT_G3 ? 112
                                  : FMT == FMT_Q8_0 ? 136 : FMT == FMT_Q4_0 ? 72 : 256;
-    static constexpr int per_thread = FMT == FMT_TQ ? entry : 2 * entry;  // staged bytes per token-head
+    static constexpr int per_thread = combined ? entry : 2 * entry;  // staged bytes per token-head
     static constexpr bool staged = FMT >= FMT_Q8_0;
     static constexpr int spp = staged ? (per_thread + 63) / 64 : 1;
     static constexpr bool dma = FMT == FMT_TQ;
@@ -81,7 +88,7 @@ struct Geo {
     static constexpr int nc_max = nc_of(4);
     // chunks per lane per page for any group size (1..4 heads, one wave each)
     static constexpr int spt = std::max(std::max(spt_of(1), spt_of(2)), std::max(spt_of(3), spt_of(4)));
-    static constexpr int kBuf = dma ? kBs * nc_max * 16 : 2 * kHalf;  // one LDS buffer
+    static constexpr int kBuf = dma ? kBs * nc_max * 16 : combined ? kHalf : 2 * kHalf;  // one LDS buffer
 };
 
 // TurboQuant V codes enter the PV MFMA as fp16 subnormals: the code field of
@@ -142,6 +149,7 @@ struct DecodeParams {
     // TurboQuant
     int mse_bytes, key_packed, val_data;
     TQTables tab;
+    uint32_t sgn[4];     // per-32-group variant: bit i set = rotation sign of dim i is -1
 };
 
 // ------------------------------------------------------------------ layout
@@ -250,6 +258,36 @@ __device__ __forceinline__ void build_pair_lut(uint32_t* lut, const TQTables& ta
 
 __device__ __forceinline__ uint32_t lds16(const uint8_t* p) {
     return (uint32_t)*reinterpret_cast<const uint16_t*>(p);
+}
+
+// per-32-group variant: the codes of values 8j .. 8j+7 of the 32-value
+// block at blk (LDS, even address), value v of the 8 at bits 4v (4-bit:
+// byte i of the 16 holds values i and i + 16) or 3v (3-bit: 8 codes per 3
+// bytes, little endian)
+template <int FMT>
+__device__ __forceinline__ uint32_t g32_codes8(const uint8_t* blk, int j) {
+    if constexpr (FMT == FMT_G4) {
+        const uint8_t* cb = blk + 4 + 8 * (j & 1);
+        const uint32_t w0 = lds16(cb) | (lds16(cb + 2) << 16);
+        const uint32_t w1 = lds16(cb + 4) | (lds16(cb + 6) << 16);
+        const int sh = j < 2 ? 0 : 4;
+        uint32_t cw = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            cw |= ((w0 >> (8 * e + sh)) & 0xfu) << (4 * e);
+            cw |= ((w1 >> (8 * e + sh)) & 0xfu) << (4 * e + 16);
+        }
+        return cw;
+    } else {
+        const int o = 2 + 3 * j;  // the block start is even: o's parity is j's
+        const uint8_t* cb = blk + (o & ~1);
+        const uint32_t w = lds16(cb) | (lds16(cb + 2) << 16);
+        return (w >> (8 * (o & 1))) & 0xffffffu;
+    }
+}
+template <int FMT>
+__device__ __forceinline__ float g32_code(uint32_t cw, int v) {
+    return FMT == FMT_G4 ? (float)((cw >> (4 * v)) & 0xfu) : (float)((cw >> (3 * v)) & 7u);
 }
 
 template <int FMT>
@@ -371,7 +409,9 @@ paged_decode_kernel(DecodeParams p) {
     AT qb[HALF ? 8 : 4];
     auto load_q = [&](int b) __attribute__((always_inline)) {
         const int64_t qrow = ((int64_t)b * p.Hq + hq0 + qh) * kD;
-        if constexpr (FMT == FMT_TQ) {
+        if constexpr (FMT == FMT_TQ || FMT == FMT_G4 || FMT == FMT_G3) {
+            // q in the rotated domain of the keys: H (s q) / sqrt(d), s = +1 for
+            // the reference layout
             float y[32];
             if (q_ok) {
                 const u32x4* src = reinterpret_cast<const u32x4*>(p.q + qrow + 32 * grp);
@@ -388,6 +428,11 @@ paged_decode_kernel(DecodeParams p) {
             } else {
 #pragma unroll
                 for (int e = 0; e < 32; ++e) y[e] = 0.0f;
+            }
+            if constexpr (FMT != FMT_TQ) {
+                const uint32_t sb = p.sgn[grp];  // dims 32*grp .. +31
+#pragma unroll
+                for (int e = 0; e < 32; ++e) y[e] = ((sb >> e) & 1u) ? -y[e] : y[e];
             }
             // Walsh-Hadamard: half-widths 1..16 inside the lane, 32 and 64 across
             // the lane groups (dim bit 32 = grp bit 0, dim bit 64 = grp bit 1).
@@ -472,6 +517,40 @@ paged_decode_kernel(DecodeParams p) {
                                __builtin_amdgcn_readfirstlane(plan.last_cut);
         const bool whole = !cut_before && !cut_after;
         const int slot = cut_before ? 2 * w : 2 * w + 1;
+        if constexpr (FMT == FMT_G4 || FMT == FMT_G3) {
+            // O back from the rotated domain: s (H O_r) / sqrt(d) (linear, so
+            // partial rows may be rotated before the merge).  oacc[c][i] =
+            // dim 8*r16 + c: half-widths 1..4 in the lane, 8..64 across r16.
+#pragma unroll
+            for (int hw = 1; hw < 8; hw <<= 1)
+#pragma unroll
+                for (int c0 = 0; c0 < 8; c0 += 2 * hw)
+#pragma unroll
+                    for (int c = c0; c < c0 + hw; ++c)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const float a = oacc[c][i], bb = oacc[c + hw][i];
+                            oacc[c][i] = a + bb;
+                            oacc[c + hw][i] = a - bb;
+                        }
+#pragma unroll
+            for (int m = 1; m < 16; m <<= 1)
+#pragma unroll
+                for (int c = 0; c < 8; ++c)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float o = __shfl_xor(oacc[c][i], m, 64);
+                        oacc[c][i] = (r16 & m) ? o - oacc[c][i] : oacc[c][i] + o;
+                    }
+            const uint32_t sb = (p.sgn[r16 >> 2] >> (8 * (r16 & 3))) & 0xffu;  // dims 8*r16 .. +7
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float v = oacc[c][i] * p.tab.rot_c;
+                    oacc[c][i] = ((sb >> c) & 1u) ? -v : v;
+                }
+        }
         float l_tot = sum_over_groups(l_part);
         float z_tot = (FMT == FMT_TQ) ? sum_over_groups(z_part) : 0.0f;
         if constexpr (HALF) {
@@ -529,7 +608,7 @@ paged_decode_kernel(DecodeParams p) {
     using GE = Geo<FMT, KB, VB>;
     constexpr int SPP = GE::spp, PF = GE::pf;
     const int n16_k = (int)(page_bytes / 16);
-    const int n16 = (FMT == FMT_TQ) ? n16_k : 2 * n16_k;
+    const int n16 = GE::combined ? n16_k : 2 * n16_k;
     u32x4 stage[PF][SPP];
     auto stage_load = [&](auto slot_c, int i) __attribute__((always_inline)) {
         constexpr int S = decltype(slot_c)::value;
@@ -542,7 +621,7 @@ paged_decode_kernel(DecodeParams p) {
 #pragma unroll
         for (int c = 0; c < SPP; ++c) {
             const int idx = min(tid + c * nthreads, n16 - 1);
-            const u32x4* src = (FMT == FMT_TQ || idx < n16_k) ? ks + idx : vs + (idx - n16_k);
+            const u32x4* src = (GE::combined || idx < n16_k) ? ks + idx : vs + (idx - n16_k);
             stage[S][c] = *src;
         }
     };
@@ -553,7 +632,7 @@ paged_decode_kernel(DecodeParams p) {
 #pragma unroll
         for (int c = 0; c < SPP; ++c) {
             const int idx = tid + c * nthreads;
-            const int off = (FMT == FMT_TQ || idx < n16_k) ? 16 * idx : GE::kHalf + 16 * (idx - n16_k);
+            const int off = (GE::combined || idx < n16_k) ? 16 * idx : GE::kHalf + 16 * (idx - n16_k);
             if (idx < n16) *reinterpret_cast<u32x4*>(buf + off) = stage[S][c];
         }
     };
@@ -915,7 +994,8 @@ paged_decode_kernel(DecodeParams p) {
     auto process = [&](int i, auto buf_c) __attribute__((always_inline)) {
         constexpr int BUF = decltype(buf_c)::value;
         const uint8_t* kpage = smem + BUF * GE::kBuf;
-        const uint8_t* vpage = kpage + GE::kHalf;
+        // V entries: the other cache's page, or the slot's V part
+        const uint8_t* vpage = kpage + (GE::combined ? GE::entry / 2 : GE::kHalf);
         const int info = __builtin_amdgcn_readfirstlane(info_lds[i]);
         const int b = info >> 6;
         const int nv = (info >> 1) & 31;  // valid tokens in this page
@@ -931,7 +1011,36 @@ paged_decode_kernel(DecodeParams p) {
         if constexpr (kStaged) {
             // ---- K operand for token r16
             const uint8_t* ke = kpage + k_off;
-            {
+            if constexpr (FMT == FMT_G4 || FMT == FMT_G3) {
+                // block grp of the K part (dims 32*grp .. +31): code * d + m (4-bit)
+                // or (code - 4) * d (3-bit); MFMA j takes values 8j .. 8j+7
+                constexpr int BE = FMT == FMT_G4 ? 20 : 14;
+                const uint8_t* kb = ke + BE * grp;
+                const float d = f16_bits_to_f32((uint16_t)lds16(kb));
+                const float m = FMT == FMT_G4 ? f16_bits_to_f32((uint16_t)lds16(kb + 2)) : -4.0f * d;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t cw = g32_codes8<FMT>(kb, j);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) a[j][e] = (_Float16)__builtin_fmaf(g32_code<FMT>(cw, e), d, m);
+                }
+                // V of tokens 4*grp + i, dims 8*r16 .. +7: block r16 / 4, values 8 (r16 % 4) ..
+#pragma unroll
+                for (int i2 = 0; i2 < 4; ++i2) {
+                    const bool ok = 4 * grp + i2 < nv;
+                    const uint8_t* vb = vpage + v_off[i2] + BE * (r16 >> 2);
+                    const float dv = f16_bits_to_f32((uint16_t)lds16(vb));
+                    const float mv = FMT == FMT_G4 ? f16_bits_to_f32((uint16_t)lds16(vb + 2)) : -4.0f * dv;
+                    const uint32_t cw = g32_codes8<FMT>(vb, r16 & 3);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float x0 = __builtin_fmaf(g32_code<FMT>(cw, 2 * e), dv, mv);
+                        const float x1 = __builtin_fmaf(g32_code<FMT>(cw, 2 * e + 1), dv, mv);
+                        vw[i2][e] = (uint32_t)f32_to_f16_bits(ok ? x0 : 0.0f) |
+                                    ((uint32_t)f32_to_f16_bits(ok ? x1 : 0.0f) << 16);
+                    }
+                }
+            } else {
                 // GGUF blocks: lane group grp owns block grp (dims 32*grp .. +31)
                 constexpr int BE = FMT == FMT_Q8_0 ? 34 : 18;
                 const uint8_t* kb = ke + BE * grp;
@@ -1488,6 +1597,29 @@ extern "C" int vmc_turboquant_decode_attention(void* output, const void* query, 
     if (half_dtype != VMC_DTYPE_F16 && half_dtype != VMC_DTYPE_BF16) return VMC_EINVAL;
     if (max_num_blocks_per_req > 0x7fffffff) return VMC_EINVAL;
     DecodeParams prm = {};
+    if (cfg->group_size != 0) {
+        // per-32-group variant: fp16 queries; d and m are fp16 whatever the
+        // stored half_dtype of the reference layout would be
+        if (half_dtype != VMC_DTYPE_F16) return VMC_EINVAL;
+        int rc = setup_common(prm, output, query, block_tables, seq_lens, batch_size, num_heads,
+                              num_kv_heads, head_dim, (int)block_size, (int)max_num_blocks_per_req,
+                              scale, max_num_kv_splits, workspace, workspace_bytes);
+        if (rc != VMC_OK) return rc;
+        if (batch_size == 0) return VMC_OK;
+        if (!kv_cache) return VMC_EINVAL;
+        prm.kc = reinterpret_cast<const uint8_t*>(kv_cache);
+        prm.vc = prm.kc;
+        prm.q_bf16 = 0;
+        prm.entry_bytes = cfg->slot_size_aligned;
+        prm.page_bytes = (int64_t)kBs * num_kv_heads * cfg->slot_size_aligned;
+        prm.hnd = 0;
+        prm.tab = tq_tables(head_dim, cfg->key_quant_bits);
+        const G32Signs sg = g32_signs(cfg->sign_seed);
+        for (int i = 0; i < 4; ++i) prm.sgn[i] = sg.w[i];
+        hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+        return cfg->key_quant_bits == 4 ? launch_decode<FMT_G4, 0, 0, false>(prm, s)
+                                        : launch_decode<FMT_G3, 0, 0, false>(prm, s);
+    }
     int rc = setup_common(prm, output, query, block_tables, seq_lens, batch_size, num_heads,
                           num_kv_heads, head_dim, (int)block_size, (int)max_num_blocks_per_req,
                           scale, max_num_kv_splits, workspace, workspace_bytes);

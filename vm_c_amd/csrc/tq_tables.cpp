@@ -81,9 +81,36 @@ const TQTables& tq_tables(int head_dim, int bits) {
     return cache.emplace(key, t).first->second;
 }
 
+G32Signs g32_signs(unsigned long long seed) {
+    auto mix = [](uint64_t x) {
+        x += 0x9e3779b97f4a7c15ULL;
+        x = (x ^ (x >> 30)) * 0xbf58476d1ce4e5b9ULL;
+        x = (x ^ (x >> 27)) * 0x94d049bb133111ebULL;
+        return x ^ (x >> 31);
+    };
+    G32Signs s = {{0u, 0u, 0u, 0u}};
+    if (seed == 0) return s;
+    for (int k = 0; k < 2; ++k) {
+        const uint64_t w = mix(mix(mix(seed) ^ 0x5349474eULL) ^ (uint64_t)k);
+        s.w[2 * k] = (uint32_t)(w & 0xffffffffu);
+        s.w[2 * k + 1] = (uint32_t)(w >> 32);
+    }
+    return s;
+}
+
 bool tq_config_valid(const vmc_tq_config* c) {
     if (!c) return false;
     if (c->key_fp8) return false;
+    if (c->group_size != 0) {
+        // per-32-group variant: head_dim 128, equal K/V bits, the fixed part sizes
+        const int b = c->key_quant_bits;
+        if (c->group_size != 32 || c->head_dim != 128 || (b != 3 && b != 4) || c->value_quant_bits != b)
+            return false;
+        const int part = b == 4 ? 80 : 56;
+        return c->mse_bytes == 16 * b && c->key_packed_size == part && c->val_data_bytes == 16 * b &&
+               c->value_packed_size == part && c->slot_size == 2 * part &&
+               c->slot_size_aligned == 2 * part && c->n_centroids == 0 && c->norm_correction == 0;
+    }
     if (c->head_dim != 64 && c->head_dim != 128 && c->head_dim != 256) return false;
     if (c->key_quant_bits != 3 && c->key_quant_bits != 4) return false;
     if (c->value_quant_bits != 3 && c->value_quant_bits != 4) return false;
@@ -116,6 +143,20 @@ extern "C" int vmc_tq_config_from_method(int head_dim, const char* method, vmc_t
     } else if (m.empty() || m == "turboquant_4bit_nc") {
         c.key_quant_bits = 4;
         c.value_quant_bits = 4;
+    } else if ((m == "turboquant_4bit_g32" || m == "turboquant_3bit_g32") && head_dim == 128) {
+        // per-32-group variant (no reference counterpart): see vmc_attn.h
+        const int b = m == "turboquant_4bit_g32" ? 4 : 3;
+        const int part = b == 4 ? 80 : 56;
+        c.key_quant_bits = c.value_quant_bits = b;
+        c.norm_correction = 0;
+        c.n_centroids = 0;
+        c.mse_bytes = c.val_data_bytes = 16 * b;
+        c.key_packed_size = c.value_packed_size = part;
+        c.slot_size = c.slot_size_aligned = 2 * part;
+        c.group_size = 32;
+        c.sign_seed = 0;
+        *out = c;
+        return VMC_OK;
     } else {
         return VMC_EINVAL;
     }

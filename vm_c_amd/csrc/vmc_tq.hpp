@@ -16,4 +16,12 @@ struct TQTables {
 const TQTables& tq_tables(int head_dim, int bits);
 bool tq_config_valid(const vmc_tq_config* c);
 
+// Rotation signs of the per-32-group variant: bit i of the 128 (word i / 32)
+// set = sign of dim i is -1; bit i % 64 of the splitmix64-mixed words
+// (seed, stream 0x5349474e, i / 64); seed 0: all +1.
+struct G32Signs {
+    uint32_t w[4];
+};
+G32Signs g32_signs(unsigned long long seed);
+
 }  // namespace vmc

@@ -43,10 +43,15 @@ struct TQConfig {
     int slot_size_aligned = 0;
     int n_centroids = 0;
     int max_num_kv_splits = 32;
+    // Not in vm_c: the per-32-group variant of the benchmark configurations
+    // ("turboquant_4bit_g32" / "turboquant_3bit_g32"; format in vmc_attn.h).
+    int group_size = 0;        // 0: the reference layout
+    uint64_t sign_seed = 0;    // rotation signs (0: all +1), the same for store and decode
 
     void compute_layout();
     // "turboquant_4bit_nc" (default), "turboquant_3bit_nc", "turboquant_k3v4_nc",
-    // "turboquant_k8v4"; gpu_device is accepted for signature compatibility
+    // "turboquant_k8v4", and the variants "turboquant_4bit_g32",
+    // "turboquant_3bit_g32"; gpu_device is accepted for signature compatibility
     static TQConfig from_method(int head_dim, const char* method, int gpu_device = 0);
 
     vmc_tq_config to_c() const;

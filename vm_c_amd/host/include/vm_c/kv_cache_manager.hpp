@@ -115,6 +115,7 @@ struct TurboQuantLayout {
     int slot_size = 0;
     int slot_size_aligned = 0;
     int n_centroids = 0;
+    int group_size = 0;  // not in vm_c: 32 for the "*_g32" variants (vmc_attn.h)
 
     // kv_cache_manager.hpp:121-162; an unknown method leaves the 4-bit
     // defaults, as there.  fp8_e4b15 is false (gfx950 has e4m3).

@@ -17,6 +17,14 @@ namespace vm_c {
 // ------------------------------------------------------------ TurboQuant
 
 void TQConfig::compute_layout() {
+    if (group_size != 0) {  // per-32-group variant: two parts of four blocks
+        const int part = key_quant_bits == 4 ? 80 : 56;
+        n_centroids = 0;
+        mse_bytes = val_data_bytes = 16 * key_quant_bits;
+        key_packed_size = value_packed_size = part;
+        slot_size = slot_size_aligned = 2 * part;
+        return;
+    }
     n_centroids = 1 << key_quant_bits;
     if (key_fp8) {
         mse_bytes = head_dim;
@@ -48,6 +56,10 @@ TQConfig TQConfig::from_method(int head_dim_, const char* method, int gpu_device
     } else if (m == "turboquant_3bit_nc") {
         cfg.key_quant_bits = 3;
         cfg.value_quant_bits = 3;
+    } else if (m == "turboquant_4bit_g32" || m == "turboquant_3bit_g32") {
+        cfg.key_quant_bits = cfg.value_quant_bits = m == "turboquant_4bit_g32" ? 4 : 3;
+        cfg.norm_correction = false;
+        cfg.group_size = 32;
     }
     cfg.compute_layout();
     return cfg;
@@ -69,6 +81,8 @@ vmc_tq_config TQConfig::to_c() const {
     c.slot_size_aligned = slot_size_aligned;
     c.n_centroids = n_centroids;
     c.max_num_kv_splits = max_num_kv_splits;
+    c.group_size = group_size;
+    c.sign_seed = sign_seed;
     return c;
 }
 

@@ -116,6 +116,18 @@ TurboQuantLayout TurboQuantLayout::create(int head_dim, const std::string& metho
     } else if (method == "turboquant_3bit_nc") {
         l.key_quant_bits = 3;
         l.value_quant_bits = 3;
+    } else if (method == "turboquant_4bit_g32" || method == "turboquant_3bit_g32") {
+        // per-32-group variant (not in vm_c): K part + V part of four blocks
+        const int b = method == "turboquant_4bit_g32" ? 4 : 3;
+        const int part = b == 4 ? 80 : 56;
+        l.key_quant_bits = l.value_quant_bits = b;
+        l.norm_correction = false;
+        l.group_size = 32;
+        l.n_centroids = 0;
+        l.mse_bytes = l.val_data_bytes = 16 * b;
+        l.key_packed_size = l.value_packed_size = part;
+        l.slot_size = l.slot_size_aligned = 2 * part;
+        return l;
     }
     l.n_centroids = 1 << l.key_quant_bits;
     l.mse_bytes = l.key_fp8 ? head_dim : (head_dim * l.key_quant_bits + 7) / 8;
