@@ -154,6 +154,38 @@ int vmc_turboquant_store(const void* key, const void* value, void* kv_cache,
                          int half_dtype, vmc_stream_t stream);
 
 /*
+ * Fused Q/K RMSNorm + RoPE + quantize-on-append, one launch.
+ * Replaces vm_c::fused_qk_norm_rope_store and vm_c::fused_qk_norm_rope
+ * (include/vm_c/cuda/kernels_fused_attn.h:51-93; fused_attn_kernels.cu:39-313).
+ *   q_buf [num_tokens][num_heads][head_dim], k_buf, v_buf [num_tokens]
+ *   [num_kv_heads][head_dim], all of dtype; q and k are updated in place.
+ *   q_norm_weight [num_heads*head_dim], k_norm_weight [num_kv_heads*head_dim]
+ *   of dtype, or NULL (no norm for that side):
+ *     y = (x * (1/sqrtf(sum(x^2)/head_dim + eps))) * w, rounded to dtype.
+ *   cos_sin_cache [max_pos][head_dim] of dtype, cos in [0, head_dim/2), sin in
+ *   [head_dim/2, head_dim); position_ids int64 [num_tokens].  Neox pairs
+ *   (d, d + head_dim/2), GPT-J pairs (2d, 2d+1); a' = a cos - b sin,
+ *   b' = b cos + a sin, rounded to dtype.
+ *   key_cache == NULL: norm + RoPE only (fused_qk_norm_rope).  Otherwise the
+ *   rotated K row and the V row are appended at slot_mapping (int64, < 0
+ *   skips): tq_config == NULL -> paged pools key_cache / value_cache with
+ *   kv_format, layout and cache_stride as in vmc_reshape_and_cache;
+ *   tq_config != NULL -> packed TurboQuant slots in key_cache (value_cache
+ *   unused), as vmc_turboquant_store writes them.
+ * Limits: head_dim == 128.  The reference's 128-thread reduction across
+ * warps and its GPT-J read of the neox pairs are not reproduced.
+ */
+int vmc_fused_qk_norm_rope_store(void* q_buf, void* k_buf, const void* v_buf,
+                                 const void* q_norm_weight, const void* k_norm_weight,
+                                 const void* cos_sin_cache, const int64_t* position_ids,
+                                 void* key_cache, void* value_cache,
+                                 const int64_t* slot_mapping, int num_tokens, int num_heads,
+                                 int num_kv_heads, int head_dim, float rms_norm_eps,
+                                 int is_neox, int64_t block_size, int64_t cache_stride,
+                                 int kv_format, int layout, const vmc_tq_config* tq_config,
+                                 int dtype, vmc_stream_t stream);
+
+/*
  * Split-KV paged decode over packed TurboQuant slots.
  * Replaces vm_c::turboquant_decode_attention (kernels_turboquant.h:121-138;
  * turboquant_kernels.cu:939-1007): q rotated by the Hadamard transform, K

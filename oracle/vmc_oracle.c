@@ -851,6 +851,81 @@ void orc_g32_decode_exact(double* out, const uint16_t* query, const uint8_t* kv_
 }
 
 /* ------------------------------------------------------------------------ */
+/* fused Q/K RMSNorm + RoPE (src/cuda/fused_attn_kernels.cu:39-313)         */
+/* ------------------------------------------------------------------------ */
+/* Intended semantics of fused_qk_norm_rope_store_kernel, in place on q
+ * [T][Hq][D] and k [T][Hkv][D] (fp16 or bf16 bits):
+ *   RMSNorm (:72-124, when the weight is given): S = sum of x^2 over the
+ *     head's D values, inv = 1 / sqrtf(S / D + eps), y = (x * inv) * w[h*D+d],
+ *     rounded to the element type (the reference writes the buffer back);
+ *   RoPE (:128-178): cos = cache[pos][0 .. D/2), sin = cache[pos][D/2 .. D);
+ *     neox pairs (d, d + D/2), GPT-J pairs (2d, 2d+1), pair index d:
+ *     a' = a*cos[d] - b*sin[d], b' = b*cos[d] + a*sin[d], rounded.
+ * The reference's reduction shuffles across warps of a 128-thread block and
+ * its GPT-J branch reads the neox pairs; those are defects, not semantics.
+ * Declared order of S (shared with the kernel): 16 partial sums, partial j
+ * = fmaf chain over dims 8j .. 8j+7 from 0, then a butterfly over j with
+ * lane distances 1, 2, 4, 8 (s_j += s_{j^m}).  No other contraction. */
+static float norm_sum_sq(const float* x, int D) {
+    float p[32];
+    const int L = D / 8;
+    for (int j = 0; j < L; ++j) {
+        float a = 0.0f;
+        for (int e = 0; e < 8; ++e) a = fmaf(x[8 * j + e], x[8 * j + e], a);
+        p[j] = a;
+    }
+    for (int m = 1; m < L; m <<= 1) {
+        float t[32];
+        for (int j = 0; j < L; ++j) t[j] = p[j] + p[j ^ m];
+        for (int j = 0; j < L; ++j) p[j] = t[j];
+    }
+    return p[0];
+}
+
+static void norm_rope_row(uint16_t* row, const uint16_t* w, const uint16_t* cs, int D, float eps,
+                          int is_neox, int bf16) {
+    float x[256];
+    for (int d = 0; d < D; ++d) x[d] = half_to_f32(row[d], bf16);
+    if (w) {
+        const float S = norm_sum_sq(x, D);
+        const float inv = 1.0f / sqrtf(S / (float)D + eps);
+        for (int d = 0; d < D; ++d) {
+            float t = x[d] * inv;
+            t = t * half_to_f32(w[d], bf16);
+            x[d] = half_to_f32(f32_to_half(t, bf16), bf16);
+        }
+    }
+    const int half = D / 2;
+    for (int d = 0; d < half; ++d) {
+        const int ia = is_neox ? d : 2 * d, ib = is_neox ? d + half : 2 * d + 1;
+        const float a = x[ia], b = x[ib];
+        const float c = half_to_f32(cs[d], bf16), s = half_to_f32(cs[half + d], bf16);
+        float t0 = a * c, t1 = b * s;
+        const float na = t0 - t1;
+        t0 = b * c;
+        t1 = a * s;
+        const float nb = t0 + t1;
+        row[ia] = f32_to_half(na, bf16);
+        row[ib] = f32_to_half(nb, bf16);
+    }
+}
+
+void orc_qk_norm_rope(uint16_t* q, uint16_t* k, const uint16_t* q_weight, const uint16_t* k_weight,
+                      const uint16_t* cos_sin, const int64_t* pos, int T, int Hq, int Hkv, int D,
+                      float eps, int is_neox, int bf16) {
+#pragma omp parallel for schedule(static)
+    for (int t = 0; t < T; ++t) {
+        const uint16_t* cs = cos_sin + pos[t] * D;
+        for (int h = 0; h < Hq; ++h)
+            norm_rope_row(q + ((int64_t)t * Hq + h) * D, q_weight ? q_weight + (int64_t)h * D : NULL, cs, D,
+                          eps, is_neox, bf16);
+        for (int h = 0; h < Hkv; ++h)
+            norm_rope_row(k + ((int64_t)t * Hkv + h) * D, k_weight ? k_weight + (int64_t)h * D : NULL, cs, D,
+                          eps, is_neox, bf16);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
 /* paged decode over f16 / bf16 / q8_0 / q4_0 pages                         */
 /* ------------------------------------------------------------------------ */
 

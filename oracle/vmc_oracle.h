@@ -126,6 +126,16 @@ void orc_g32_decode_exact(double* out, const uint16_t* query, const uint8_t* kv_
                           double scale, int64_t block_size, int64_t max_blocks_per_req,
                           int bits, uint64_t seed, int q_is_bf16, int nthreads);
 
+/* ---- fused Q/K RMSNorm + RoPE (src/cuda/fused_attn_kernels.cu:39-313),
+ * in place; weights and cos/sin cache of the element type; either weight may
+ * be NULL (no norm).  The append that follows is orc_kv_append /
+ * orc_tq_store / orc_g32_store on the updated k and the original v. ---- */
+void orc_qk_norm_rope(uint16_t* q, uint16_t* k, const uint16_t* q_weight,
+                      const uint16_t* k_weight, const uint16_t* cos_sin,
+                      const int64_t* pos, int num_tokens, int num_heads,
+                      int num_kv_heads, int head_dim, float eps, int is_neox,
+                      int half_is_bf16);
+
 /* ---- paged decode over f16/bf16/q8_0/q4_0 pages ---- */
 /* exact fp64 softmax attention over the dequantized pages; q is fp32 */
 void orc_paged_decode_exact(double* out, const float* q,

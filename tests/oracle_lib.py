@@ -82,6 +82,8 @@ def lib():
         L.orc_g32_decode_exact.argtypes = [_P, _P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int,
                                            C.c_double, C.c_int64, C.c_int64, C.c_int, C.c_uint64,
                                            C.c_int, C.c_int]
+        L.orc_qk_norm_rope.argtypes = [_P, _P, _P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int,
+                                        C.c_float, C.c_int, C.c_int]
         L.orc_paged_decode_exact.argtypes = [_P, _P, _P, _P, C.c_int, C.c_int, _P, _P,
                                              C.c_int, C.c_int, C.c_int, C.c_int, C.c_double,
                                              C.c_int64, C.c_int64, C.c_int]
@@ -253,6 +255,21 @@ def g32_decode_exact(q_bits, cache, block_tables, seq_lens, Hkv, scale, block_si
                                _ptr(np.ascontiguousarray(seq_lens, dtype=np.int32)), B, Hq, Hkv, D,
                                scale, block_size, bt.shape[1], bits, seed, int(bf16), nthreads)
     return out
+
+
+def qk_norm_rope(q_bits, k_bits, q_weight, k_weight, cos_sin, pos, eps, is_neox, bf16=False):
+    """In-place restatement on copies; returns (q, k) as uint16 bit arrays."""
+    q = np.ascontiguousarray(q_bits, dtype=np.uint16).copy()
+    k = np.ascontiguousarray(k_bits, dtype=np.uint16).copy()
+    T, Hq, D = q.shape
+    Hkv = k.shape[1]
+    qw = None if q_weight is None else np.ascontiguousarray(q_weight, dtype=np.uint16)
+    kw = None if k_weight is None else np.ascontiguousarray(k_weight, dtype=np.uint16)
+    lib().orc_qk_norm_rope(_ptr(q), _ptr(k), _ptr(qw), _ptr(kw),
+                           _ptr(np.ascontiguousarray(cos_sin, dtype=np.uint16)),
+                           _ptr(np.ascontiguousarray(pos, dtype=np.int64)), T, Hq, Hkv, D, eps,
+                           int(is_neox), int(bf16))
+    return q, k
 
 
 def paged_decode_exact(q, kcache, vcache, fmt, block_tables, seq_lens, Hkv, scale, block_size,

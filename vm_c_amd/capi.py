@@ -71,6 +71,10 @@ def load():
     L.vmc_turboquant_decode_attention.restype = _I
     L.vmc_turboquant_decode_attention.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I64,
                                                   _I64, C.POINTER(TQConfig), _I, _I, _P, _SZ, _P]
+    L.vmc_fused_qk_norm_rope_store.restype = _I
+    L.vmc_fused_qk_norm_rope_store.argtypes = [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I,
+                                               _F, _I, _I64, _I64, _I, _I, C.POINTER(TQConfig), _I,
+                                               _P]
     L.vmc_flash_attention_prefill.restype = _I
     L.vmc_flash_attention_prefill.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P, _P,
                                               _P, _I64, _I, _I, _P]
@@ -226,3 +230,19 @@ def flash_attention_prefill(out, query, key, value, token_positions, num_kv_head
         _ptr(slot_mapping), block_size, kv_format, layout, _stream(stream))
     _check(rc, "vmc_flash_attention_prefill")
     return out
+
+
+def fused_qk_norm_rope_store(q, k, v, q_norm_weight, k_norm_weight, cos_sin_cache, position_ids,
+                             key_cache=None, value_cache=None, slot_mapping=None, block_size=16,
+                             eps=1e-6, is_neox=True, kv_format=KV_F16, layout=LAYOUT_NHD,
+                             cache_stride=0, tq_cfg=None, stream=None):
+    """q [T][Hq][D], k, v [T][Hkv][D] (q, k updated in place); key_cache None:
+    norm + RoPE only; tq_cfg given: TurboQuant slots in key_cache."""
+    T, Hq, D = q.shape
+    Hkv = k.shape[1]
+    rc = load().vmc_fused_qk_norm_rope_store(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(q_norm_weight), _ptr(k_norm_weight), _ptr(cos_sin_cache),
+        _ptr(position_ids), _ptr(key_cache), _ptr(value_cache), _ptr(slot_mapping), T, Hq, Hkv, D,
+        eps, int(bool(is_neox)), block_size, cache_stride, kv_format, layout,
+        None if tq_cfg is None else C.byref(tq_cfg), _dtype_code(q), _stream(stream))
+    _check(rc, "vmc_fused_qk_norm_rope_store")

@@ -1,0 +1,370 @@
+// fused_norm_rope.hip -- Q/K RMSNorm + RoPE + quantize-on-append in one launch.
+//
+// Replaces vm_c::fused_qk_norm_rope_store / fused_qk_norm_rope
+// (include/vm_c/cuda/kernels_fused_attn.h; src/cuda/fused_attn_kernels.cu:
+// 39-313: one 128-thread block per token, serial loops over the heads, the
+// K/V rows copied into fp16 pages).  Here 16 lanes own one (token, head) row,
+// 8 dims each in VGPRs, and the append writes any of the paged formats --
+// fp16/bf16/q8_0/q4_0 pages (NHD/HND), TurboQuant slots, or the per-32-group
+// variant -- from the rotated K row still in registers, so K/V make one trip
+// through HBM.  Semantics (the reference's intent; its cross-warp reduction
+// and its GPT-J read are defects):
+//   RMSNorm (:72-124): S = sum of x^2 over the row, inv = 1/sqrtf(S/D + eps),
+//     y = (x * inv) * w[h*D + d], rounded to the element type; S in the
+//     declared order: lane j's fmaf chain over its 8 dims, then a butterfly
+//     over the 16 lanes (distances 1, 2, 4, 8);
+//   RoPE (:128-178): cos/sin = cache[pos][0, D/2) / [D/2, D); neox pairs
+//     (d, d + D/2), GPT-J pairs (2d, 2d+1); a' = a c - b s, b' = b c + a s,
+//     rounded; the rows are written back in place (Q and K);
+//   append: the rotated K row (as rounded) and the V row, as
+//     vmc_reshape_and_cache / vmc_turboquant_store would write them.
+#include "kv_quant.hpp"
+#include "vmc_store.hpp"
+
+namespace vmc {
+namespace {
+
+enum { ST_NONE = 0, ST_F16 = 1, ST_BF16 = 2, ST_Q8_0 = 3, ST_Q4_0 = 4, ST_TQ = 5, ST_G32 = 6 };
+
+struct FusedParams {
+    uint16_t* q;
+    uint16_t* k;
+    const uint16_t* v;
+    const uint16_t* qw;
+    const uint16_t* kw;
+    const uint16_t* cs;
+    const int64_t* pos;
+    uint8_t* kc;
+    uint8_t* vc;
+    const int64_t* slots;
+    int T, Hq, Hkv;
+    float eps;
+    int neox;
+    int64_t bs;
+    // paged formats
+    int64_t E, stride;
+    int hnd;
+    // TurboQuant slot
+    int SA, mse_bytes, key_packed, val_data;
+    TQTables tab;
+    G32Signs sg;
+};
+
+// The fp32 result is materialised before the conversion (opaque): otherwise
+// fp16(u * w) becomes one v_fma_mix, a single rounding of the exact product
+// where the declared order rounds to fp32 first.
+template <bool BF16>
+__device__ __forceinline__ float round_half(float x) {
+    return half_to_f32<BF16>(f32_to_half<BF16>(opaque(x)));
+}
+
+template <bool BF16>
+__device__ __forceinline__ u32x4 pack8(const float* x) {
+    u32x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        w[e] = (uint32_t)f32_to_half<BF16>(opaque(x[2 * e])) |
+               ((uint32_t)f32_to_half<BF16>(opaque(x[2 * e + 1])) << 16);
+    return w;
+}
+
+// q8_0 / q4_0 block of 32 values held by lanes 4b .. 4b+3 (lane l: values
+// 8l .. 8l+7); the encoders of kv_quant.hpp, element for element
+template <int ST>
+__device__ __forceinline__ void gguf_block4(const float* x, int j, uint8_t* entry, bool write) {
+    const int l = j & 3, ib = j >> 2;
+    if constexpr (ST == ST_Q8_0) {
+        float amax = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[e]));
+#pragma unroll
+        for (int m = 1; m < 4; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 16));
+        const float d = opaque(amax / 127.0f);
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        if (write) {
+            uint16_t* d16 = reinterpret_cast<uint16_t*>(entry + 34 * ib);
+            if (l == 0) d16[0] = f32_to_f16_bits(d);
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                const int q0 = (int)roundf(x[e] * id);
+                const int q1 = (int)roundf(x[e + 1] * id);
+                d16[1 + 4 * l + e / 2] = (uint16_t)((q0 & 0xff) | ((q1 & 0xff) << 8));
+            }
+        }
+    } else {
+        // signed value of the first largest |x| (index order)
+        float amax = 0.0f, mx = 0.0f;
+        int idx = 1 << 20;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float a = fabsf(x[e]);
+            if (amax < a) {
+                amax = a;
+                mx = x[e];
+                idx = 8 * l + e;
+            }
+        }
+#pragma unroll
+        for (int m = 1; m < 4; m <<= 1) {
+            const float a2 = __shfl_xor(amax, m, 16);
+            const float x2 = __shfl_xor(mx, m, 16);
+            const int i2 = __shfl_xor(idx, m, 16);
+            if (a2 > amax || (a2 == amax && i2 < idx)) {
+                amax = a2;
+                mx = x2;
+                idx = i2;
+            }
+        }
+        const float d = opaque(mx / -8.0f);
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint32_t q[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float x0 = __fmul_rn(x[e], id);
+            const int t0 = (int)(int8_t)(int)__fadd_rn(x0, 8.5f);
+            q[e] = (uint32_t)(t0 < 15 ? t0 : 15);
+        }
+        // byte i = value i | value i + 16 << 4: lanes 0, 1 take lanes 2, 3's codes
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            lo |= q[e] << (8 * e);
+            hi |= q[e + 4] << (8 * e);
+        }
+        const uint32_t plo = (uint32_t)__shfl_xor((int)lo, 2, 16);
+        const uint32_t phi = (uint32_t)__shfl_xor((int)hi, 2, 16);
+        if (write) {
+            uint16_t* d16 = reinterpret_cast<uint16_t*>(entry + 18 * ib);
+            if (l == 0) d16[0] = f32_to_f16_bits(d);
+            if (l < 2) {
+                const uint32_t w0 = lo | (plo << 4), w1 = hi | (phi << 4);
+                d16[1 + 4 * l] = (uint16_t)(w0 & 0xffffu);
+                d16[2 + 4 * l] = (uint16_t)(w0 >> 16);
+                d16[3 + 4 * l] = (uint16_t)(w1 & 0xffffu);
+                d16[4 + 4 * l] = (uint16_t)(w1 >> 16);
+            }
+        }
+    }
+}
+
+// Groups 0 .. T*Hkv-1 are the K rows (norm, RoPE, append of K and V), the
+// rest the Q rows; 16 groups per 256-thread workgroup.
+template <bool BF16, int ST, int KB, int VB>
+__global__ void __launch_bounds__(256)
+fused_norm_rope_kernel(FusedParams p) {
+    __shared__ __attribute__((aligned(16))) float sq[16][128];  // TurboQuant norm chain, per group
+    const int lane = threadIdx.x & 63, j = lane & 15;
+    const int gi = threadIdx.x >> 4;
+    const int64_t nk = (int64_t)p.T * p.Hkv;
+    const int64_t ng = nk + (int64_t)p.T * p.Hq;
+    const int64_t g0 = (int64_t)blockIdx.x * 16 + gi;
+    const bool live = g0 < ng;
+    const int64_t g = live ? g0 : 0;  // dead groups repeat row 0 without writing
+    const bool is_k = g < nk;
+    const int64_t t = is_k ? g / p.Hkv : (g - nk) / p.Hq;
+    const int h = is_k ? (int)(g % p.Hkv) : (int)((g - nk) % p.Hq);
+    uint16_t* row = is_k ? p.k + (t * p.Hkv + h) * 128 : p.q + (t * p.Hq + h) * 128;
+    const uint16_t* w = is_k ? p.kw : p.qw;
+
+    float x[8];
+    load8<BF16>(row + 8 * j, x);
+    if (w) {  // the same in the whole group
+        float s = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s = __builtin_fmaf(x[e], x[e], s);
+#pragma unroll
+        for (int m = 1; m < 16; m <<= 1) s = s + __shfl_xor(s, m, 16);
+        const float inv = 1.0f / sqrtf(s / 128.0f + p.eps);
+        float wv[8];
+        load8<BF16>(w + (int64_t)h * 128 + 8 * j, wv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float u = x[e] * inv;
+            u = u * wv[e];
+            x[e] = round_half<BF16>(u);
+        }
+    }
+    // RoPE
+    const uint16_t* cs = p.cs + p.pos[t] * 128;
+    float y[8];
+    if (p.neox) {
+        // lane j < 8 holds a (dims 8j ..), lane j + 8 the b of the same pairs
+        const int d0 = 8 * (j & 7);
+        float c[8], sn[8], o[8];
+        load8<BF16>(cs + d0, c);
+        load8<BF16>(cs + 64 + d0, sn);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = __shfl_xor(x[e], 8, 16);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            if (j < 8) {
+                const float t0 = x[e] * c[e], t1 = o[e] * sn[e];
+                y[e] = t0 - t1;
+            } else {
+                const float t0 = x[e] * c[e], t1 = o[e] * sn[e];
+                y[e] = t0 + t1;
+            }
+        }
+    } else {
+        // pairs (8j + 2i, 8j + 2i + 1), pair index 4j + i
+        const uint16_t* cp = cs + 4 * j;
+        const uint2 cw = *reinterpret_cast<const uint2*>(cp);
+        const uint2 sw = *reinterpret_cast<const uint2*>(cp + 64);
+        const uint32_t cc[2] = {cw.x, cw.y}, ss[2] = {sw.x, sw.y};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float c = half_to_f32<BF16>((uint16_t)(cc[i >> 1] >> (16 * (i & 1))));
+            const float sn = half_to_f32<BF16>((uint16_t)(ss[i >> 1] >> (16 * (i & 1))));
+            const float a = x[2 * i], b = x[2 * i + 1];
+            float t0 = a * c, t1 = b * sn;
+            y[2 * i] = t0 - t1;
+            t0 = b * c;
+            t1 = a * sn;
+            y[2 * i + 1] = t0 + t1;
+        }
+    }
+    const u32x4 yw = pack8<BF16>(y);
+    if (live) *reinterpret_cast<u32x4*>(row + 8 * j) = yw;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = round_half<BF16>(y[e]);
+
+    // ---- append (K rows)
+    if constexpr (ST != ST_NONE) {
+        if (is_k) {
+            const int64_t slot = live ? p.slots[t] : -1;
+            const bool wr = slot >= 0;
+            float vv[8];
+            const uint16_t* vrow = p.v + (t * p.Hkv + h) * 128;
+            if constexpr (ST == ST_TQ || ST == ST_G32) {
+                load8<BF16>(vrow + 8 * j, vv);
+                const int64_t blk = slot / p.bs, off = slot % p.bs;
+                uint8_t* sp = p.kc + blk * p.bs * p.Hkv * p.SA + off * p.Hkv * p.SA + (int64_t)h * p.SA;
+                if constexpr (ST == ST_TQ) {
+                    tq_store_vec<128, KB, VB, BF16>(y, vv, j, sp, wr, sq[gi], p.tab, p.mse_bytes, p.key_packed,
+                                                    p.val_data);
+                } else {
+                    constexpr int P = KB == 4 ? 80 : 56;
+                    const uint32_t sbits = (p.sg.w[j >> 2] >> (8 * (j & 3))) & 0xffu;
+                    g32_rotate(y, j, sbits, p.tab.rot_c);
+                    g32_quantize<KB>(y, j, sp, wr);
+                    g32_rotate(vv, j, sbits, p.tab.rot_c);
+                    g32_quantize<KB>(vv, j, sp + P, wr);
+                }
+            } else {
+                const int64_t eo = kv_entry_offset(wr ? slot : 0, h, p.bs, p.Hkv, p.E, p.stride, p.hnd != 0);
+                if constexpr (ST == ST_F16 || ST == ST_BF16) {
+                    constexpr bool DB = ST == ST_BF16;
+                    u32x4 vw = *reinterpret_cast<const u32x4*>(vrow + 8 * j);
+                    if constexpr (DB != BF16) {
+                        load8<BF16>(vrow + 8 * j, vv);
+                        vw = pack8<DB>(vv);
+                    }
+                    if (wr) {
+                        *reinterpret_cast<u32x4*>(p.kc + eo + 16 * j) = DB == BF16 ? yw : pack8<DB>(y);
+                        *reinterpret_cast<u32x4*>(p.vc + eo + 16 * j) = vw;
+                    }
+                } else {
+                    load8<BF16>(vrow + 8 * j, vv);
+                    gguf_block4<ST>(y, j, p.kc + eo, wr);
+                    gguf_block4<ST>(vv, j, p.vc + eo, wr);
+                }
+            }
+        }
+    }
+}
+
+template <bool BF16, int ST, int KB = 0, int VB = 0>
+int launch_fused(const FusedParams& prm, hipStream_t s) {
+    const int64_t ng = (int64_t)prm.T * (prm.Hq + prm.Hkv);
+    const int64_t grid = (ng + 15) / 16;
+    if (grid > 0x7fffffff) return VMC_EINVAL;
+    if (grid == 0) return VMC_OK;
+    hipLaunchKernelGGL((fused_norm_rope_kernel<BF16, ST, KB, VB>), dim3((unsigned)grid), dim3(256), 0, s, prm);
+    VMC_LAUNCH_CHECK();
+    return VMC_OK;
+}
+
+template <bool BF16>
+int dispatch(const FusedParams& prm, int st, const vmc_tq_config* c, hipStream_t s) {
+    switch (st) {
+        case ST_NONE: return launch_fused<BF16, ST_NONE>(prm, s);
+        case ST_F16: return launch_fused<BF16, ST_F16>(prm, s);
+        case ST_BF16: return launch_fused<BF16, ST_BF16>(prm, s);
+        case ST_Q8_0: return launch_fused<BF16, ST_Q8_0>(prm, s);
+        case ST_Q4_0: return launch_fused<BF16, ST_Q4_0>(prm, s);
+        case ST_G32:
+            return c->key_quant_bits == 4 ? launch_fused<BF16, ST_G32, 4, 4>(prm, s)
+                                          : launch_fused<BF16, ST_G32, 3, 3>(prm, s);
+        case ST_TQ: {
+            const int kb = c->key_quant_bits, vb = c->value_quant_bits;
+            if (kb == 4 && vb == 4) return launch_fused<BF16, ST_TQ, 4, 4>(prm, s);
+            if (kb == 3 && vb == 3) return launch_fused<BF16, ST_TQ, 3, 3>(prm, s);
+            if (kb == 3 && vb == 4) return launch_fused<BF16, ST_TQ, 3, 4>(prm, s);
+            return VMC_EINVAL;
+        }
+        default: return VMC_EINVAL;
+    }
+}
+
+}  // namespace
+}  // namespace vmc
+
+using namespace vmc;
+
+extern "C" int vmc_fused_qk_norm_rope_store(void* q_buf, void* k_buf, const void* v_buf,
+                                            const void* q_norm_weight, const void* k_norm_weight,
+                                            const void* cos_sin_cache, const int64_t* position_ids,
+                                            void* key_cache, void* value_cache,
+                                            const int64_t* slot_mapping, int num_tokens,
+                                            int num_heads, int num_kv_heads, int head_dim,
+                                            float rms_norm_eps, int is_neox, int64_t block_size,
+                                            int64_t cache_stride, int kv_format, int layout,
+                                            const vmc_tq_config* tq_config, int dtype,
+                                            vmc_stream_t stream) {
+    if (head_dim != 128 || num_tokens < 0 || num_heads <= 0 || num_kv_heads <= 0) return VMC_EINVAL;
+    if (dtype != VMC_DTYPE_F16 && dtype != VMC_DTYPE_BF16) return VMC_EINVAL;
+    if (num_tokens == 0) return VMC_OK;
+    if (!q_buf || !k_buf || !cos_sin_cache || !position_ids) return VMC_EINVAL;
+    FusedParams prm = {};
+    prm.q = reinterpret_cast<uint16_t*>(q_buf);
+    prm.k = reinterpret_cast<uint16_t*>(k_buf);
+    prm.v = reinterpret_cast<const uint16_t*>(v_buf);
+    prm.qw = reinterpret_cast<const uint16_t*>(q_norm_weight);
+    prm.kw = reinterpret_cast<const uint16_t*>(k_norm_weight);
+    prm.cs = reinterpret_cast<const uint16_t*>(cos_sin_cache);
+    prm.pos = position_ids;
+    prm.T = num_tokens;
+    prm.Hq = num_heads;
+    prm.Hkv = num_kv_heads;
+    prm.eps = rms_norm_eps;
+    prm.neox = is_neox != 0;
+    int st = ST_NONE;
+    if (key_cache) {
+        if (!v_buf || !slot_mapping || block_size <= 0) return VMC_EINVAL;
+        prm.kc = reinterpret_cast<uint8_t*>(key_cache);
+        prm.slots = slot_mapping;
+        prm.bs = block_size;
+        if (tq_config) {
+            if (!tq_config_valid(tq_config) || tq_config->head_dim != head_dim) return VMC_EINVAL;
+            prm.SA = tq_config->slot_size_aligned;
+            prm.mse_bytes = tq_config->mse_bytes;
+            prm.key_packed = tq_config->key_packed_size;
+            prm.val_data = tq_config->val_data_bytes;
+            prm.tab = tq_tables(head_dim, tq_config->key_quant_bits);
+            prm.sg = g32_signs(tq_config->sign_seed);
+            st = tq_config->group_size != 0 ? ST_G32 : ST_TQ;
+        } else {
+            const int64_t E = vmc_kv_entry_bytes(kv_format, head_dim);
+            if (E < 0 || !value_cache) return VMC_EINVAL;
+            if (layout != VMC_LAYOUT_NHD && layout != VMC_LAYOUT_HND) return VMC_EINVAL;
+            prm.vc = reinterpret_cast<uint8_t*>(value_cache);
+            prm.E = E;
+            prm.stride = cache_stride > 0 ? cache_stride : block_size * num_kv_heads * E;
+            prm.hnd = layout == VMC_LAYOUT_HND;
+            st = kv_format == VMC_KV_F16 ? ST_F16 : kv_format == VMC_KV_BF16 ? ST_BF16
+               : kv_format == VMC_KV_Q8_0 ? ST_Q8_0 : ST_Q4_0;
+        }
+    }
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    return dtype == VMC_DTYPE_BF16 ? dispatch<true>(prm, st, tq_config, s) : dispatch<false>(prm, st, tq_config, s);
+}
