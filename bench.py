@@ -16,6 +16,8 @@ Also measured in the same run (extra fields of the same line):
     a 16-bit scale per 32 values, 112-byte slots);
   * causal prefill: batch 4 x 4096 tokens, 32/8 heads, bf16, fused q8_0
     quantize-on-append into the paged cache -> TFLOP/s;
+  * fused_norm_rope: Q/K RMSNorm + RoPE + q8_0 append of the same prefill
+    batch (16384 tokens, 32/8 heads, bf16) in one launch -> GB/s;
   * cpu_baseline: the CPU restatement of the TurboQuant decode (OpenMP over
     all host cores) on a bounded sample of the same workload.
 
@@ -196,6 +198,59 @@ def bench_prefill(args, torch, capi, dev):
     return dict(ms=ms, tflops=tflops, flops=flops)
 
 
+# ------------------------------------------------------------------ fused norm + RoPE + append
+
+def bench_fused_norm_rope(args, torch, capi, dev):
+    """One launch over the prefill batch: q/k RMSNorm + neox RoPE in place,
+    K (rotated) and V appended as q8_0 pages.  Algorithmic bytes: q and k read
+    and written, v read, the page entries written, slots and positions read,
+    the distinct cos/sin rows and the norm weights read once."""
+    B, S, Hq, Hkv = 4, 4096, 32, 8
+    T = B * S
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    q = torch.randn((T, Hq, D), generator=gen, device=dev).bfloat16()
+    k = torch.randn((T, Hkv, D), generator=gen, device=dev).bfloat16()
+    v = torch.randn((T, Hkv, D), generator=gen, device=dev).bfloat16()
+    qw = (1.0 + 0.1 * torch.randn(Hq * D, generator=gen, device=dev)).bfloat16()
+    kw = (1.0 + 0.1 * torch.randn(Hkv * D, generator=gen, device=dev)).bfloat16()
+    theta = 10000.0 ** (-torch.arange(D // 2, device=dev, dtype=torch.float64) * 2.0 / D)
+    ang = torch.arange(S, device=dev, dtype=torch.float64)[:, None] * theta[None, :]
+    cs = torch.cat([ang.cos(), ang.sin()], dim=1).bfloat16().contiguous()
+    pos = torch.arange(S, dtype=torch.int64, device=dev).repeat(B)
+    nblk = T // BS
+    perm = torch.randperm(nblk, generator=torch.Generator().manual_seed(5)).to(dev)
+    t = torch.arange(T, device=dev)
+    slots = (perm[t // BS] * BS + t % BS).to(torch.int64)
+    E = capi.kv_entry_bytes(capi.KV_Q8_0, D)
+    kc = torch.empty(nblk * BS * Hkv * E, dtype=torch.uint8, device=dev)
+    vc = torch.empty_like(kc)
+    stream = torch.cuda.current_stream()
+
+    def run():
+        capi.fused_qk_norm_rope_store(q, k, v, qw, kw, cs, pos, kc, vc, slots, BS, eps=1e-6,
+                                      is_neox=True, kv_format=capi.KV_Q8_0, stream=stream)
+
+    for _ in range(max(2, args.warmup // 2)):
+        run()
+    torch.cuda.synchronize()
+    n = max(5, args.steps // 2)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(n):
+        run()
+    e1.record(stream)
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / n
+    per_token = 2 * 2 * (Hq + Hkv) * D + 2 * Hkv * D + 2 * Hkv * E + 16
+    nbytes = T * per_token + S * D * 2 + (Hq + Hkv) * D * 2
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    assert torch.isfinite(q.float()).all().item(), "fused norm/RoPE produced non-finite values"
+    log(f"fused norm+rope+append {ms * 1e3:.1f} us, {gbs:.0f} GB/s")
+    return dict(ms=ms, gbs=gbs, bytes=nbytes)
+
+
 # ------------------------------------------------------------------ CPU baseline
 
 def cpu_baseline(dec, torch):
@@ -293,6 +348,7 @@ def main():
         del v
         torch.cuda.empty_cache()
     pre = None if args.skip_prefill else bench_prefill(args, torch, capi, dev)
+    fused = None if args.skip_prefill else bench_fused_norm_rope(args, torch, capi, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline(dec, torch)
 
     ms_step = dec["ms_step"]
@@ -333,6 +389,11 @@ def main():
         line["prefill"] = {"workload": "causal prefill B=4 S=4096 Hq=32 Hkv=8 bf16, fused q8_0 append",
                            "ms": round(pre["ms"], 4), "tflops": round(pre["tflops"], 1),
                            "pct_peak_mfma_bf16": round(100 * pre["tflops"] / MFMA_BF16_PEAK_TFLOPS, 2)}
+    if fused is not None:
+        line["fused_norm_rope"] = {
+            "workload": "q/k RMSNorm + neox RoPE + q8_0 K/V append, 16384 tokens, Hq=32 Hkv=8 bf16",
+            "ms": round(fused["ms"], 4), "gbs": round(fused["gbs"], 1),
+            "frac_hbm": round(fused["gbs"] / HBM_PEAK_GBS, 4), "bytes": fused["bytes"]}
     print(json.dumps(line), flush=True)
 
 

@@ -11,6 +11,7 @@
 
 #include "vm_c/attention_backend.hpp"
 #include "vm_c/attention_metadata.hpp"
+#include "vm_c/kernels_fused_attn.hpp"
 #include "vm_c/kv_cache_manager.hpp"
 #include "vmc_oracle.h"
 
@@ -220,6 +221,61 @@ static void test_paged_backend(const std::string& dtype, const std::string& layo
     std::printf("  decode max err %.3g\n", err);
 }
 
+// vm_c::fused_qk_norm_rope_store through the host layer: q/k in place and the
+// appended pages (reference placement: HND) bit-exact against the oracle's
+// norm + RoPE followed by its append
+static void test_fused_norm_rope(const std::string& dtype) {
+    std::printf("case: fused_qk_norm_rope_store %s\n", dtype.c_str());
+    std::fflush(stdout);
+    const int T = 37, P = 64, nblk = 4;
+    std::vector<uint16_t> q((size_t)T * Hq * D), k((size_t)T * Hkv * D), v(k.size());
+    std::vector<uint16_t> qw((size_t)Hq * D), kw((size_t)Hkv * D), cs((size_t)P * D);
+    orc_randn_f16(q.data(), (int64_t)q.size(), 21, 1);
+    orc_randn_f16(k.data(), (int64_t)k.size(), 21, 2);
+    orc_randn_f16(v.data(), (int64_t)v.size(), 21, 3);
+    for (size_t i = 0; i < qw.size(); ++i) qw[i] = orc_f32_to_f16(1.0f + 0.01f * (float)(i % 17));
+    for (size_t i = 0; i < kw.size(); ++i) kw[i] = orc_f32_to_f16(0.9f + 0.01f * (float)(i % 13));
+    for (int p = 0; p < P; ++p)
+        for (int d = 0; d < D / 2; ++d) {
+            const double a = p * std::pow(10000.0, -2.0 * d / D);
+            cs[(size_t)p * D + d] = orc_f32_to_f16((float)std::cos(a));
+            cs[(size_t)p * D + D / 2 + d] = orc_f32_to_f16((float)std::sin(a));
+        }
+    std::vector<int64_t> pos(T), slots(T);
+    for (int t = 0; t < T; ++t) {
+        pos[t] = (t * 7) % P;
+        slots[t] = (int64_t)((t * 5) % (nblk * BS));
+    }
+    slots[3] = -1;
+    const int fmt = dtype == "q8_0" ? ORC_KV_Q8_0 : dtype == "q4_0" ? ORC_KV_Q4_0 : ORC_KV_F16;
+    const size_t E = (size_t)vmc_kv_entry_bytes(fmt == ORC_KV_Q8_0 ? VMC_KV_Q8_0 : fmt == ORC_KV_Q4_0 ? VMC_KV_Q4_0 : VMC_KV_F16, D);
+    const size_t pool_n = (size_t)nblk * BS * Hkv * E;
+    Dev<uint16_t> dq(q), dk(k), dv(v), dqw(qw), dkw(kw), dcs(cs);
+    Dev<int64_t> dpos(pos), dslots(slots);
+    Dev<uint8_t> kc(pool_n), vc(pool_n);
+    HIP_CHECK(hipMemset(kc.p, 0, pool_n));
+    HIP_CHECK(hipMemset(vc.p, 0, pool_n));
+    fused_qk_norm_rope_store(dq.p, dk.p, dv.p, dqw.p, dkw.p, dcs.p, dpos.p, kc.p, vc.p, dslots.p, T, Hq,
+                             Hkv, D, 1e-6f, true, BS, 0, dtype, nullptr);
+    HIP_CHECK(hipDeviceSynchronize());
+    std::vector<uint16_t> rq = q, rk = k;
+    orc_qk_norm_rope(rq.data(), rk.data(), qw.data(), kw.data(), cs.data(), pos.data(), T, Hq, Hkv, D,
+                     1e-6f, 1, 0);
+    std::vector<uint8_t> ek(pool_n, 0), ev(pool_n, 0);
+    orc_kv_append(rk.data(), v.data(), 0, ek.data(), ev.data(), slots.data(), T, Hkv, D, BS, fmt, 1);
+    CHECK(dq.get() == rq);
+    CHECK(dk.get() == rk);
+    CHECK(kc.get() == ek && vc.get() == ev);
+    // norm + RoPE only, on the updated rows again (no norm weights: RoPE twice)
+    fused_qk_norm_rope(dq.p, dk.p, nullptr, nullptr, dcs.p, dpos.p, T, Hq, Hkv, D, 1e-6f, false,
+                       nullptr);
+    HIP_CHECK(hipDeviceSynchronize());
+    orc_qk_norm_rope(rq.data(), rk.data(), nullptr, nullptr, cs.data(), pos.data(), T, Hq, Hkv, D,
+                     1e-6f, 0, 0);
+    CHECK(dq.get() == rq);
+    CHECK(dk.get() == rk);
+}
+
 int main() {
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || n < 1) {
@@ -233,6 +289,8 @@ int main() {
         test_paged_backend("q8_0", "nhd");
         test_paged_backend("q4_0", "hnd");
         test_paged_backend("fp16", "hnd");
+        test_fused_norm_rope("q4_0");
+        test_fused_norm_rope("auto");
     } catch (const std::exception& e) {
         std::printf("FAIL exception: %s\n", e.what());
         return 1;

@@ -140,10 +140,13 @@ def test_g32_append(dev, bf16, method):
 
 
 def test_gqa_shapes_and_single_token(dev):
-    # decode-shaped calls: one token per sequence, wide GQA
+    # decode-shaped calls: one token per sequence, wide GQA; head counts that
+    # give one, two or four rows per 16-lane group
     _run(dev, 1, 64, 8, False, True, "both", seed=11, store=("page", O.KV_Q8_0, False))
     _run(dev, 32, 32, 8, True, True, "both", seed=12, store=("page", O.KV_Q4_0, True))
-    _run(dev, 3, 8, 1, False, False, "none", seed=13)
+    _run(dev, 3, 8, 1, False, False, "none", seed=13)         # one row per group
+    _run(dev, 19, 6, 2, True, False, "both", seed=14, store=("tq", "turboquant_4bit_nc"))  # two rows
+    _run(dev, 9, 12, 2, False, True, "k", seed=15, store=("page", O.KV_F16, True))
 
 
 def test_zero_tokens_and_bad_args(dev):

@@ -114,7 +114,9 @@ SELFTEST_CHECKS = {1: "sum over rows", 2: "max over rows", 4: "LDS gather",
                    8: "mfma 16x16x32 f16", 16: "mfma 16x16x16 f16", 32: "mfma 32x32x16 f16",
                    64: "mfma 16x16x32 bf16", 128: "mfma 32x32x16 bf16",
                    256: "mfma 16x16x16 f16 subnormal operands", 512: "LDS gather from the diagonal",
-                   1024: "mfma 16x16x32 f16 subnormal operands"}
+                   1024: "mfma 16x16x32 f16 subnormal operands",
+                   2048: "bf16 conversion instruction vs the integer rounding rule",
+                   4096: "16-lane DPP xor exchanges", 8192: "16-lane DPP row sum"}
 
 
 def selftest():

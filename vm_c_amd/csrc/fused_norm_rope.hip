@@ -77,8 +77,8 @@ __device__ __forceinline__ void gguf_block4(const float* x, int j, uint8_t* entr
         float amax = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[e]));
-#pragma unroll
-        for (int m = 1; m < 4; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 16));
+        amax = fmaxf(amax, row_xor<1>(amax, j));
+        amax = fmaxf(amax, row_xor<2>(amax, j));
         const float d = opaque(amax / 127.0f);
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
         if (write) {
@@ -104,17 +104,17 @@ __device__ __forceinline__ void gguf_block4(const float* x, int j, uint8_t* entr
                 idx = 8 * l + e;
             }
         }
-#pragma unroll
-        for (int m = 1; m < 4; m <<= 1) {
-            const float a2 = __shfl_xor(amax, m, 16);
-            const float x2 = __shfl_xor(mx, m, 16);
-            const int i2 = __shfl_xor(idx, m, 16);
+        static_for<2>([&](auto m) {
+            constexpr int M = 1 << decltype(m)::value;
+            const float a2 = row_xor<M>(amax, j);
+            const float x2 = row_xor<M>(mx, j);
+            const int i2 = row_xor<M>(idx, j);
             if (a2 > amax || (a2 == amax && i2 < idx)) {
                 amax = a2;
                 mx = x2;
                 idx = i2;
             }
-        }
+        });
         const float d = opaque(mx / -8.0f);
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
         uint32_t q[8];
@@ -131,8 +131,8 @@ __device__ __forceinline__ void gguf_block4(const float* x, int j, uint8_t* entr
             lo |= q[e] << (8 * e);
             hi |= q[e + 4] << (8 * e);
         }
-        const uint32_t plo = (uint32_t)__shfl_xor((int)lo, 2, 16);
-        const uint32_t phi = (uint32_t)__shfl_xor((int)hi, 2, 16);
+        const uint32_t plo = row_xor_u32<2>(lo, j);
+        const uint32_t phi = row_xor_u32<2>(hi, j);
         if (write) {
             uint16_t* d16 = reinterpret_cast<uint16_t*>(entry + 18 * ib);
             if (l == 0) d16[0] = f32_to_f16_bits(d);
@@ -147,141 +147,188 @@ __device__ __forceinline__ void gguf_block4(const float* x, int j, uint8_t* entr
     }
 }
 
-// Groups 0 .. T*Hkv-1 are the K rows (norm, RoPE, append of K and V), the
-// rest the Q rows; 16 groups per 256-thread workgroup.
-template <bool BF16, int ST, int KB, int VB>
+template <bool BF16>
+__device__ __forceinline__ void unpack8(const u32x4 w, float* x) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        x[2 * e] = half_to_f32<BF16>((uint16_t)(w[e] & 0xffffu));
+        x[2 * e + 1] = half_to_f32<BF16>((uint16_t)(w[e] >> 16));
+    }
+}
+
+// Each 16-lane group owns R consecutive rows (heads h0 .. h0+R-1 of one
+// token); groups 0 .. T*Hkv/R-1 are the K rows (norm, RoPE, append of K and
+// V), the rest the Q rows; 16 groups per 256-thread workgroup.  Every load of
+// the group's rows is issued before the first row is processed.
+template <bool BF16, int ST, int KB, int VB, int R>
 __global__ void __launch_bounds__(256)
 fused_norm_rope_kernel(FusedParams p) {
     __shared__ __attribute__((aligned(16))) float sq[16][128];  // TurboQuant norm chain, per group
     const int lane = threadIdx.x & 63, j = lane & 15;
     const int gi = threadIdx.x >> 4;
-    const int64_t nk = (int64_t)p.T * p.Hkv;
-    const int64_t ng = nk + (int64_t)p.T * p.Hq;
+    const int64_t nk = (int64_t)p.T * (p.Hkv / R);
+    const int64_t ng = nk + (int64_t)p.T * (p.Hq / R);
     const int64_t g0 = (int64_t)blockIdx.x * 16 + gi;
     const bool live = g0 < ng;
     const int64_t g = live ? g0 : 0;  // dead groups repeat row 0 without writing
     const bool is_k = g < nk;
-    const int64_t t = is_k ? g / p.Hkv : (g - nk) / p.Hq;
-    const int h = is_k ? (int)(g % p.Hkv) : (int)((g - nk) % p.Hq);
-    uint16_t* row = is_k ? p.k + (t * p.Hkv + h) * 128 : p.q + (t * p.Hq + h) * 128;
+    const int H = is_k ? p.Hkv : p.Hq;
+    const int64_t r0 = (is_k ? g : g - nk) * R;  // row t*H + h0
+    const int64_t t = r0 / H;
+    const int h0 = (int)(r0 % H);
+    uint16_t* rows = (is_k ? p.k : p.q) + r0 * 128;
     const uint16_t* w = is_k ? p.kw : p.qw;
 
-    float x[8];
-    load8<BF16>(row + 8 * j, x);
-    if (w) {  // the same in the whole group
-        float s = 0.0f;
+    // ---- loads
+    u32x4 xr[R], wr_[R], vr[R];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) s = __builtin_fmaf(x[e], x[e], s);
+    for (int r = 0; r < R; ++r) xr[r] = *reinterpret_cast<const u32x4*>(rows + r * 128 + 8 * j);
+    if constexpr (ST != ST_NONE) {
+        if (is_k) {
 #pragma unroll
-        for (int m = 1; m < 16; m <<= 1) s = s + __shfl_xor(s, m, 16);
-        const float inv = 1.0f / sqrtf(s / 128.0f + p.eps);
-        float wv[8];
-        load8<BF16>(w + (int64_t)h * 128 + 8 * j, wv);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            float u = x[e] * inv;
-            u = u * wv[e];
-            x[e] = round_half<BF16>(u);
+            for (int r = 0; r < R; ++r)
+                vr[r] = *reinterpret_cast<const u32x4*>(p.v + (r0 + r) * 128 + 8 * j);
         }
     }
-    // RoPE
     const uint16_t* cs = p.cs + p.pos[t] * 128;
-    float y[8];
+    float c[8], sn[8];
     if (p.neox) {
         // lane j < 8 holds a (dims 8j ..), lane j + 8 the b of the same pairs
         const int d0 = 8 * (j & 7);
-        float c[8], sn[8], o[8];
         load8<BF16>(cs + d0, c);
         load8<BF16>(cs + 64 + d0, sn);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = __shfl_xor(x[e], 8, 16);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            if (j < 8) {
-                const float t0 = x[e] * c[e], t1 = o[e] * sn[e];
-                y[e] = t0 - t1;
-            } else {
-                const float t0 = x[e] * c[e], t1 = o[e] * sn[e];
-                y[e] = t0 + t1;
-            }
-        }
     } else {
         // pairs (8j + 2i, 8j + 2i + 1), pair index 4j + i
-        const uint16_t* cp = cs + 4 * j;
-        const uint2 cw = *reinterpret_cast<const uint2*>(cp);
-        const uint2 sw = *reinterpret_cast<const uint2*>(cp + 64);
+        const uint2 cw = *reinterpret_cast<const uint2*>(cs + 4 * j);
+        const uint2 sw = *reinterpret_cast<const uint2*>(cs + 64 + 4 * j);
         const uint32_t cc[2] = {cw.x, cw.y}, ss[2] = {sw.x, sw.y};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float c = half_to_f32<BF16>((uint16_t)(cc[i >> 1] >> (16 * (i & 1))));
-            const float sn = half_to_f32<BF16>((uint16_t)(ss[i >> 1] >> (16 * (i & 1))));
-            const float a = x[2 * i], b = x[2 * i + 1];
-            float t0 = a * c, t1 = b * sn;
-            y[2 * i] = t0 - t1;
-            t0 = b * c;
-            t1 = a * sn;
-            y[2 * i + 1] = t0 + t1;
+            c[i] = half_to_f32<BF16>((uint16_t)(cc[i >> 1] >> (16 * (i & 1))));
+            sn[i] = half_to_f32<BF16>((uint16_t)(ss[i >> 1] >> (16 * (i & 1))));
         }
     }
-    const u32x4 yw = pack8<BF16>(y);
-    if (live) *reinterpret_cast<u32x4*>(row + 8 * j) = yw;
+    if (w) {  // the same in the whole group
 #pragma unroll
-    for (int e = 0; e < 8; ++e) y[e] = round_half<BF16>(y[e]);
-
-    // ---- append (K rows)
+        for (int r = 0; r < R; ++r)
+            wr_[r] = *reinterpret_cast<const u32x4*>(w + (int64_t)(h0 + r) * 128 + 8 * j);
+    }
+    int64_t slot = -1;
     if constexpr (ST != ST_NONE) {
-        if (is_k) {
-            const int64_t slot = live ? p.slots[t] : -1;
-            const bool wr = slot >= 0;
-            float vv[8];
-            const uint16_t* vrow = p.v + (t * p.Hkv + h) * 128;
-            if constexpr (ST == ST_TQ || ST == ST_G32) {
-                load8<BF16>(vrow + 8 * j, vv);
-                const int64_t blk = slot / p.bs, off = slot % p.bs;
-                uint8_t* sp = p.kc + blk * p.bs * p.Hkv * p.SA + off * p.Hkv * p.SA + (int64_t)h * p.SA;
-                if constexpr (ST == ST_TQ) {
-                    tq_store_vec<128, KB, VB, BF16>(y, vv, j, sp, wr, sq[gi], p.tab, p.mse_bytes, p.key_packed,
-                                                    p.val_data);
-                } else {
-                    constexpr int P = KB == 4 ? 80 : 56;
-                    const uint32_t sbits = (p.sg.w[j >> 2] >> (8 * (j & 3))) & 0xffu;
-                    g32_rotate(y, j, sbits, p.tab.rot_c);
-                    g32_quantize<KB>(y, j, sp, wr);
-                    g32_rotate(vv, j, sbits, p.tab.rot_c);
-                    g32_quantize<KB>(vv, j, sp + P, wr);
-                }
-            } else {
-                const int64_t eo = kv_entry_offset(wr ? slot : 0, h, p.bs, p.Hkv, p.E, p.stride, p.hnd != 0);
-                if constexpr (ST == ST_F16 || ST == ST_BF16) {
-                    constexpr bool DB = ST == ST_BF16;
-                    u32x4 vw = *reinterpret_cast<const u32x4*>(vrow + 8 * j);
-                    if constexpr (DB != BF16) {
-                        load8<BF16>(vrow + 8 * j, vv);
-                        vw = pack8<DB>(vv);
+        if (is_k && live) slot = p.slots[t];
+    }
+
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int h = h0 + r;
+        float x[8];
+        unpack8<BF16>(xr[r], x);
+        if (w) {
+            float s = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s = __builtin_fmaf(x[e], x[e], s);
+            s = row_sum16(s);
+            const float inv = 1.0f / sqrtf(s / 128.0f + p.eps);
+            float wv[8];
+            unpack8<BF16>(wr_[r], wv);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float u = x[e] * inv;
+                u = u * wv[e];
+                x[e] = round_half<BF16>(u);
+            }
+        }
+        // RoPE
+        float y[8];
+        if (p.neox) {
+            float o[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = row_xor<8>(x[e], j);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float t0 = x[e] * c[e], t1 = o[e] * sn[e];
+                y[e] = j < 8 ? t0 - t1 : t0 + t1;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float a = x[2 * i], b = x[2 * i + 1];
+                float t0 = a * c[i], t1 = b * sn[i];
+                y[2 * i] = t0 - t1;
+                t0 = b * c[i];
+                t1 = a * sn[i];
+                y[2 * i + 1] = t0 + t1;
+            }
+        }
+        const u32x4 yw = pack8<BF16>(y);
+        if (live) *reinterpret_cast<u32x4*>(rows + r * 128 + 8 * j) = yw;
+
+        // ---- append (K rows)
+        if constexpr (ST != ST_NONE) {
+            if (is_k) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) y[e] = round_half<BF16>(y[e]);
+                const bool wr = slot >= 0;
+                float vv[8];
+                if constexpr (ST == ST_TQ || ST == ST_G32) {
+                    unpack8<BF16>(vr[r], vv);
+                    const int64_t blk = slot / p.bs, off = slot % p.bs;
+                    uint8_t* sp = p.kc + blk * p.bs * p.Hkv * p.SA + off * p.Hkv * p.SA + (int64_t)h * p.SA;
+                    if constexpr (ST == ST_TQ) {
+                        tq_store_vec<128, KB, VB, BF16>(y, vv, j, sp, wr, sq[gi], p.tab, p.mse_bytes,
+                                                        p.key_packed, p.val_data);
+                    } else {
+                        constexpr int P = KB == 4 ? 80 : 56;
+                        const uint32_t sbits = (p.sg.w[j >> 2] >> (8 * (j & 3))) & 0xffu;
+                        g32_rotate(y, j, sbits, p.tab.rot_c);
+                        g32_quantize<KB>(y, j, sp, wr);
+                        g32_rotate(vv, j, sbits, p.tab.rot_c);
+                        g32_quantize<KB>(vv, j, sp + P, wr);
                     }
-                    if (wr) {
-                        *reinterpret_cast<u32x4*>(p.kc + eo + 16 * j) = DB == BF16 ? yw : pack8<DB>(y);
-                        *reinterpret_cast<u32x4*>(p.vc + eo + 16 * j) = vw;
-                    }
                 } else {
-                    load8<BF16>(vrow + 8 * j, vv);
-                    gguf_block4<ST>(y, j, p.kc + eo, wr);
-                    gguf_block4<ST>(vv, j, p.vc + eo, wr);
+                    const int64_t eo = kv_entry_offset(wr ? slot : 0, h, p.bs, p.Hkv, p.E, p.stride, p.hnd != 0);
+                    if constexpr (ST == ST_F16 || ST == ST_BF16) {
+                        constexpr bool DB = ST == ST_BF16;
+                        u32x4 vw = vr[r], kw = yw;
+                        if constexpr (DB != BF16) {
+                            unpack8<BF16>(vr[r], vv);
+                            vw = pack8<DB>(vv);
+                            kw = pack8<DB>(y);
+                        }
+                        if (wr) {
+                            *reinterpret_cast<u32x4*>(p.kc + eo + 16 * j) = kw;
+                            *reinterpret_cast<u32x4*>(p.vc + eo + 16 * j) = vw;
+                        }
+                    } else {
+                        unpack8<BF16>(vr[r], vv);
+                        gguf_block4<ST>(y, j, p.kc + eo, wr);
+                        gguf_block4<ST>(vv, j, p.vc + eo, wr);
+                    }
                 }
             }
         }
     }
 }
 
-template <bool BF16, int ST, int KB = 0, int VB = 0>
-int launch_fused(const FusedParams& prm, hipStream_t s) {
-    const int64_t ng = (int64_t)prm.T * (prm.Hq + prm.Hkv);
+template <bool BF16, int ST, int KB, int VB, int R>
+int launch_r(const FusedParams& prm, hipStream_t s) {
+    const int64_t ng = (int64_t)prm.T * (prm.Hq / R + prm.Hkv / R);
     const int64_t grid = (ng + 15) / 16;
     if (grid > 0x7fffffff) return VMC_EINVAL;
     if (grid == 0) return VMC_OK;
-    hipLaunchKernelGGL((fused_norm_rope_kernel<BF16, ST, KB, VB>), dim3((unsigned)grid), dim3(256), 0, s, prm);
+    hipLaunchKernelGGL((fused_norm_rope_kernel<BF16, ST, KB, VB, R>), dim3((unsigned)grid), dim3(256), 0, s,
+                       prm);
     VMC_LAUNCH_CHECK();
     return VMC_OK;
+}
+
+// rows per group: 4 when both head counts allow it (four 16-byte loads in
+// flight per lane), else 2, else 1
+template <bool BF16, int ST, int KB = 0, int VB = 0>
+int launch_fused(const FusedParams& prm, hipStream_t s) {
+    if (prm.Hq % 4 == 0 && prm.Hkv % 4 == 0) return launch_r<BF16, ST, KB, VB, 4>(prm, s);
+    if (prm.Hq % 2 == 0 && prm.Hkv % 2 == 0) return launch_r<BF16, ST, KB, VB, 2>(prm, s);
+    return launch_r<BF16, ST, KB, VB, 1>(prm, s);
 }
 
 template <bool BF16>

@@ -1,8 +1,10 @@
 // selftest.hip -- device check of the lane-level assumptions the kernels rely
 // on: cross-row reductions, the wave-private LDS gathers, the operand /
 // result layouts of the MFMA shapes used (16x16x32 f16/bf16, 16x16x16 f16,
-// 32x32x16 f16/bf16), and exact fp16 subnormal operands in the 16x16x16 MFMA.  One wave, fixed small integer inputs (exact in every
-// format), every lane compares its own results with the expected values.
+// 32x32x16 f16/bf16), exact fp16 subnormal operands in the 16x16x16 MFMA,
+// the bf16 conversion instruction and the 16-lane DPP exchanges.  One wave,
+// fixed inputs (small integers where arithmetic is checked), every lane
+// compares its own results with the expected values.
 #include "vmc_common.hpp"
 
 namespace vmc {
@@ -11,8 +13,16 @@ namespace {
 enum {
     kSumGroups = 1, kMaxGroups = 2, kGather = 4, kMfma16x32 = 8, kMfma16x16 = 16,
     kMfma32x16 = 32, kMfma16x32bf = 64, kMfma32x16bf = 128, kMfma16x16Subnormal = 256,
-    kGatherDiag = 512, kMfma16x32Subnormal = 1024
+    kGatherDiag = 512, kMfma16x32Subnormal = 1024, kBf16Convert = 2048, kRowXor = 4096,
+    kRowSum = 8192
 };
+
+// bf16 rounding cases: ties to even (both ways), a carry into the exponent,
+// overflow to infinity, subnormals, signed zeros, NaN payloads, infinities
+__constant__ uint32_t kBf16Cases[16] = {
+    0x3f808000u, 0x3f818000u, 0x3f80ffffu, 0x7f7fffffu, 0x7f7f7fffu, 0x00018000u,
+    0x80028000u, 0x007fffffu, 0x80000000u, 0x00000000u, 0x7fa00001u, 0xffc12345u,
+    0x7f800001u, 0xff800000u, 0xc0490fdbu, 0x3eaaaaabu};
 
 // A[i][k] = (i + 2k) % 5 - 2, B[k][j] = (3k + j) % 7 - 3 (all exact)
 __device__ __forceinline__ float Aval(int i, int k) { return (float)((i + 2 * k) % 5 - 2); }
@@ -37,6 +47,23 @@ __global__ void __launch_bounds__(64) selftest_kernel(int* fail) {
             const int row = 4 * grp + i;
             if (gd[i] != (float)(200 + 16 * (row >> 2) + row)) bad |= kGatherDiag;
         }
+    }
+    // bf16 conversion instruction against the integer rule; 16-lane DPP
+    // exchanges and the row sum against their definitions
+    {
+        const uint32_t c = kBf16Cases[r16];
+        for (int v = 0; v < 2; ++v) {
+            const float f = __builtin_bit_cast(float, v ? c ^ (uint32_t)(grp * 0x00011001u) : c);
+            if (f32_to_bf16_bits(f) != f32_to_bf16_bits_int(f)) bad |= kBf16Convert;
+        }
+        const float x = (float)(1000 + l);
+        if (row_xor<1>(x, l) != (float)(1000 + (l ^ 1)) || row_xor<2>(x, l) != (float)(1000 + (l ^ 2)) ||
+            row_xor<4>(x, l) != (float)(1000 + (l ^ 4)) || row_xor<8>(x, l) != (float)(1000 + (l ^ 8)) ||
+            row_xor<4>(l, l) != (l ^ 4))
+            bad |= kRowXor;
+        float ref = 0.0f;
+        for (int i = 0; i < 16; ++i) ref += (float)(3 * (16 * grp + i) + 1);
+        if (row_sum16((float)(3 * l + 1)) != ref) bad |= kRowSum;
     }
     // 16x16x32 f16: A lane (row l%16, k = 8*(l/16) + e), D rows 4*(l/16)+i, col l%16
     {
@@ -145,6 +172,6 @@ extern "C" int vmc_selftest(void) {
             hipMemcpy(&h, d, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
             rc = VMC_EIO;
     }
-    hipFree(d);
+    (void)hipFree(d);
     return rc == VMC_OK ? h : rc;
 }

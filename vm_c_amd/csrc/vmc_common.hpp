@@ -43,11 +43,18 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t b) {
     return (float)__builtin_bit_cast(_Float16, b);
 }
-__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+// round to nearest even; a NaN keeps its sign and upper payload with the
+// quiet bit set ((x >> 16) | 0x40).  v_cvt_pk_bf16_f32 does both in one
+// instruction; f32_to_bf16_bits_int is the same rule in integer arithmetic
+// (the device self-test compares the two).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits_int(float f) {
     uint32_t x = __builtin_bit_cast(uint32_t, f);
     if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u);
     x += 0x7fffu + ((x >> 16) & 1u);
     return (uint16_t)(x >> 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 __device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
     return __builtin_bit_cast(float, (uint32_t)b << 16);
@@ -113,6 +120,46 @@ __device__ __forceinline__ float max_over_groups(float v) {
     b = a;
     swap_pair32(a, b);
     return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+
+// 16-lane row exchanges by DPP (one VALU op, no LDS).  row_xor<M>: the value
+// of lane l ^ M of the same 16-lane row (M = 1, 2: quad_perm; 8: row_ror:8;
+// 4: row_shl:4 / row_shr:4 selected by lane bit 2).
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+}
+template <int M>
+__device__ __forceinline__ uint32_t row_xor_u32(uint32_t v, int lane) {
+    static_assert(M == 1 || M == 2 || M == 4 || M == 8, "xor distance within a 16-lane row");
+    if constexpr (M == 1) return dpp_u32<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    else if constexpr (M == 2) return dpp_u32<0x4E>(v);  // quad_perm [2, 3, 0, 1]
+    else if constexpr (M == 8) return dpp_u32<0x128>(v);  // row_ror:8
+    else {
+        const uint32_t up = dpp_u32<0x104>(v);    // row_shl:4: lane l + 4
+        const uint32_t down = dpp_u32<0x114>(v);  // row_shr:4: lane l - 4
+        return (lane & 4) ? down : up;
+    }
+}
+template <int M>
+__device__ __forceinline__ float row_xor(float v, int lane) {
+    return __builtin_bit_cast(float, row_xor_u32<M>(__builtin_bit_cast(uint32_t, v), lane));
+}
+template <int M>
+__device__ __forceinline__ int row_xor(int v, int lane) {
+    return (int)row_xor_u32<M>((uint32_t)v, lane);
+}
+// Sum over a 16-lane row, every lane gets the same value: the butterfly
+// s += s[l ^ 1], s += s[l ^ 2], s += s[l ^ 4], s += s[l ^ 8].  The last two
+// steps read the mirrored lane (7 - l within 8, 15 - l within 16): after the
+// steps before, it holds the same value as lane l ^ 4 (l ^ 8), so the sums
+// are the butterfly's, bit for bit.
+__device__ __forceinline__ float row_sum16(float s) {
+    s = s + __builtin_bit_cast(float, dpp_u32<0xB1>(__builtin_bit_cast(uint32_t, s)));
+    s = s + __builtin_bit_cast(float, dpp_u32<0x4E>(__builtin_bit_cast(uint32_t, s)));
+    s = s + __builtin_bit_cast(float, dpp_u32<0x141>(__builtin_bit_cast(uint32_t, s)));  // row_half_mirror
+    s = s + __builtin_bit_cast(float, dpp_u32<0x140>(__builtin_bit_cast(uint32_t, s)));  // row_mirror
+    return s;
 }
 
 // Wave-private LDS exchange: lanes of row 0 publish v[l % 16]; every lane

@@ -24,6 +24,20 @@ __device__ __forceinline__ void load8(const uint16_t* src, float* x) {
     }
 }
 
+// Walsh-Hadamard butterflies of half-width 8 .. 64 across the group's lanes
+// (partner j ^ m for m = 1, 2, 4, 8): the lane with bit m clear keeps a + b,
+// its partner a - b, as in the sequential order
+__device__ __forceinline__ void wht_lanes(float* y, int j) {
+    static_for<4>([&](auto mi) {
+        constexpr int M = 1 << decltype(mi)::value;
+#pragma unroll
+        for (int e = 0; e < kDims; ++e) {
+            const float o = row_xor<M>(y[e], j);
+            y[e] = (j & M) ? o - y[e] : y[e] + o;
+        }
+    });
+}
+
 // codes of this lane's 8 dims -> its bytes of the packed slot (dst 2-byte
 // aligned).  4-bit: even d in the low nibble (:291), lane j's 4 bytes at 4j.
 // 3-bit: 8 codes -> 3 bytes little endian, code i at bits 3i (:294-309);
@@ -41,7 +55,7 @@ __device__ __forceinline__ void store_codes8(const int* q, uint8_t* dst, int j) 
         uint32_t w = 0;
 #pragma unroll
         for (int i = 0; i < 8; ++i) w |= (uint32_t)(q[i] & 7) << (3 * i);
-        const uint32_t hi = (uint32_t)__shfl_xor((int)w, 1, kGroup);
+        const uint32_t hi = row_xor_u32<1>(w, j);
         if ((j & 1) == 0) {
             const uint64_t w48 = (uint64_t)w | ((uint64_t)hi << 24);
             d16[3 * (j >> 1) + 0] = (uint16_t)(w48 & 0xffff);
@@ -94,14 +108,7 @@ __device__ __forceinline__ void tq_store_vec(float* y, float* vv, int j, uint8_t
                 y[k] = a + b;
                 y[k + hw] = a - b;
             }
-#pragma unroll
-    for (int m = 1; m < kGroup; m <<= 1) {
-#pragma unroll
-        for (int e = 0; e < kDims; ++e) {
-            const float o = __shfl_xor(y[e], m, kGroup);
-            y[e] = (j & m) ? o - y[e] : y[e] + o;
-        }
-    }
+    wht_lanes(y, j);
     constexpr int NC = 1 << KB;
 #pragma unroll
     for (int e = 0; e < kDims; ++e) {
@@ -127,11 +134,11 @@ __device__ __forceinline__ void tq_store_vec(float* y, float* vv, int j, uint8_t
         vmin = fminf(vmin, y[e]);
         vmax = fmaxf(vmax, y[e]);
     }
-#pragma unroll
-    for (int m = 1; m < kGroup; m <<= 1) {
-        vmin = fminf(vmin, __shfl_xor(vmin, m, kGroup));
-        vmax = fmaxf(vmax, __shfl_xor(vmax, m, kGroup));
-    }
+    static_for<4>([&](auto m) {
+        constexpr int M = 1 << decltype(m)::value;
+        vmin = fminf(vmin, row_xor<M>(vmin, j));
+        vmax = fmaxf(vmax, row_xor<M>(vmax, j));
+    });
     constexpr int VMAXQ = VB == 4 ? 15 : 7;
     float vscale = (vmax - vmin) / (float)VMAXQ;
     vscale = fmaxf(vscale, 1e-8f);
@@ -167,14 +174,7 @@ __device__ __forceinline__ void g32_rotate(float* y, int j, uint32_t sbits, floa
                 y[k] = a + b;
                 y[k + hw] = a - b;
             }
-#pragma unroll
-    for (int m = 1; m < kGroup; m <<= 1) {
-#pragma unroll
-        for (int e = 0; e < kDims; ++e) {
-            const float o = __shfl_xor(y[e], m, kGroup);
-            y[e] = (j & m) ? o - y[e] : y[e] + o;
-        }
-    }
+    wht_lanes(y, j);
 #pragma unroll
     for (int e = 0; e < kDims; ++e) y[e] = __fmul_rn(y[e], rot_c);
 }
@@ -191,11 +191,10 @@ __device__ __forceinline__ void g32_quantize(const float* y, int j, uint8_t* dst
             mn = fminf(mn, y[e]);
             mx = fmaxf(mx, y[e]);
         }
-#pragma unroll
-        for (int m = 1; m < 4; m <<= 1) {
-            mn = fminf(mn, __shfl_xor(mn, m, kGroup));
-            mx = fmaxf(mx, __shfl_xor(mx, m, kGroup));
-        }
+        mn = fminf(mn, row_xor<1>(mn, j));
+        mx = fmaxf(mx, row_xor<1>(mx, j));
+        mn = fminf(mn, row_xor<2>(mn, j));
+        mx = fmaxf(mx, row_xor<2>(mx, j));
         const float d = (mx - mn) / 15.0f;
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
 #pragma unroll
@@ -213,8 +212,8 @@ __device__ __forceinline__ void g32_quantize(const float* y, int j, uint8_t* dst
             lo |= (uint32_t)q[e] << (8 * e);
             hi |= (uint32_t)q[e + 4] << (8 * e);
         }
-        const uint32_t plo = (uint32_t)__shfl_xor((int)lo, 2, kGroup);
-        const uint32_t phi = (uint32_t)__shfl_xor((int)hi, 2, kGroup);
+        const uint32_t plo = row_xor_u32<2>(lo, j);
+        const uint32_t phi = row_xor_u32<2>(hi, j);
         if (write) {
             uint8_t* blk = dst + 20 * (j >> 2);
             if (l == 0)
@@ -239,17 +238,17 @@ __device__ __forceinline__ void g32_quantize(const float* y, int j, uint8_t* dst
                 idx = 8 * l + e;
             }
         }
-#pragma unroll
-        for (int m = 1; m < 4; m <<= 1) {
-            const float a2 = __shfl_xor(amax, m, kGroup);
-            const float v2 = __shfl_xor(v, m, kGroup);
-            const int i2 = __shfl_xor(idx, m, kGroup);
+        static_for<2>([&](auto m) {
+            constexpr int M = 1 << decltype(m)::value;
+            const float a2 = row_xor<M>(amax, j);
+            const float v2 = row_xor<M>(v, j);
+            const int i2 = row_xor<M>(idx, j);
             if (a2 > amax || (a2 == amax && i2 < idx)) {
                 amax = a2;
                 v = v2;
                 idx = i2;
             }
-        }
+        });
         const float d = v / -4.0f;
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
         uint32_t w = 0;
@@ -261,7 +260,7 @@ __device__ __forceinline__ void g32_quantize(const float* y, int j, uint8_t* dst
             w |= (uint32_t)(c > 7 ? 7 : c) << (3 * e);
         }
         // lanes 2i, 2i+1 of the group: 6 bytes at 2 + 6i, written by the even lane
-        const uint32_t hiw = (uint32_t)__shfl_xor((int)w, 1, kGroup);
+        const uint32_t hiw = row_xor_u32<1>(w, j);
         if (write) {
             uint8_t* blk = dst + 14 * (j >> 2);
             uint16_t* d16 = reinterpret_cast<uint16_t*>(blk);

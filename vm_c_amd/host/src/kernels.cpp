@@ -1,5 +1,6 @@
 // kernels.cpp -- vm_c's kernel entry points (kernels_turboquant.h,
-// kernels_cache.h, kernels_attention.h, kernels_flash_attn.h) over the C ABI
+// kernels_cache.h, kernels_attention.h, kernels_flash_attn.h,
+// kernels_fused_attn.h) over the C ABI
 // of vmc_attn.h.  Argument checks that need no device live in the C ABI;
 // this layer maps vm_c's string/enum conventions and turns failures into
 // std::runtime_error.
@@ -10,6 +11,7 @@
 #include <vector>
 
 #include "vm_c/kernels_attention.hpp"
+#include "vm_c/kernels_fused_attn.hpp"
 #include "vm_c/kernels_turboquant.hpp"
 
 namespace vm_c {
@@ -303,6 +305,56 @@ void flash_attention_prefill_local_with_cache(
                                          vmc_dtype_of(dtype), key_cache, value_cache, slot_mapping,
                                          block_size, vmc_kv_format_of(kv_cache_dtype, dtype),
                                          vmc_layout_of(layout), stream));
+}
+
+// ------------------------------------------------------------ fused norm + RoPE
+
+void fused_qk_norm_rope_store(void* q_buf, void* k_buf, const void* v_buf,
+                              const void* q_norm_weight, const void* k_norm_weight,
+                              const void* cos_sin_cache, const int64_t* position_ids,
+                              void* key_cache, void* value_cache, const int64_t* slot_mapping,
+                              int num_tokens, int num_heads, int num_kv_heads, int head_dim,
+                              float rms_norm_eps, bool is_neox, int64_t block_size,
+                              int64_t cache_stride, const std::string& kv_cache_dtype,
+                              hipStream_t stream, ScalarType dtype, const std::string& layout) {
+    // fused_attn_kernels.cu:243: the append needs both the cache and the slots
+    const bool store = key_cache != nullptr && slot_mapping != nullptr;
+    VMC_CALL(vmc_fused_qk_norm_rope_store(
+        q_buf, k_buf, v_buf, q_norm_weight, k_norm_weight, cos_sin_cache, position_ids,
+        store ? key_cache : nullptr, store ? value_cache : nullptr, store ? slot_mapping : nullptr,
+        num_tokens, num_heads, num_kv_heads, head_dim, rms_norm_eps, is_neox ? 1 : 0, block_size,
+        cache_stride, vmc_kv_format_of(kv_cache_dtype, dtype), vmc_layout_of(layout), nullptr,
+        vmc_dtype_of(dtype), stream));
+}
+
+void fused_qk_norm_rope_store(void* q_buf, void* k_buf, const void* v_buf,
+                              const void* q_norm_weight, const void* k_norm_weight,
+                              const void* cos_sin_cache, const int64_t* position_ids,
+                              void* kv_cache, const int64_t* slot_mapping, int num_tokens,
+                              int num_heads, int num_kv_heads, int head_dim, float rms_norm_eps,
+                              bool is_neox, int64_t block_size, const TQConfig& config,
+                              hipStream_t stream, ScalarType dtype) {
+    if (config.key_fp8) throw std::runtime_error("turboquant_k8v4 (fp8 keys) is not implemented");
+    if (!kv_cache || !slot_mapping)
+        throw std::runtime_error("fused_qk_norm_rope_store: TurboQuant append needs a cache and slots");
+    const vmc_tq_config c = config.to_c();
+    VMC_CALL(vmc_fused_qk_norm_rope_store(
+        q_buf, k_buf, v_buf, q_norm_weight, k_norm_weight, cos_sin_cache, position_ids, kv_cache,
+        nullptr, slot_mapping, num_tokens, num_heads, num_kv_heads, head_dim, rms_norm_eps,
+        is_neox ? 1 : 0, block_size, 0, VMC_KV_F16, VMC_LAYOUT_NHD, &c, vmc_dtype_of(dtype),
+        stream));
+}
+
+void fused_qk_norm_rope(void* q_buf, void* k_buf, const void* q_norm_weight,
+                        const void* k_norm_weight, const void* cos_sin_cache,
+                        const int64_t* position_ids, int num_tokens, int num_heads,
+                        int num_kv_heads, int head_dim, float rms_norm_eps, bool is_neox,
+                        hipStream_t stream, ScalarType dtype) {
+    VMC_CALL(vmc_fused_qk_norm_rope_store(q_buf, k_buf, nullptr, q_norm_weight, k_norm_weight,
+                                          cos_sin_cache, position_ids, nullptr, nullptr, nullptr,
+                                          num_tokens, num_heads, num_kv_heads, head_dim,
+                                          rms_norm_eps, is_neox ? 1 : 0, 0, 0, VMC_KV_F16,
+                                          VMC_LAYOUT_NHD, nullptr, vmc_dtype_of(dtype), stream));
 }
 
 }  // namespace vm_c
