@@ -155,7 +155,7 @@ extern "C" int vmc_tq_config_from_method(int head_dim, const char* method, vmc_t
         c.slot_size = c.slot_size_aligned = 2 * part;
         c.group_size = 32;
         c.sign_seed = 0;
-        *out = c;
+        std::memcpy(out, &c, sizeof(c));  // padding bytes included (zeroed)
         return VMC_OK;
     } else {
         return VMC_EINVAL;
@@ -167,7 +167,7 @@ extern "C" int vmc_tq_config_from_method(int head_dim, const char* method, vmc_t
     c.value_packed_size = c.val_data_bytes + 4;
     c.slot_size = c.key_packed_size + c.value_packed_size;
     c.slot_size_aligned = c.slot_size + (c.slot_size % 2);
-    *out = c;
+    std::memcpy(out, &c, sizeof(c));
     return VMC_OK;
 }
 

@@ -69,6 +69,7 @@ TQConfig TQConfig::from_method(int head_dim_, const char* method, int gpu_device
 
 vmc_tq_config TQConfig::to_c() const {
     vmc_tq_config c;
+    std::memset(&c, 0, sizeof(c));  // the padding before sign_seed too (callers compare bytes)
     c.head_dim = head_dim;
     c.key_quant_bits = key_quant_bits;
     c.value_quant_bits = value_quant_bits;
