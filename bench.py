@@ -14,6 +14,9 @@ Also measured in the same run (extra fields of the same line):
   * variant_g32: the same decode step with the configuration text's KV
     format, turboquant_3bit_g32 (random-sign Walsh-Hadamard, 3-bit codes and
     a 16-bit scale per 32 values, 112-byte slots);
+  * decode_other_configs: the attention operator on batch 32 x 8192 with
+    4-bit TurboQuant, and on batch 16 (lengths in [512, 4096]) with q8_0
+    K/V pages -> GB/s;
   * causal prefill: batch 4 x 4096 tokens, 32/8 heads, bf16, fused q8_0
     quantize-on-append into the paged cache -> TFLOP/s;
   * fused_norm_rope: Q/K RMSNorm + RoPE + q8_0 append of the same prefill
@@ -150,6 +153,101 @@ def bench_decode(args, torch, capi, dev, method="turboquant_3bit_nc", sign_seed=
     log(f"decode step {ms_step * 1e3:.1f} us, attention {ms_attn * 1e3:.1f} us, "
         f"{attn_bytes / ms_attn / 1e6:.0f} GB/s attention-only")
     return res
+
+
+def bench_decode_cfg(args, torch, capi, dev, kind):
+    """The other two decode configurations, attention operator only:
+    "tq4_32x8192": batch 32 x 8192 tokens, 32/8 heads, turboquant_4bit_nc
+    (134 B slots), seed 2; "q8_0_batch16": batch 16, lengths uniform in
+    [512, 4096] (seed 1), 32/8 heads, q8_0 K and V pages (136 B per
+    token-head each).  Pools replicated to >= 2 GiB and rotated."""
+    if kind == "tq4_32x8192":
+        seed, B, Hq, Hkv = 2, 32, 32, 8
+        lens = np.full(B, 8192, np.int32)
+    else:
+        seed, B, Hq, Hkv = 1, 16, 32, 8
+        lens = np.random.default_rng(seed).integers(512, 4097, B).astype(np.int32)
+    rng = np.random.default_rng(seed)
+    pages = (lens + BS - 1) // BS
+    nblk = int(pages.sum())
+    perm = rng.permutation(nblk).astype(np.int32)
+    bt = np.full((B, int(pages.max())), -1, np.int32)
+    k = 0
+    for b in range(B):
+        bt[b, :pages[b]] = perm[k:k + pages[b]]
+        k += pages[b]
+    b_all = np.repeat(np.arange(B), lens)
+    p_all = np.concatenate([np.arange(n) for n in lens])
+    slots = torch.from_numpy(slots_for(bt, lens, (b_all, p_all))).to(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    tq = kind == "tq4_32x8192"
+    if tq:
+        cfg = capi.tq_config(D, "turboquant_4bit_nc")
+        entry = cfg.slot_size_aligned
+        pool_bytes = nblk * BS * Hkv * entry
+    else:
+        entry = capi.kv_entry_bytes(capi.KV_Q8_0, D)
+        pool_bytes = 2 * nblk * BS * Hkv * entry
+    npool = max(2, math.ceil(2 * 1024 ** 3 / pool_bytes))
+    pools = [torch.empty(pool_bytes, dtype=torch.uint8, device=dev) for _ in range(npool)]
+    T = int(lens.sum())
+    for s0 in range(0, T, 65536):
+        n = min(65536, T - s0)
+        kk = torch.randn((n, Hkv, D), generator=gen, device=dev).half()
+        vv = torch.randn((n, Hkv, D), generator=gen, device=dev).half()
+        if tq:
+            capi.turboquant_store(kk, vv, pools[0], slots[s0:s0 + n], BS, cfg)
+        else:
+            half = pool_bytes // 2
+            capi.reshape_and_cache(kk, vv, pools[0][:half], pools[0][half:], slots[s0:s0 + n], BS,
+                                   kv_format=capi.KV_Q8_0)
+    for i in range(1, npool):
+        pools[i].copy_(pools[0])
+    q = torch.randn((B, Hq, D), generator=gen, device=dev).half()
+    out = torch.empty_like(q)
+    bt_d, lens_d = torch.from_numpy(bt).to(dev), torch.from_numpy(lens).to(dev)
+    scale = 1.0 / math.sqrt(D)
+    stream = torch.cuda.current_stream()
+    if tq:
+        ws = torch.empty(capi.turboquant_decode_workspace_size(B, Hq, Hkv, D, bt.shape[1], BS),
+                         dtype=torch.uint8, device=dev)
+    else:
+        ws = torch.empty(max(1, capi.paged_decode_workspace_size(B, Hq, Hkv, D, bt.shape[1], BS)),
+                         dtype=torch.uint8, device=dev)
+
+    def run(i):
+        pool = pools[i % npool]
+        if tq:
+            capi.turboquant_decode_attention(out, q, pool, bt_d, lens_d, Hkv, scale, cfg, BS,
+                                             workspace=ws, stream=stream)
+        else:
+            half = pool_bytes // 2
+            capi.paged_attention_decode(out, q, pool[:half], pool[half:], bt_d, lens_d, Hkv, scale,
+                                        block_size=BS, kv_format=capi.KV_Q8_0, workspace=ws,
+                                        stream=stream)
+
+    for i in range(args.warmup):
+        run(i)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(args.steps):
+        run(args.warmup + i)
+    e1.record(stream)
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    assert torch.isfinite(out.float()).all().item(), f"{kind} decode produced non-finite values"
+    kv = T * Hkv * entry * (1 if tq else 2)
+    nbytes = kv + 2 * B * Hq * D * 2 + nblk * 4 + B * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"decode {kind}: {ms * 1e3:.1f} us, {gbs:.0f} GB/s")
+    del pools
+    torch.cuda.empty_cache()
+    return {"workload": kind, "batch": B, "num_heads": Hq, "num_kv_heads": Hkv,
+            "sum_ctx": T, "ms": round(ms, 4), "gbs": round(gbs, 1),
+            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes}
 
 
 # ------------------------------------------------------------------ prefill
@@ -347,6 +445,8 @@ def main():
                "tokens_per_s": round(v["w"]["B"] / (v["ms_step"] * 1e-3), 1)}
         del v
         torch.cuda.empty_cache()
+    others = [] if args.skip_variant else [bench_decode_cfg(args, torch, capi, dev, k)
+                                           for k in ("tq4_32x8192", "q8_0_batch16")]
     pre = None if args.skip_prefill else bench_prefill(args, torch, capi, dev)
     fused = None if args.skip_prefill else bench_fused_norm_rope(args, torch, capi, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline(dec, torch)
@@ -385,6 +485,8 @@ def main():
     }
     if var is not None:
         line["variant_g32"] = var
+    if others:
+        line["decode_other_configs"] = others
     if pre is not None:
         line["prefill"] = {"workload": "causal prefill B=4 S=4096 Hq=32 Hkv=8 bf16, fused q8_0 append",
                            "ms": round(pre["ms"], 4), "tflops": round(pre["tflops"], 1),

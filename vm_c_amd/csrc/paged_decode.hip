@@ -49,7 +49,6 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kBs = 16;
-constexpr int kChunkPages = 256;  // pages whose block-table entries are staged in LDS at once
 constexpr float kNegInf = -__builtin_inff();
 
 // FMT_G4 / FMT_G3: the per-32-group variant (no reference counterpart): one
@@ -78,8 +77,6 @@ struct Geo {
     static constexpr bool staged = FMT >= FMT_Q8_0;
     static constexpr int spp = staged ? (per_thread + 63) / 64 : 1;
     static constexpr bool dma = FMT == FMT_TQ;
-    static constexpr int pf = !staged ? 1 : dma ? 2 : (spp <= 2 ? 4 : (spp <= 3 ? 3 : 2));
-    static constexpr int nbuf = dma ? pf + 2 : pf;
     static constexpr int kHalf = kBs * 8 * entry;  // one cache's page, 8 heads
     // TurboQuant: a head group (<= 4 heads) of 16 tokens, each token's run
     // fetched as a window of whole 16-byte chunks (at most nc_max of them)
@@ -89,6 +86,15 @@ struct Geo {
     // chunks per lane per page for any group size (1..4 heads, one wave each)
     static constexpr int spt = std::max(std::max(spt_of(1), spt_of(2)), std::max(spt_of(3), spt_of(4)));
     static constexpr int kBuf = dma ? kBs * nc_max * 16 : combined ? kHalf : 2 * kHalf;  // one LDS buffer
+    // pages whose block-table entries are staged in LDS at once, and waves per
+    // workgroup (TurboQuant: one head group of at most 4 KV heads)
+    static constexpr int chunk = 256;
+    static constexpr int waves = dma ? 4 : 8;
+    // TurboQuant: two pages in flight behind the pair being read (four
+    // measured no faster: the kernel is bound by its K/V decode, not by the
+    // bytes in flight)
+    static constexpr int pf = !staged ? 1 : dma ? 2 : (spp <= 2 ? 4 : (spp <= 3 ? 3 : 2));
+    static constexpr int nbuf = dma ? pf + 2 : pf;
 };
 
 // TurboQuant V codes enter the PV MFMA as fp16 subnormals: the code field of
@@ -306,10 +312,10 @@ struct alignas(16) DecodeLds {
     uint8_t ring[GE::staged ? GE::nbuf * GE::kBuf : 16];
     u32x2 lut4[FMT == FMT_TQ && KB == 3 ? 4096 : 1];  // 3-bit keys: four fp16 centroids per 12 bits
     uint32_t lut[FMT == FMT_TQ ? 256 : 1];              // key code pair -> two fp16 centroids
-    float wscr[8][80];                                  // per-wave exchange
-    int32_t bt[kChunkPages];                            // block of each page of the chunk
-    int32_t info[kChunkPages];                          // b << 6 | valid tokens << 1 | piece ends
-    int32_t seg_b[kChunkPages], seg_ps[kChunkPages], seg_L[kChunkPages];
+    float wscr[GE::waves][80];                          // per-wave exchange
+    int32_t bt[GE::chunk];                              // block of each page of the chunk
+    int32_t info[GE::chunk];                            // b << 6 | valid tokens << 1 | piece ends
+    int32_t seg_b[GE::chunk], seg_ps[GE::chunk], seg_L[GE::chunk];
     WGPlan plan;
     int n_seg;
 };
@@ -1176,10 +1182,10 @@ paged_decode_kernel(DecodeParams p) {
         if (info & 1) finalize(b);  // last page of this sequence's piece
     };
 
-    // ---- chunks of up to kChunkPages pages: stage the block-table slice and
+    // ---- chunks of up to GE::chunk pages: stage the block-table slice and
     // the per-page sequence info in LDS, then stream the pages
-    for (int c_lo = p_lo; c_lo < p_hi; c_lo += kChunkPages) {
-        const int c_hi = min(p_hi, c_lo + kChunkPages);
+    for (int c_lo = p_lo; c_lo < p_hi; c_lo += GE::chunk) {
+        const int c_hi = min(p_hi, c_lo + GE::chunk);
         npc = c_hi - c_lo;
         if (wave == 0) {
             const int ns = collect_segments(p, c_lo, c_hi, lane, seg_b, seg_ps, seg_L, &plan,
