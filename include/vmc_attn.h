@@ -119,8 +119,10 @@ typedef struct vmc_tq_config {
 } vmc_tq_config;
 
 /* TQConfig::from_method: "turboquant_4bit_nc" (default), "turboquant_3bit_nc",
- * "turboquant_k3v4_nc".  Returns VMC_EINVAL for an unknown method or for
- * "turboquant_k8v4" (fp8 keys, not implemented).
+ * "turboquant_k3v4_nc", "turboquant_k8v4" (fp8 keys: 128 bytes of the
+ * reference's own e4m3 codes -- fp8_e4b15 = 1 selects its e4b15 codes -- then
+ * 4-bit V codes, fp16 scale and zero; 196-byte slots; no rotation, no norm).
+ * Returns VMC_EINVAL for an unknown method.
  * The per-32-group variant (no reference counterpart): "turboquant_4bit_g32"
  * and "turboquant_3bit_g32".  For both K and V, y = H (s * x) / sqrt(128)
  * (s = +-1 signs from sign_seed), then per 32 values of y:

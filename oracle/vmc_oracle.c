@@ -267,7 +267,14 @@ int orc_tq_layout_from_method(int head_dim, const char* method, orc_tq_layout* L
     memset(L, 0, sizeof(*L));
     L->head_dim = head_dim;
     L->norm_correction = 1;
-    if (method && strcmp(method, "turboquant_k3v4_nc") == 0) {
+    if (method && strcmp(method, "turboquant_k8v4") == 0) {
+        /* kernels_turboquant.h:47-55: fp8 keys, 4-bit values, no norm
+         * correction; e4m3 on devices with fp8 support (the flag is the
+         * caller's to change) */
+        L->key_quant_bits = 8; L->value_quant_bits = 4;
+        L->norm_correction = 0;
+        L->key_fp8 = 1;
+    } else if (method && strcmp(method, "turboquant_k3v4_nc") == 0) {
         L->key_quant_bits = 3; L->value_quant_bits = 4;
     } else if (method && strcmp(method, "turboquant_3bit_nc") == 0) {
         L->key_quant_bits = 3; L->value_quant_bits = 3;
@@ -277,9 +284,10 @@ int orc_tq_layout_from_method(int head_dim, const char* method, orc_tq_layout* L
     } else {
         return -1;
     }
+    /* compute_layout, kernels_turboquant.h:29-42 */
     L->n_centroids = 1 << L->key_quant_bits;
-    L->mse_bytes = (head_dim * L->key_quant_bits + 7) / 8;
-    L->key_packed_size = L->mse_bytes + 2;
+    L->mse_bytes = L->key_fp8 ? head_dim : (head_dim * L->key_quant_bits + 7) / 8;
+    L->key_packed_size = L->key_fp8 ? head_dim : L->mse_bytes + 2;
     L->val_data_bytes = (head_dim * L->value_quant_bits + 7) / 8;
     L->value_packed_size = L->val_data_bytes + 4;
     L->slot_size = L->key_packed_size + L->value_packed_size;
@@ -370,6 +378,46 @@ void orc_tq_rotate(const float* x, const float* signs, float* y, int d) {
     for (int i = 0; i < d; ++i) y[i] = y[i] * c;
 }
 
+/* float_to_fp8_e4m3 / _e4b15 (turboquant_kernels.cu:47-83, :98-134): the
+ * same code with exponent bias B = 7 or 15 and the exponent-255 code 0x7C
+ * (e4m3) or 0x78 (e4b15); values below the smallest normal keep exponent
+ * field 1 with a rounded, clamped mantissa; overflow saturates to 0x7F. */
+uint8_t orc_f32_to_fp8(float v, int e4b15) {
+    uint32_t bits;
+    memcpy(&bits, &v, 4);
+    const uint32_t sign = (bits >> 31) & 1;
+    const int32_t exp_f32 = (int32_t)((bits >> 23) & 0xFF);
+    const uint32_t mant_f32 = bits & 0x7FFFFF;
+    const int32_t bias = e4b15 ? 15 : 7;
+    if (exp_f32 == 0 && mant_f32 == 0) return (uint8_t)(sign << 7);
+    if (exp_f32 == 255) return (uint8_t)((sign << 7) | (e4b15 ? 0x78 : 0x7C));
+    int32_t e = exp_f32 - 127 + bias;
+    if (e < 1) {
+        const int32_t shift = 1 - e;
+        if (shift > 24) return (uint8_t)(sign << 7);
+        const uint32_t mant = (0x800000u | mant_f32) >> shift;
+        uint32_t m8 = (mant + 4) >> 4;
+        if (m8 > 7) m8 = 7;
+        return (uint8_t)((sign << 7) | (1 << 3) | m8);
+    }
+    if (e > 15) return (uint8_t)((sign << 7) | 0x7F);
+    uint32_t m8 = (mant_f32 + 0x40000) >> 19;
+    if (m8 > 7) {
+        m8 = 0;
+        e++;
+        if (e > 15) return (uint8_t)((sign << 7) | 0x7F);
+    }
+    return (uint8_t)((sign << 7) | ((e & 0xF) << 3) | (m8 & 0x7));
+}
+
+/* fp8_e4m3_to_float / fp8_e4b15_to_float (:85-96, :136-143) */
+float orc_fp8_to_f32(uint8_t b, int e4b15) {
+    const uint32_t sign = (b >> 7) & 1, e = (b >> 3) & 0xF, m = b & 0x7;
+    if (e == 0 && m == 0) return sign ? -0.0f : 0.0f;
+    const float v = ldexpf(1.0f + (float)m / 8.0f, (int)e - (e4b15 ? 15 : 7));
+    return sign ? -v : v;
+}
+
 static inline void put_half(uint8_t* p, float v, int bf16) {
     const uint16_t b = f32_to_half(v, bf16);
     p[0] = (uint8_t)(b & 0xff);
@@ -434,6 +482,11 @@ void orc_tq_store(const uint16_t* key, const uint16_t* value, uint8_t* kv_cache,
             uint8_t* sp = kv_cache + blk * block_size * num_kv_heads * L->slot_size_aligned +
                           off * num_kv_heads * L->slot_size_aligned +
                           (int64_t)h * L->slot_size_aligned;
+            if (L->key_fp8) {
+                /* half_to_fp8_store_kernel :188-245: K byte d = fp8(k[d]) */
+                for (int d = 0; d < D; ++d)
+                    sp[d] = orc_f32_to_fp8(half_to_f32(key[pid * D + d], bf16), L->fp8_e4b15);
+            } else {
             float norm_sq = 0.0f;
             for (int d = 0; d < D; ++d) {
                 kf[d] = half_to_f32(key[pid * D + d], bf16);
@@ -453,6 +506,7 @@ void orc_tq_store(const uint16_t* key, const uint16_t* value, uint8_t* kv_cache,
             }
             pack_codes(q, D, L->key_quant_bits, sp);
             put_half(sp + L->mse_bytes, norm, bf16);
+            }
 
             float vmin = FLT_MAX, vmax = -FLT_MAX;
             for (int d = 0; d < D; ++d) {
@@ -476,11 +530,23 @@ void orc_tq_store(const uint16_t* key, const uint16_t* value, uint8_t* kv_cache,
     }
 }
 
-/* Dequantisation of tq_decode_stage1_kernel :416-483. */
+/* Dequantisation of tq_decode_stage1_kernel :416-483.  fp8 keys (:407-415)
+ * carry no norm: the reference also multiplies them by the fp16 read at
+ * +mse_bytes (:444-450), which for k8v4 is the first two bytes of the V
+ * codes -- a defect, not restated. */
 void orc_tq_dequant_slot(const uint8_t* sp, const orc_tq_layout* L, const float* C,
                          int bf16, float* k_out, float* v_out) {
     const int D = L->head_dim;
     int q[256];
+    if (L->key_fp8) {
+        for (int d = 0; d < D; ++d) k_out[d] = orc_fp8_to_f32(sp[d], L->fp8_e4b15);
+        const uint8_t* vp = sp + L->key_packed_size;
+        const float vs = get_half(vp + L->val_data_bytes, bf16);
+        const float vz = get_half(vp + L->val_data_bytes + 2, bf16);
+        unpack_codes(vp, D, L->value_quant_bits, q);
+        for (int d = 0; d < D; ++d) v_out[d] = fmaf((float)q[d], vs, vz);
+        return;
+    }
     unpack_codes(sp, D, L->key_quant_bits, q);
     for (int d = 0; d < D; ++d) k_out[d] = C[q[d]];
     if (L->norm_correction) {
@@ -533,7 +599,9 @@ void orc_tq_decode(uint16_t* out, const uint16_t* query, const uint8_t* kv_cache
         float* mid = (float*)malloc(sizeof(float) * (size_t)ns * (size_t)(D + 1));
         int* valid = (int*)malloc(sizeof(int) * (size_t)ns);
         for (int d = 0; d < D; ++d) qf[d] = half_to_f32(query[(int64_t)bh * D + d], bf16);
-        orc_tq_rotate(qf, NULL, qr, D);
+        /* fp8 keys: q is not rotated (the reference copies it, :984) */
+        if (L->key_fp8) memcpy(qr, qf, sizeof(float) * (size_t)D);
+        else orc_tq_rotate(qf, NULL, qr, D);
         const int split_len = (seq_len + ns - 1) / ns;
         for (int sid = 0; sid < ns; ++sid) {
             const int start = split_len * sid;
@@ -640,14 +708,19 @@ void orc_tq_decode_exact(double* out, const uint16_t* query, const uint8_t* kv_c
             if (blk < 0) continue;
             const uint8_t* sp = tq_slot_ptr(kv_cache, blk, pos % bs, kvh, bs, Hkv,
                                             L->slot_size_aligned);
-            /* exact dequant: centroid / ||centroids|| * norm, code*scale + zero */
+            /* exact dequant: centroid / ||centroids|| * norm (fp8 keys: the
+             * decoded byte), code*scale + zero */
             int qc[256];
+            if (L->key_fp8) {
+                for (int d = 0; d < D; ++d) K[(int64_t)cnt * D + d] = orc_fp8_to_f32(sp[d], L->fp8_e4b15);
+            } else {
             unpack_codes(sp, D, L->key_quant_bits, qc);
             double cn = 0.0;
             for (int d = 0; d < D; ++d) cn += (double)C[qc[d]] * (double)C[qc[d]];
             const double ci = L->norm_correction ? 1.0 / sqrt(cn + 1e-16) : 1.0;
             const double nrm = get_half(sp + L->mse_bytes, bf16);
             for (int d = 0; d < D; ++d) K[(int64_t)cnt * D + d] = (double)C[qc[d]] * ci * nrm;
+            }
             const uint8_t* vp = sp + L->key_packed_size;
             const double vs = get_half(vp + L->val_data_bytes, bf16);
             const double vz = get_half(vp + L->val_data_bytes + 2, bf16);
@@ -661,7 +734,7 @@ void orc_tq_decode_exact(double* out, const uint16_t* query, const uint8_t* kv_c
             double acc = 0.0;
             for (int j = 0; j < D; ++j)
                 acc += ((__builtin_popcount((unsigned)(i & j)) & 1) ? -c : c) * qd[j];
-            qr[i] = acc;
+            qr[i] = L->key_fp8 ? qd[i] : acc;
         }
         softmax_av_exact(qr, K, V, cnt, D, scale, out + (int64_t)bh * D);
         free(K);

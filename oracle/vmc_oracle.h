@@ -75,7 +75,15 @@ typedef struct {
     int slot_size;
     int slot_size_aligned;
     int n_centroids;
+    int key_fp8;     /* turboquant_k8v4: K stored as 128 fp8 bytes, no norm */
+    int fp8_e4b15;   /* fp8 flavour of those keys: e4m3 (0) or e4b15 (1)  */
 } orc_tq_layout;
+
+/* the reference's own fp8 converters (turboquant_kernels.cu:47-143): bias 7
+ * (e4m3) or 15 (e4b15), no NaN/inf codes, exponent 0 with a non-zero
+ * mantissa decodes as (1 + m/8) 2^-bias like every other code. */
+uint8_t orc_f32_to_fp8(float v, int e4b15);
+float   orc_fp8_to_f32(uint8_t b, int e4b15);
 
 int  orc_tq_layout_from_method(int head_dim, const char* method, orc_tq_layout* out);
 void orc_tq_hadamard(float* out, int d);

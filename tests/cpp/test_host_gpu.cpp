@@ -105,8 +105,10 @@ static void test_turboquant_backend(const char* method) {
     std::vector<float> C(16), M(15);
     if (!g32) {
         CHECK(orc_tq_layout_from_method(D, method, &L) == 0);
-        orc_tq_lloyd_max(C.data(), D, L.key_quant_bits);
-        orc_tq_midpoints(C.data(), L.n_centroids, M.data());
+        if (!L.key_fp8) {  // fp8 keys (turboquant_k8v4) use no codebook
+            orc_tq_lloyd_max(C.data(), D, L.key_quant_bits);
+            orc_tq_midpoints(C.data(), L.n_centroids, M.data());
+        }
     }
     auto ref_store = [&](const uint16_t* k, const uint16_t* v, uint8_t* dst, const int64_t* slots, int n) {
         if (g32) orc_g32_store(k, v, dst, slots, n, Hkv, D, BS, gbits, 0, 0);
@@ -284,7 +286,7 @@ int main() {
     }
     try {
         for (const char* m : {"turboquant_3bit_nc", "turboquant_4bit_nc", "turboquant_3bit_g32",
-                              "turboquant_4bit_g32"})
+                              "turboquant_4bit_g32", "turboquant_k8v4"})
             test_turboquant_backend(m);
         test_paged_backend("q8_0", "nhd");
         test_paged_backend("q4_0", "hnd");

@@ -26,7 +26,7 @@ class TQLayout(C.Structure):
     _fields_ = [(n, C.c_int) for n in (
         "head_dim", "key_quant_bits", "value_quant_bits", "norm_correction",
         "mse_bytes", "key_packed_size", "val_data_bytes", "value_packed_size",
-        "slot_size", "slot_size_aligned", "n_centroids")]
+        "slot_size", "slot_size_aligned", "n_centroids", "key_fp8", "fp8_e4b15")]
 
 
 _lib = None
@@ -82,6 +82,10 @@ def lib():
         L.orc_g32_decode_exact.argtypes = [_P, _P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int,
                                            C.c_double, C.c_int64, C.c_int64, C.c_int, C.c_uint64,
                                            C.c_int, C.c_int]
+        L.orc_f32_to_fp8.argtypes = [C.c_float, C.c_int]
+        L.orc_f32_to_fp8.restype = C.c_uint8
+        L.orc_fp8_to_f32.argtypes = [C.c_uint8, C.c_int]
+        L.orc_fp8_to_f32.restype = C.c_float
         L.orc_qk_norm_rope.argtypes = [_P, _P, _P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int,
                                         C.c_float, C.c_int, C.c_int]
         L.orc_paged_decode_exact.argtypes = [_P, _P, _P, _P, C.c_int, C.c_int, _P, _P,
@@ -255,6 +259,18 @@ def g32_decode_exact(q_bits, cache, block_tables, seq_lens, Hkv, scale, block_si
                                _ptr(np.ascontiguousarray(seq_lens, dtype=np.int32)), B, Hq, Hkv, D,
                                scale, block_size, bt.shape[1], bits, seed, int(bf16), nthreads)
     return out
+
+
+def fp8_encode(x, e4b15=False):
+    x = np.asarray(x, np.float32)
+    return np.array([lib().orc_f32_to_fp8(float(v), int(e4b15)) for v in x.ravel()],
+                    np.uint8).reshape(x.shape)
+
+
+def fp8_decode(b, e4b15=False):
+    b = np.asarray(b, np.uint8)
+    return np.array([lib().orc_fp8_to_f32(int(v), int(e4b15)) for v in b.ravel()],
+                    np.float32).reshape(b.shape)
 
 
 def qk_norm_rope(q_bits, k_bits, q_weight, k_weight, cos_sin, pos, eps, is_neox, bf16=False):

@@ -50,9 +50,11 @@ def test_tq_config_layouts():
         L = O.tq_layout(m)
         assert L.slot_size_aligned == slot
     assert capi.tq_config(256, "turboquant_4bit_nc").slot_size_aligned == 262
-    import pytest
-    with pytest.raises(capi.VmcError):
-        capi.tq_config(128, "turboquant_k8v4")
+    # fp8 keys (turboquant_k8v4): 128 key bytes, no norm, 4-bit values
+    c8 = capi.tq_config(128, "turboquant_k8v4")
+    L8 = O.tq_layout("turboquant_k8v4")
+    assert c8.slot_size_aligned == L8.slot_size_aligned == 196
+    assert c8.key_fp8 == L8.key_fp8 == 1 and c8.fp8_e4b15 == 0 and c8.key_packed_size == 128
 
 
 def test_g32_config_layouts():

@@ -97,7 +97,7 @@ def _run(dev, T, Hq, Hkv, bf16, neox, norms, seed, store=None, poison=0):
             ref = np.full(n, poison, np.uint8)
             if store[0] == "tq":
                 L = O.tq_layout(store[1])
-                _, mid = O.tq_tables(D, L.key_quant_bits)
+                _, mid = O.tq_tables(D, 4 if L.key_fp8 else L.key_quant_bits)
                 O.tq_store(rk, vb, slots, ref, BS, L, mid, bf16=bf16)
             else:
                 O.g32_store(rk, vb, slots, ref, BS, cfg.key_quant_bits, seed_s, bf16=bf16)
@@ -128,7 +128,8 @@ def test_paged_append(dev, bf16, fmt, hnd):
 
 
 @pytest.mark.parametrize("bf16", [False, True])
-@pytest.mark.parametrize("method", ["turboquant_4bit_nc", "turboquant_3bit_nc", "turboquant_k3v4_nc"])
+@pytest.mark.parametrize("method", ["turboquant_4bit_nc", "turboquant_3bit_nc", "turboquant_k3v4_nc",
+                                    "turboquant_k8v4"])
 def test_turboquant_append(dev, bf16, method):
     _run(dev, 40, 8, 8, bf16, True, "both", seed=7, store=("tq", method), poison=0x5A)
 

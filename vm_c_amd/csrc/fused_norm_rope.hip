@@ -24,7 +24,7 @@
 namespace vmc {
 namespace {
 
-enum { ST_NONE = 0, ST_F16 = 1, ST_BF16 = 2, ST_Q8_0 = 3, ST_Q4_0 = 4, ST_TQ = 5, ST_G32 = 6 };
+enum { ST_NONE = 0, ST_F16 = 1, ST_BF16 = 2, ST_Q8_0 = 3, ST_Q4_0 = 4, ST_TQ = 5, ST_G32 = 6, ST_K8 = 7 };
 
 struct FusedParams {
     uint16_t* q;
@@ -48,6 +48,7 @@ struct FusedParams {
     int SA, mse_bytes, key_packed, val_data;
     TQTables tab;
     G32Signs sg;
+    int e4b15;  // turboquant_k8v4 key codes
 };
 
 // The fp32 result is materialised before the conversion (opaque): otherwise
@@ -270,11 +271,13 @@ fused_norm_rope_kernel(FusedParams p) {
                 for (int e = 0; e < 8; ++e) y[e] = round_half<BF16>(y[e]);
                 const bool wr = slot >= 0;
                 float vv[8];
-                if constexpr (ST == ST_TQ || ST == ST_G32) {
+                if constexpr (ST == ST_TQ || ST == ST_G32 || ST == ST_K8) {
                     unpack8<BF16>(vr[r], vv);
                     const int64_t blk = slot / p.bs, off = slot % p.bs;
                     uint8_t* sp = p.kc + blk * p.bs * p.Hkv * p.SA + off * p.Hkv * p.SA + (int64_t)h * p.SA;
-                    if constexpr (ST == ST_TQ) {
+                    if constexpr (ST == ST_K8) {
+                        k8v4_store_vec<BF16>(y, vv, j, sp, wr, p.e4b15);
+                    } else if constexpr (ST == ST_TQ) {
                         tq_store_vec<128, KB, VB, BF16>(y, vv, j, sp, wr, sq[gi], p.tab, p.mse_bytes,
                                                         p.key_packed, p.val_data);
                     } else {
@@ -339,6 +342,7 @@ int dispatch(const FusedParams& prm, int st, const vmc_tq_config* c, hipStream_t
         case ST_BF16: return launch_fused<BF16, ST_BF16>(prm, s);
         case ST_Q8_0: return launch_fused<BF16, ST_Q8_0>(prm, s);
         case ST_Q4_0: return launch_fused<BF16, ST_Q4_0>(prm, s);
+        case ST_K8: return launch_fused<BF16, ST_K8>(prm, s);
         case ST_G32:
             return c->key_quant_bits == 4 ? launch_fused<BF16, ST_G32, 4, 4>(prm, s)
                                           : launch_fused<BF16, ST_G32, 3, 3>(prm, s);
@@ -397,9 +401,14 @@ extern "C" int vmc_fused_qk_norm_rope_store(void* q_buf, void* k_buf, const void
             prm.mse_bytes = tq_config->mse_bytes;
             prm.key_packed = tq_config->key_packed_size;
             prm.val_data = tq_config->val_data_bytes;
-            prm.tab = tq_tables(head_dim, tq_config->key_quant_bits);
-            prm.sg = g32_signs(tq_config->sign_seed);
-            st = tq_config->group_size != 0 ? ST_G32 : ST_TQ;
+            if (tq_config->key_fp8) {
+                prm.e4b15 = tq_config->fp8_e4b15 ? 1 : 0;
+                st = ST_K8;
+            } else {
+                prm.tab = tq_tables(head_dim, tq_config->key_quant_bits);
+                prm.sg = g32_signs(tq_config->sign_seed);
+                st = tq_config->group_size != 0 ? ST_G32 : ST_TQ;
+            }
         } else {
             const int64_t E = vmc_kv_entry_bytes(kv_format, head_dim);
             if (E < 0 || !value_cache) return VMC_EINVAL;

@@ -55,7 +55,10 @@ constexpr float kNegInf = -__builtin_inff();
 // slot per (token, head) holds the K part then the V part, each four 32-value
 // blocks {fp16 d, fp16 m, 16 B of nibbles} (4-bit) or {fp16 d, 12 B of 3-bit
 // codes} (3-bit) of the rotated vector
-enum { FMT_F16 = 0, FMT_BF16 = 1, FMT_Q8_0 = 2, FMT_Q4_0 = 3, FMT_TQ = 4, FMT_G4 = 5, FMT_G3 = 6 };
+// FMT_K8: turboquant_k8v4 (kernels_turboquant.h:47-55): K as 128 fp8 bytes
+// (the reference's own e4m3 / e4b15 codes), V as 4-bit codes + fp16 scale and
+// zero, 196-byte slots; no rotation, no norm
+enum { FMT_F16 = 0, FMT_BF16 = 1, FMT_Q8_0 = 2, FMT_Q4_0 = 3, FMT_TQ = 4, FMT_G4 = 5, FMT_G3 = 6, FMT_K8 = 7 };
 
 // Compile-time geometry of a page format (head_dim 128, block 16, at most 8
 // KV heads): TurboQuant slot fields (kernels_turboquant.h:29-45), GGUF entry
@@ -69,8 +72,9 @@ template <int FMT, int KB, int VB>
 struct Geo {
     static constexpr int mse = 16 * KB, key_packed = mse + 2, val_data = 16 * VB;
     // K and V in one slot per (token, head), one pool
-    static constexpr bool combined = FMT == FMT_TQ || FMT == FMT_G4 || FMT == FMT_G3;
+    static constexpr bool combined = FMT == FMT_TQ || FMT == FMT_G4 || FMT == FMT_G3 || FMT == FMT_K8;
     static constexpr int entry = FMT == FMT_TQ ? (key_packed + val_data + 4 + 1) / 2 * 2
+                                 : FMT == FMT_K8 ? 196
                                  : FMT == FMT_G4 ? 160 : FMT == FMT_G3 ? 112
                                  : FMT == FMT_Q8_0 ? 136 : FMT == FMT_Q4_0 ? 72 : 256;
     static constexpr int per_thread = combined ? entry : 2 * entry;  // staged bytes per token-head
@@ -156,6 +160,7 @@ struct DecodeParams {
     int mse_bytes, key_packed, val_data;
     TQTables tab;
     uint32_t sgn[4];     // per-32-group variant: bit i set = rotation sign of dim i is -1
+    int fp8_e4b15;       // turboquant_k8v4 keys: e4b15 (1) or e4m3 (0) codes
 };
 
 // ------------------------------------------------------------------ layout
@@ -262,6 +267,19 @@ __device__ __forceinline__ void build_pair_lut(uint32_t* lut, const TQTables& ta
     }
 }
 
+// fp16 bits of one of the reference's fp8 key codes (low byte of b):
+// e4m3 (1 + m/8) 2^(e-7) -> exponent field e + 8; e4b15 (1 + m/8) 2^(e-15)
+// -> exponent field e, or for e = 0 the fp16 subnormal (8 + m) 2^-18; the
+// zero code (either sign) -> signed zero.  Exact.
+__device__ __forceinline__ uint16_t fp8_f16_bits(uint32_t b, int e4b15) {
+    const uint32_t mag = b & 0x7fu, m = b & 7u;
+    const uint32_t h = !e4b15 ? (mag ? (mag << 7) + 0x2000u : 0u)
+                              : ((mag >> 3) ? (mag << 7) : (m ? 0x200u + (m << 6) : 0u));
+    return (uint16_t)(h | ((b & 0x80u) << 8));
+}
+__device__ __forceinline__ uint32_t lds32(const uint8_t* p) {
+    return *reinterpret_cast<const uint32_t*>(p);
+}
 __device__ __forceinline__ uint32_t lds16(const uint8_t* p) {
     return (uint32_t)*reinterpret_cast<const uint16_t*>(p);
 }
@@ -1001,7 +1019,7 @@ paged_decode_kernel(DecodeParams p) {
         constexpr int BUF = decltype(buf_c)::value;
         const uint8_t* kpage = smem + BUF * GE::kBuf;
         // V entries: the other cache's page, or the slot's V part
-        const uint8_t* vpage = kpage + (GE::combined ? GE::entry / 2 : GE::kHalf);
+        const uint8_t* vpage = kpage + (FMT == FMT_K8 ? 128 : GE::combined ? GE::entry / 2 : GE::kHalf);
         const int info = __builtin_amdgcn_readfirstlane(info_lds[i]);
         const int b = info >> 6;
         const int nv = (info >> 1) & 31;  // valid tokens in this page
@@ -1017,7 +1035,37 @@ paged_decode_kernel(DecodeParams p) {
         if constexpr (kStaged) {
             // ---- K operand for token r16
             const uint8_t* ke = kpage + k_off;
-            if constexpr (FMT == FMT_G4 || FMT == FMT_G3) {
+            if constexpr (FMT == FMT_K8) {
+                // fp8 keys: lane group grp owns bytes 32*grp .. +31 (MFMA j
+                // takes 8j .. 8j+7); every code is exact in fp16
+                const uint8_t* kb = ke + 32 * grp;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t w0 = lds32(kb + 8 * j), w1 = lds32(kb + 8 * j + 4);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        a[j][e] = __builtin_bit_cast(_Float16, fp8_f16_bits(w0 >> (8 * e), p.fp8_e4b15));
+                        a[j][4 + e] = __builtin_bit_cast(_Float16, fp8_f16_bits(w1 >> (8 * e), p.fp8_e4b15));
+                    }
+                }
+                // V of tokens 4*grp + i, dims 8*r16 .. +7: bytes 4*r16 .. +3
+                // (even dim in the low nibble), code * scale + zero
+#pragma unroll
+                for (int i2 = 0; i2 < 4; ++i2) {
+                    const bool ok = 4 * grp + i2 < nv;
+                    const uint8_t* vb = vpage + v_off[i2];
+                    const float sc = f16_bits_to_f32((uint16_t)lds16(vb + 64));
+                    const float zr = f16_bits_to_f32((uint16_t)lds16(vb + 66));
+                    const uint32_t cw = lds32(vb + 4 * r16);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float x0 = __builtin_fmaf((float)((cw >> (8 * e)) & 0xfu), sc, zr);
+                        const float x1 = __builtin_fmaf((float)((cw >> (8 * e + 4)) & 0xfu), sc, zr);
+                        vw[i2][e] = (uint32_t)f32_to_f16_bits(ok ? x0 : 0.0f) |
+                                    ((uint32_t)f32_to_f16_bits(ok ? x1 : 0.0f) << 16);
+                    }
+                }
+            } else if constexpr (FMT == FMT_G4 || FMT == FMT_G3) {
                 // block grp of the K part (dims 32*grp .. +31): code * d + m (4-bit)
                 // or (code - 4) * d (3-bit); MFMA j takes values 8j .. 8j+7
                 constexpr int BE = FMT == FMT_G4 ? 20 : 14;
@@ -1625,6 +1673,25 @@ extern "C" int vmc_turboquant_decode_attention(void* output, const void* query, 
         hipStream_t s = reinterpret_cast<hipStream_t>(stream);
         return cfg->key_quant_bits == 4 ? launch_decode<FMT_G4, 0, 0, false>(prm, s)
                                         : launch_decode<FMT_G3, 0, 0, false>(prm, s);
+    }
+    if (cfg->key_fp8) {
+        // turboquant_k8v4: fp8 keys (q not rotated, no norm), 4-bit values;
+        // scale and zero stored as fp16
+        if (half_dtype != VMC_DTYPE_F16) return VMC_EINVAL;
+        int rc = setup_common(prm, output, query, block_tables, seq_lens, batch_size, num_heads,
+                              num_kv_heads, head_dim, (int)block_size, (int)max_num_blocks_per_req,
+                              scale, max_num_kv_splits, workspace, workspace_bytes);
+        if (rc != VMC_OK) return rc;
+        if (batch_size == 0) return VMC_OK;
+        if (!kv_cache) return VMC_EINVAL;
+        prm.kc = reinterpret_cast<const uint8_t*>(kv_cache);
+        prm.vc = prm.kc;
+        prm.q_bf16 = 0;
+        prm.entry_bytes = cfg->slot_size_aligned;
+        prm.page_bytes = (int64_t)kBs * num_kv_heads * cfg->slot_size_aligned;
+        prm.hnd = 0;
+        prm.fp8_e4b15 = cfg->fp8_e4b15 ? 1 : 0;
+        return launch_decode<FMT_K8, 0, 0, false>(prm, reinterpret_cast<hipStream_t>(stream));
     }
     int rc = setup_common(prm, output, query, block_tables, seq_lens, batch_size, num_heads,
                           num_kv_heads, head_dim, (int)block_size, (int)max_num_blocks_per_req,

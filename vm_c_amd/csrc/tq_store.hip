@@ -69,6 +69,31 @@ g32_store_kernel(const uint16_t* __restrict__ key, const uint16_t* __restrict__ 
     g32_quantize<BITS>(yv, j, sp + P, slot >= 0);
 }
 
+// turboquant_k8v4 (half_to_fp8_store_kernel, turboquant_kernels.cu:188-245),
+// same 16-lane ownership: fp8 key bytes by the reference's converter, the V
+// part as in every TurboQuant slot
+template <bool BF16>
+__global__ void __launch_bounds__(256)
+k8v4_store_kernel(const uint16_t* __restrict__ key, const uint16_t* __restrict__ value,
+                  uint8_t* __restrict__ cache, const int64_t* __restrict__ slot_mapping, int T,
+                  int Hkv, int64_t bs, int e4b15) {
+    constexpr int D = kGroup * kDims, S = 196;
+    const int lane = threadIdx.x & 63, j = lane & (kGroup - 1);
+    const int gi = threadIdx.x / kGroup;
+    const int64_t pid = (int64_t)blockIdx.x * (blockDim.x / kGroup) + gi;
+    const bool live = pid < (int64_t)T * Hkv;
+    const int64_t pv = live ? pid : 0;  // every lane stays in the exchanges
+    const int64_t t = pv / Hkv;
+    const int h = (int)(pv % Hkv);
+    const int64_t slot = live ? slot_mapping[t] : -1;  // :207: slot < 0 skips
+    const int64_t blk = slot / bs, off = slot % bs;
+    uint8_t* sp = cache + blk * bs * Hkv * S + off * Hkv * S + (int64_t)h * S;
+    float yk[kDims], yv[kDims];
+    load8<BF16>(key + pv * D + kDims * j, yk);
+    load8<BF16>(value + pv * D + kDims * j, yv);
+    k8v4_store_vec<BF16>(yk, yv, j, sp, slot >= 0, e4b15);
+}
+
 int launch_g32_store(const void* key, const void* value, void* cache, const int64_t* slots, int T,
                      int Hkv, int64_t bs, const vmc_tq_config* c, bool bf16, hipStream_t stream) {
     const int64_t n = (int64_t)T * Hkv;
@@ -128,6 +153,21 @@ extern "C" int vmc_turboquant_store(const void* key, const void* value, void* kv
     if (num_tokens < 0 || num_kv_heads <= 0 || block_size <= 0) return VMC_EINVAL;
     if (half_dtype != VMC_DTYPE_F16 && half_dtype != VMC_DTYPE_BF16) return VMC_EINVAL;
     if (num_tokens == 0) return VMC_OK;
+    if (cfg->key_fp8) {
+        const int64_t grid = ((int64_t)num_tokens * num_kv_heads + 15) / 16;
+        if (grid > 0x7fffffff) return VMC_EINVAL;
+        hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+        if (half_dtype == VMC_DTYPE_BF16)
+            hipLaunchKernelGGL((k8v4_store_kernel<true>), dim3((unsigned)grid), dim3(256), 0, s,
+                               (const uint16_t*)key, (const uint16_t*)value, (uint8_t*)kv_cache, slot_mapping,
+                               num_tokens, num_kv_heads, block_size, cfg->fp8_e4b15);
+        else
+            hipLaunchKernelGGL((k8v4_store_kernel<false>), dim3((unsigned)grid), dim3(256), 0, s,
+                               (const uint16_t*)key, (const uint16_t*)value, (uint8_t*)kv_cache, slot_mapping,
+                               num_tokens, num_kv_heads, block_size, cfg->fp8_e4b15);
+        VMC_LAUNCH_CHECK();
+        return VMC_OK;
+    }
     if (!key || !value || !kv_cache || !slot_mapping) return VMC_EINVAL;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const bool bf = half_dtype == VMC_DTYPE_BF16;

@@ -100,7 +100,14 @@ G32Signs g32_signs(unsigned long long seed) {
 
 bool tq_config_valid(const vmc_tq_config* c) {
     if (!c) return false;
-    if (c->key_fp8) return false;
+    if (c->key_fp8) {
+        // turboquant_k8v4 (kernels_turboquant.h:29-55): 128 fp8 key bytes,
+        // 4-bit values, no norm, 196-byte slots
+        return c->head_dim == 128 && c->group_size == 0 && c->key_quant_bits == 8 &&
+               c->value_quant_bits == 4 && c->norm_correction == 0 && c->mse_bytes == 128 &&
+               c->key_packed_size == 128 && c->val_data_bytes == 64 && c->value_packed_size == 68 &&
+               c->slot_size == 196 && c->slot_size_aligned == 196;
+    }
     if (c->group_size != 0) {
         // per-32-group variant: head_dim 128, equal K/V bits, the fixed part sizes
         const int b = c->key_quant_bits;
@@ -133,7 +140,13 @@ extern "C" int vmc_tq_config_from_method(int head_dim, const char* method, vmc_t
     c.max_num_kv_splits = 32;
     const std::string m = method ? method : "";
     if (m == "turboquant_k8v4") {
-        return VMC_EINVAL;  // fp8 keys: not implemented
+        // fp8 keys; the reference picks e4b15 below sm_89 (no native fp8), e4m3
+        // otherwise -- e4m3 here, fp8_e4b15 may be set by the caller
+        c.key_quant_bits = 8;
+        c.value_quant_bits = 4;
+        c.norm_correction = 0;
+        c.key_fp8 = 1;
+        c.fp8_e4b15 = 0;
     } else if (m == "turboquant_k3v4_nc") {
         c.key_quant_bits = 3;
         c.value_quant_bits = 4;
@@ -161,8 +174,8 @@ extern "C" int vmc_tq_config_from_method(int head_dim, const char* method, vmc_t
         return VMC_EINVAL;
     }
     c.n_centroids = 1 << c.key_quant_bits;
-    c.mse_bytes = (head_dim * c.key_quant_bits + 7) / 8;
-    c.key_packed_size = c.mse_bytes + 2;
+    c.mse_bytes = c.key_fp8 ? head_dim : (head_dim * c.key_quant_bits + 7) / 8;
+    c.key_packed_size = c.key_fp8 ? head_dim : c.mse_bytes + 2;
     c.val_data_bytes = (head_dim * c.value_quant_bits + 7) / 8;
     c.value_packed_size = c.val_data_bytes + 4;
     c.slot_size = c.key_packed_size + c.value_packed_size;

@@ -65,6 +65,43 @@ __device__ __forceinline__ void store_codes8(const int* q, uint8_t* dst, int j) 
     }
 }
 
+// V part of a TurboQuant slot (tq_store_mse_kernel :314-350, the same in
+// half_to_fp8_store_kernel :228-244): asymmetric min/max over the whole
+// vector, codes at vp, fp16/bf16 scale and zero at vp + val_data (+2)
+template <int VB, bool BF16>
+__device__ __forceinline__ void tq_store_v(const float* vv, int j, uint8_t* vp, bool write, int val_data) {
+    int q[kDims];
+    float y[kDims];
+#pragma unroll
+    for (int e = 0; e < kDims; ++e) y[e] = vv[e];
+    float vmin = y[0], vmax = y[0];
+#pragma unroll
+    for (int e = 1; e < kDims; ++e) {
+        vmin = fminf(vmin, y[e]);
+        vmax = fmaxf(vmax, y[e]);
+    }
+    static_for<4>([&](auto m) {
+        constexpr int M = 1 << decltype(m)::value;
+        vmin = fminf(vmin, row_xor<M>(vmin, j));
+        vmax = fmaxf(vmax, row_xor<M>(vmax, j));
+    });
+    constexpr int VMAXQ = VB == 4 ? 15 : 7;
+    float vscale = (vmax - vmin) / (float)VMAXQ;
+    vscale = fmaxf(vscale, 1e-8f);
+#pragma unroll
+    for (int e = 0; e < kDims; ++e) {
+        int qq = (int)roundf((y[e] - vmin) / vscale);
+        q[e] = qq < 0 ? 0 : (qq > VMAXQ ? VMAXQ : qq);
+    }
+    if (write) {
+        store_codes8<VB>(q, vp, j);
+        if (j == 0) {
+            *reinterpret_cast<uint16_t*>(vp + val_data) = f32_to_half<BF16>(vscale);
+            *reinterpret_cast<uint16_t*>(vp + val_data + 2) = f32_to_half<BF16>(vmin);
+        }
+    }
+}
+
 // The TurboQuant store of one (token, head) vector held by a 16-lane group,
 // lane j owning dims 8j .. 8j+7 of K (y, overwritten) and V (vv):
 // tq_store_mse_kernel (src/cuda/turboquant_kernels.cu:247-351) after the
@@ -125,36 +162,7 @@ __device__ __forceinline__ void tq_store_vec(float* y, float* vv, int j, uint8_t
         if (j == 0) *reinterpret_cast<uint16_t*>(sp + mse_bytes) = f32_to_half<BF16>(norm);
     }
 
-    // ---- V: asymmetric min/max over the whole vector (:314-347)
-#pragma unroll
-    for (int e = 0; e < kDims; ++e) y[e] = vv[e];
-    float vmin = y[0], vmax = y[0];
-#pragma unroll
-    for (int e = 1; e < kDims; ++e) {
-        vmin = fminf(vmin, y[e]);
-        vmax = fmaxf(vmax, y[e]);
-    }
-    static_for<4>([&](auto m) {
-        constexpr int M = 1 << decltype(m)::value;
-        vmin = fminf(vmin, row_xor<M>(vmin, j));
-        vmax = fmaxf(vmax, row_xor<M>(vmax, j));
-    });
-    constexpr int VMAXQ = VB == 4 ? 15 : 7;
-    float vscale = (vmax - vmin) / (float)VMAXQ;
-    vscale = fmaxf(vscale, 1e-8f);
-#pragma unroll
-    for (int e = 0; e < kDims; ++e) {
-        int qq = (int)roundf((y[e] - vmin) / vscale);
-        q[e] = qq < 0 ? 0 : (qq > VMAXQ ? VMAXQ : qq);
-    }
-    if (write) {
-        uint8_t* vp = sp + key_packed;
-        store_codes8<VB>(q, vp, j);
-        if (j == 0) {
-            *reinterpret_cast<uint16_t*>(vp + val_data) = f32_to_half<BF16>(vscale);
-            *reinterpret_cast<uint16_t*>(vp + val_data + 2) = f32_to_half<BF16>(vmin);
-        }
-    }
+    tq_store_v<VB, BF16>(vv, j, sp + key_packed, write, val_data);
 }
 
 // ---- per-32-group variant (no reference counterpart; format in vmc_attn.h)
@@ -274,6 +282,57 @@ __device__ __forceinline__ void g32_quantize(const float* y, int j, uint8_t* dst
             }
         }
     }
+}
+
+// float_to_fp8_e4m3 / _e4b15 (src/cuda/turboquant_kernels.cu:47-83, :98-134),
+// operation for operation: exponent bias 7 or 15, the mantissa taken as
+// (m + 2^18) >> 19 with a carry into the exponent when it exceeds 7,
+// exponent 255 -> 0x7C / 0x78, overflow -> 0x7F, values below the smallest
+// normal -> exponent field 1 with mantissa min(7, ((1.m >> shift) + 4) >> 4)
+__device__ __forceinline__ uint32_t fp8_encode(float v, int e4b15) {
+    const uint32_t bits = __builtin_bit_cast(uint32_t, v);
+    const uint32_t sign = (bits >> 31) & 1u;
+    const int exp_f32 = (int)((bits >> 23) & 0xffu);
+    const uint32_t mant_f32 = bits & 0x7fffffu;
+    if (exp_f32 == 0 && mant_f32 == 0) return sign << 7;
+    if (exp_f32 == 255) return (sign << 7) | (e4b15 ? 0x78u : 0x7Cu);
+    int e = exp_f32 - 127 + (e4b15 ? 15 : 7);
+    if (e < 1) {
+        const int shift = 1 - e;
+        if (shift > 24) return sign << 7;
+        const uint32_t mant = (0x800000u | mant_f32) >> shift;
+        uint32_t m8 = (mant + 4) >> 4;
+        if (m8 > 7) m8 = 7;
+        return (sign << 7) | (1u << 3) | m8;
+    }
+    if (e > 15) return (sign << 7) | 0x7Fu;
+    uint32_t m8 = (mant_f32 + 0x40000u) >> 19;
+    if (m8 > 7) {
+        m8 = 0;
+        ++e;
+        if (e > 15) return (sign << 7) | 0x7Fu;
+    }
+    return (sign << 7) | ((uint32_t)(e & 0xf) << 3) | (m8 & 7u);
+}
+
+// turboquant_k8v4 slot of one (token, head) vector (half_to_fp8_store_kernel,
+// turboquant_kernels.cu:188-245): K byte d = fp8(k[d]) at sp + d (lane j:
+// bytes 8j .. 8j+7; slots are 196 bytes, so 4-byte aligned), then the V part
+template <bool BF16>
+__device__ __forceinline__ void k8v4_store_vec(const float* k, const float* vv, int j, uint8_t* sp, bool write,
+                                               int e4b15) {
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        w0 |= fp8_encode(k[e], e4b15) << (8 * e);
+        w1 |= fp8_encode(k[4 + e], e4b15) << (8 * e);
+    }
+    if (write) {
+        uint32_t* d = reinterpret_cast<uint32_t*>(sp + 8 * j);
+        d[0] = w0;
+        d[1] = w1;
+    }
+    tq_store_v<4, BF16>(vv, j, sp + 128, write, 64);
 }
 
 }  // namespace vmc

@@ -111,8 +111,8 @@ TurboQuantBackend::TurboQuantBackend(int head_dim, const std::string& quant_meth
       head_dim_(head_dim) {
     HIP_CHECK(hipSetDevice(gpu_device_));
     config_ = TQConfig::from_method(head_dim, quant_method.c_str(), gpu_device_);
-    if (config_.key_fp8) throw std::runtime_error("TurboQuantBackend: turboquant_k8v4 is not implemented");
-    buffers_.init(head_dim, config_.key_quant_bits, gpu_device);
+    // fp8 keys (turboquant_k8v4) use no codebook and no rotation
+    if (!config_.key_fp8) buffers_.init(head_dim, config_.key_quant_bits, gpu_device);
 }
 
 TurboQuantBackend::~TurboQuantBackend() {

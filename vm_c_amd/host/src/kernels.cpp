@@ -181,7 +181,6 @@ void turboquant_store(const void* key, const void* value, void* kv_cache,
                       TQWorkspace& workspace, hipStream_t stream, ScalarType dtype) {
     (void)buffers;
     (void)workspace;
-    if (config.key_fp8) throw std::runtime_error("turboquant_k8v4 (fp8 keys) is not implemented");
     const vmc_tq_config c = config.to_c();
     VMC_CALL(vmc_turboquant_store(key, value, kv_cache, slot_mapping, num_tokens, num_kv_heads,
                                   head_dim, block_size, &c, vmc_dtype_of(dtype), stream));
@@ -195,7 +194,6 @@ void turboquant_decode_attention(void* output, const void* query, const void* kv
                                  TQWorkspace& workspace, int max_num_kv_splits,
                                  hipStream_t stream) {
     (void)buffers;
-    if (config.key_fp8) throw std::runtime_error("turboquant_k8v4 (fp8 keys) is not implemented");
     int dev = 0;
     HIP_CHECK(hipGetDevice(&dev));
     workspace.ensure_decode(batch_size, num_heads, num_kv_heads, head_dim, max_num_blocks_per_req,
@@ -335,7 +333,6 @@ void fused_qk_norm_rope_store(void* q_buf, void* k_buf, const void* v_buf,
                               int num_heads, int num_kv_heads, int head_dim, float rms_norm_eps,
                               bool is_neox, int64_t block_size, const TQConfig& config,
                               hipStream_t stream, ScalarType dtype) {
-    if (config.key_fp8) throw std::runtime_error("turboquant_k8v4 (fp8 keys) is not implemented");
     if (!kv_cache || !slot_mapping)
         throw std::runtime_error("fused_qk_norm_rope_store: TurboQuant append needs a cache and slots");
     const vmc_tq_config c = config.to_c();
