@@ -82,6 +82,11 @@ struct Geo {
     static constexpr int spp = staged ? (per_thread + 63) / 64 : 1;
     static constexpr bool dma = FMT == FMT_TQ;
     static constexpr int kHalf = kBs * 8 * entry;  // one cache's page, 8 heads
+    // staged NHD pages sit in LDS with a 16-byte pad after each token row, so
+    // the 16 rows a lane group reads fall on distinct LDS banks (a row of
+    // 8 x 160 B is a multiple of the 256-byte bank cycle: all 16 would hit one)
+    static constexpr int kPad = 16;
+    static constexpr int kHalfP = kHalf + kBs * kPad;
     // TurboQuant: a head group (<= 4 heads) of 16 tokens, each token's run
     // fetched as a window of whole 16-byte chunks (at most nc_max of them)
     static constexpr int nc_of(int h) { return (h * entry + 30) / 16; }
@@ -89,7 +94,7 @@ struct Geo {
     static constexpr int nc_max = nc_of(4);
     // chunks per lane per page for any group size (1..4 heads, one wave each)
     static constexpr int spt = std::max(std::max(spt_of(1), spt_of(2)), std::max(spt_of(3), spt_of(4)));
-    static constexpr int kBuf = dma ? kBs * nc_max * 16 : combined ? kHalf : 2 * kHalf;  // one LDS buffer
+    static constexpr int kBuf = dma ? kBs * nc_max * 16 : combined ? kHalfP : 2 * kHalfP;  // one LDS buffer
     // pages whose block-table entries are staged in LDS at once, and waves per
     // workgroup (TurboQuant: one head group of at most 4 KV heads)
     static constexpr int chunk = 256;
@@ -154,6 +159,10 @@ struct DecodeParams {
     int grid;            // page ranges (flat) or sequences (per-sequence mode)
     int hgroups, hpw;    // KV-head groups per page (one workgroup each), heads per group
     int row_bytes;       // TurboQuant: one token's entries, all KV heads (Hkv * slot)
+    int lds_pad;         // staged NHD pages: token rows padded in LDS (row a whole number of chunks)
+    int lds_row;         // padded row bytes in LDS
+    int row_chunks;      // 16-byte chunks of one token row in HBM
+    int rc_inv;          // ceil(2^20 / row_chunks): chunk / row_chunks = chunk * rc_inv >> 20 (chunk * row_chunks < 2^20)
     int tq_nc;           // TurboQuant: 16-byte chunks fetched per token for one head group
     int q_bf16;
     // TurboQuant
@@ -649,14 +658,25 @@ paged_decode_kernel(DecodeParams p) {
             stage[S][c] = *src;
         }
     };
-    // slot S of the register ring goes to LDS buffer S (V half at kHalf)
+    // slot S of the register ring goes to LDS buffer S (V half at kHalfP);
+    // chunk ci of a padded page lands in row ci / row_chunks
+    const bool lds_pad = p.lds_pad != 0;
+    const int lds_row = p.lds_row, row_chunks = p.row_chunks;
+    const uint32_t rc_inv = (uint32_t)p.rc_inv;
     auto stage_store = [&](auto slot_c) __attribute__((always_inline)) {
         constexpr int S = decltype(slot_c)::value;
         uint8_t* buf = smem + S * GE::kBuf;
 #pragma unroll
         for (int c = 0; c < SPP; ++c) {
             const int idx = tid + c * nthreads;
-            const int off = (GE::combined || idx < n16_k) ? 16 * idx : GE::kHalf + 16 * (idx - n16_k);
+            const bool kpart = GE::combined || idx < n16_k;
+            const int ci = kpart ? idx : idx - n16_k;
+            int off = 16 * ci;
+            if (lds_pad) {
+                const int row = (int)(((uint32_t)ci * rc_inv) >> 20);
+                off = row * lds_row + 16 * (ci - row * row_chunks);
+            }
+            if (!kpart) off += GE::kHalfP;
             if (idx < n16) *reinterpret_cast<u32x4*>(buf + off) = stage[S][c];
         }
     };
@@ -704,7 +724,7 @@ paged_decode_kernel(DecodeParams p) {
     // (TurboQuant: this group's window layout, local head = wave)
     auto lds_entry = [&](int t) {
         return FMT == FMT_TQ ? t * tq_nc * 16 + run_mis(t) + wave * GE::entry
-                             : entry_off<FMT>(t, g, Hkv, GE::entry, hnd);
+                             : lds_pad ? t * lds_row + g * GE::entry : entry_off<FMT>(t, g, Hkv, GE::entry, hnd);
     };
     const int k_off = lds_entry(r16);
     int v_off[4];
@@ -1019,7 +1039,7 @@ paged_decode_kernel(DecodeParams p) {
         constexpr int BUF = decltype(buf_c)::value;
         const uint8_t* kpage = smem + BUF * GE::kBuf;
         // V entries: the other cache's page, or the slot's V part
-        const uint8_t* vpage = kpage + (FMT == FMT_K8 ? 128 : GE::combined ? GE::entry / 2 : GE::kHalf);
+        const uint8_t* vpage = kpage + (FMT == FMT_K8 ? 128 : GE::combined ? GE::entry / 2 : GE::kHalfP);
         const int info = __builtin_amdgcn_readfirstlane(info_lds[i]);
         const int b = info >> 6;
         const int nv = (info >> 1) & 31;  // valid tokens in this page
@@ -1540,6 +1560,11 @@ int launch_decode(DecodeParams& prm, hipStream_t stream) {
     } else {
         prm.hpw = prm.Hkv;
         prm.hgroups = 1;
+        const int rowb = prm.Hkv * GE::entry;
+        prm.lds_pad = GE::staged && !prm.hnd && rowb % 16 == 0;
+        prm.row_chunks = rowb / 16;
+        prm.lds_row = rowb + GE::kPad;
+        prm.rc_inv = prm.row_chunks > 0 ? ((1 << 20) + prm.row_chunks - 1) / prm.row_chunks : 0;
         prm.grid = prm.per_seq ? prm.B : flat_grid(prm.B, prm.Hkv, prm.max_blocks, prm.max_splits, num_cus());
     }
     hipLaunchKernelGGL(kern, dim3(prm.grid * prm.hgroups), dim3(64 * prm.hpw), 0, stream, prm);
