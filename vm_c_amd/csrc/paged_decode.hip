@@ -286,6 +286,22 @@ __device__ __forceinline__ uint16_t fp8_f16_bits(uint32_t b, int e4b15) {
                               : ((mag >> 3) ? (mag << 7) : (m ? 0x200u + (m << 6) : 0u));
     return (uint16_t)(h | ((b & 0x80u) << 8));
 }
+// Two GGUF values -> packed fp16 x * d, bit-identical to fp16(float(x) * d):
+// x * d is exact in fp32 (8-bit x, 11-bit d), and v_pk_mul_f16 rounds the
+// exact product once, as the conversion does.  x enters as fp16 exactly: the
+// two bytes spread into the 16-bit halves, then 0x64 in the high byte makes
+// 1024 + low byte; q8_0 flips the sign bit first (1024 + x + 128 - 1152 = x),
+// q4_0 takes a nibble (1024 + u - 1032 = u - 8).
+__device__ __forceinline__ uint32_t q8_pair_f16(uint32_t w16, f16x2 d2) {
+    const uint32_t t = __builtin_amdgcn_perm(0u, w16, 0x0c010c00u) ^ 0x64806480u;
+    const f16x2 x = __builtin_bit_cast(f16x2, t) - f16x2{(_Float16)1152.0f, (_Float16)1152.0f};
+    return __builtin_bit_cast(uint32_t, x * d2);
+}
+__device__ __forceinline__ uint32_t q4_pair_f16(uint32_t w16, int sh, f16x2 d2) {
+    const uint32_t t = ((__builtin_amdgcn_perm(0u, w16, 0x0c010c00u) >> sh) & 0x000f000fu) | 0x64006400u;
+    const f16x2 x = __builtin_bit_cast(f16x2, t) - f16x2{(_Float16)1032.0f, (_Float16)1032.0f};
+    return __builtin_bit_cast(uint32_t, x * d2);
+}
 __device__ __forceinline__ uint32_t lds32(const uint8_t* p) {
     return *reinterpret_cast<const uint32_t*>(p);
 }
@@ -1118,52 +1134,40 @@ paged_decode_kernel(DecodeParams p) {
                 // GGUF blocks: lane group grp owns block grp (dims 32*grp .. +31)
                 constexpr int BE = FMT == FMT_Q8_0 ? 34 : 18;
                 const uint8_t* kb = ke + BE * grp;
-                const float d = f16_bits_to_f32((uint16_t)lds16(kb));
+                const uint32_t d16 = lds16(kb);
+                const f16x2 d2 = __builtin_bit_cast(f16x2, d16 | (d16 << 16));
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
+                    u32x4 kw;
 #pragma unroll
                     for (int e = 0; e < 8; e += 2) {
                         const int jj = 8 * j + e;  // index inside the 32-block
-                        float x0, x1;
                         if constexpr (FMT == FMT_Q8_0) {
-                            const uint32_t wv = lds16(kb + 2 + jj);
-                            x0 = (float)(int8_t)(wv & 0xff);
-                            x1 = (float)(int8_t)(wv >> 8);
+                            kw[e / 2] = q8_pair_f16(lds16(kb + 2 + jj), d2);
                         } else {
-                            const int bi = jj & 15;
-                            const uint32_t wv = lds16(kb + 2 + bi);
-                            const int sh = jj < 16 ? 0 : 4;
-                            x0 = (float)((int)((wv >> sh) & 0xf) - 8);
-                            x1 = (float)((int)((wv >> (8 + sh)) & 0xf) - 8);
+                            kw[e / 2] = q4_pair_f16(lds16(kb + 2 + (jj & 15)), jj < 16 ? 0 : 4, d2);
                         }
-                        a[j][e] = (_Float16)(x0 * d);
-                        a[j][e + 1] = (_Float16)(x1 * d);
                     }
+                    a[j] = __builtin_bit_cast(AT, kw);
                 }
 #pragma unroll
                 for (int i2 = 0; i2 < 4; ++i2) {
                     const int tok = 4 * grp + i2;
                     const bool ok = tok < nv;
                     const uint8_t* vb = vpage + v_off[i2] + BE * (r16 >> 2);
-                    const float dv = ok ? f16_bits_to_f32((uint16_t)lds16(vb)) : 0.0f;
+                    const uint32_t dv16 = lds16(vb);
+                    const f16x2 dv2 = __builtin_bit_cast(f16x2, dv16 | (dv16 << 16));
                     const int q0 = 8 * (r16 & 3);  // index inside the block
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        float x0, x1;
+                        uint32_t x;
                         if constexpr (FMT == FMT_Q8_0) {
-                            const uint32_t wv = lds16(vb + 2 + q0 + 2 * e);
-                            x0 = (float)(int8_t)(wv & 0xff);
-                            x1 = (float)(int8_t)(wv >> 8);
+                            x = q8_pair_f16(lds16(vb + 2 + q0 + 2 * e), dv2);
                         } else {
                             const int jj = q0 + 2 * e;
-                            const int bi = jj & 15;
-                            const int sh = jj < 16 ? 0 : 4;
-                            const uint32_t wv = lds16(vb + 2 + bi);
-                            x0 = (float)((int)((wv >> sh) & 0xf) - 8);
-                            x1 = (float)((int)((wv >> (8 + sh)) & 0xf) - 8);
+                            x = q4_pair_f16(lds16(vb + 2 + (jj & 15)), jj < 16 ? 0 : 4, dv2);
                         }
-                        vw[i2][e] = (uint32_t)f32_to_f16_bits(ok ? x0 * dv : 0.0f) |
-                                    ((uint32_t)f32_to_f16_bits(ok ? x1 * dv : 0.0f) << 16);
+                        vw[i2][e] = ok ? x : 0u;
                     }
                 }
             }
