@@ -302,6 +302,30 @@ __device__ __forceinline__ uint32_t q4_pair_f16(uint32_t w16, int sh, f16x2 d2) 
     const f16x2 x = __builtin_bit_cast(f16x2, t) - f16x2{(_Float16)1032.0f, (_Float16)1032.0f};
     return __builtin_bit_cast(uint32_t, x * d2);
 }
+// Codes 2e and 2e+1 of an 8-code word of the per-32-group variant -> packed
+// fp16 code * d + m (4-bit, one fused rounding) or (code - 4) * d (3-bit,
+// exact operand times d, one rounding): the two fields go to the 16-bit
+// halves under 0x64 (fp16 1024 + code), then a packed subtract and a packed
+// FMA / multiply.
+template <int FMT>
+__device__ __forceinline__ uint32_t g32_pair_f16(uint32_t cw, int e, f16x2 d2, f16x2 m2) {
+    uint32_t z;
+    if constexpr (FMT == FMT_G4) {
+        const uint32_t b = (cw >> (8 * e)) & 0xffu;  // code 2e low nibble, 2e+1 high
+        z = ((b | (b << 12)) & 0x000f000fu) | 0x64006400u;
+    } else {
+        const uint32_t t = (cw >> (6 * e)) & 0x3fu;  // code 2e bits 0-2, 2e+1 bits 3-5
+        z = ((t | (t << 13)) & 0x00070007u) | 0x64006400u;
+    }
+    const f16x2 f = __builtin_bit_cast(f16x2, z);
+    if constexpr (FMT == FMT_G4) {
+        const f16x2 c = f - f16x2{(_Float16)1024.0f, (_Float16)1024.0f};
+        return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c, d2, m2));
+    } else {
+        const f16x2 c = f - f16x2{(_Float16)1028.0f, (_Float16)1028.0f};
+        return __builtin_bit_cast(uint32_t, c * d2);
+    }
+}
 __device__ __forceinline__ uint32_t lds32(const uint8_t* p) {
     return *reinterpret_cast<const uint32_t*>(p);
 }
@@ -1106,29 +1130,28 @@ paged_decode_kernel(DecodeParams p) {
                 // or (code - 4) * d (3-bit); MFMA j takes values 8j .. 8j+7
                 constexpr int BE = FMT == FMT_G4 ? 20 : 14;
                 const uint8_t* kb = ke + BE * grp;
-                const float d = f16_bits_to_f32((uint16_t)lds16(kb));
-                const float m = FMT == FMT_G4 ? f16_bits_to_f32((uint16_t)lds16(kb + 2)) : -4.0f * d;
+                const uint32_t d16 = lds16(kb), m16 = FMT == FMT_G4 ? lds16(kb + 2) : 0u;
+                const f16x2 d2 = __builtin_bit_cast(f16x2, d16 | (d16 << 16));
+                const f16x2 m2 = __builtin_bit_cast(f16x2, m16 | (m16 << 16));
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const uint32_t cw = g32_codes8<FMT>(kb, j);
+                    u32x4 kw;
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) a[j][e] = (_Float16)__builtin_fmaf(g32_code<FMT>(cw, e), d, m);
+                    for (int e = 0; e < 4; ++e) kw[e] = g32_pair_f16<FMT>(cw, e, d2, m2);
+                    a[j] = __builtin_bit_cast(AT, kw);
                 }
                 // V of tokens 4*grp + i, dims 8*r16 .. +7: block r16 / 4, values 8 (r16 % 4) ..
 #pragma unroll
                 for (int i2 = 0; i2 < 4; ++i2) {
                     const bool ok = 4 * grp + i2 < nv;
                     const uint8_t* vb = vpage + v_off[i2] + BE * (r16 >> 2);
-                    const float dv = f16_bits_to_f32((uint16_t)lds16(vb));
-                    const float mv = FMT == FMT_G4 ? f16_bits_to_f32((uint16_t)lds16(vb + 2)) : -4.0f * dv;
+                    const uint32_t dv16 = lds16(vb), mv16 = FMT == FMT_G4 ? lds16(vb + 2) : 0u;
+                    const f16x2 dv2 = __builtin_bit_cast(f16x2, dv16 | (dv16 << 16));
+                    const f16x2 mv2 = __builtin_bit_cast(f16x2, mv16 | (mv16 << 16));
                     const uint32_t cw = g32_codes8<FMT>(vb, r16 & 3);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float x0 = __builtin_fmaf(g32_code<FMT>(cw, 2 * e), dv, mv);
-                        const float x1 = __builtin_fmaf(g32_code<FMT>(cw, 2 * e + 1), dv, mv);
-                        vw[i2][e] = (uint32_t)f32_to_f16_bits(ok ? x0 : 0.0f) |
-                                    ((uint32_t)f32_to_f16_bits(ok ? x1 : 0.0f) << 16);
-                    }
+                    for (int e = 0; e < 4; ++e) vw[i2][e] = ok ? g32_pair_f16<FMT>(cw, e, dv2, mv2) : 0u;
                 }
             } else {
                 // GGUF blocks: lane group grp owns block grp (dims 32*grp .. +31)
