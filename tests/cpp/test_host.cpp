@@ -232,6 +232,8 @@ static void test_swap() {
             std::memset(static_cast<uint8_t*>(m.key_cache_ptr(l)) + b * bb, (int)(10 * l + b), bb);
             std::memset(static_cast<uint8_t*>(m.value_cache_ptr(l)) + b * bb, (int)(50 + 10 * l + b), bb);
         }
+    // quantized pages need no separate compression step (reference stubs)
+    CHECK(m.compress_kv_block(s[0]) && m.decompress_kv_block(s[0]));
     m.swap_request_slots("r");
     CHECK(m.num_free_cpu_blocks() == 2);
     CHECK(m.num_free_gpu_blocks() == 5);
