@@ -236,10 +236,6 @@ public:
     bool compress_kv_block(int64_t) { return true; }
     bool decompress_kv_block(int64_t) { return true; }
 
-    // kv_cache_manager.cpp:731-737: no-ops that report success -- pages are
-    // stored in their quantized format from the append on
-    bool compress_kv_block(int64_t block_id);
-    bool decompress_kv_block(int64_t block_id);
     void offload_to_cpu(int64_t block_id);
     void load_from_cpu(int64_t block_id);
 

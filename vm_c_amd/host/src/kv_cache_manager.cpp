@@ -544,16 +544,6 @@ void KVCacheManager::copy_block(int64_t gpu_block, int64_t cpu_block, bool to_cp
 
 // :710-748: copy to the first free host block, move the block's reference
 // count and hash there
-bool KVCacheManager::compress_kv_block(int64_t block_id) {
-    (void)block_id;
-    return true;
-}
-
-bool KVCacheManager::decompress_kv_block(int64_t block_id) {
-    (void)block_id;
-    return true;
-}
-
 void KVCacheManager::offload_to_cpu(int64_t block_id) {
     if (block_id < 0 || block_id >= (int64_t)gpu_blocks_.size() || num_cpu_blocks_ == 0) return;
     if (gpu_to_cpu_mapping_.count(block_id)) return;
