@@ -144,6 +144,25 @@ int vmc_tq_config_from_method(int head_dim, const char* method, vmc_tq_config* o
 int vmc_tq_host_tables(int head_dim, int bits, float* centroids, float* midpoints);
 
 /*
+ * Prefill attention over the paged cache (a cached prefix plus this step's
+ * tokens, already appended): token t is token_positions[t] of sequence
+ * token_to_seq[t] and attends that sequence's positions 0 .. token_positions[t]
+ * through its block_tables row.  Replaces vm_c::paged_attention_prefill
+ * (src/cuda/attention_kernels.cu:416-436, the path of
+ * PagedAttentionBackend::forward_prefill); semantics as
+ * vmc_paged_attention_decode with one row per token (formats, layouts,
+ * workspace: vmc_paged_decode_workspace_size(num_tokens, ...), none when
+ * max_num_kv_splits == 1).  query / out [num_tokens][num_heads][head_dim].
+ */
+int vmc_paged_attention_prefill(void* out, const void* query, const void* key_cache,
+                                const void* value_cache, int num_tokens, int num_heads,
+                                int num_kv_heads, int head_dim, float scale, int block_size,
+                                int max_num_blocks_per_req, const int32_t* block_tables,
+                                const int32_t* token_to_seq, const int32_t* token_positions,
+                                int q_dtype, int kv_format, int layout, int max_num_kv_splits,
+                                void* workspace, size_t workspace_bytes, vmc_stream_t stream);
+
+/*
  * Quantize-on-append of K/V into packed TurboQuant slots.
  * Replaces vm_c::turboquant_store (kernels_turboquant.h:107-119;
  * turboquant_kernels.cu:792-860).  key/value [num_tokens][num_kv_heads]

@@ -221,6 +221,47 @@ static void test_paged_backend(const std::string& dtype, const std::string& layo
     double err = 0;
     CHECK(close(dO.get(), ex, &err));
     std::printf("  decode max err %.3g\n", err);
+
+    // a second prefill chunk over the cached prompts: store_kv, then
+    // forward_prefill attends through the pages (token t: positions 0 .. p)
+    std::vector<ScheduledRequest> ch(lens.size());
+    for (size_t i = 0; i < lens.size(); ++i) {
+        ch[i].request_id = "p" + std::to_string(i);
+        ch[i].num_computed_tokens = lens[i];
+        ch[i].num_scheduled_tokens = 5 + (int)i;
+        ch[i].is_prefill = true;
+    }
+    HostBatchMetadata hc = build_batch_metadata(mgr, ch);
+    CHECK(hc.ok && hc.num_computed_tokens > 0);
+    const int Tc = hc.num_tokens;
+    std::vector<uint16_t> Kc((size_t)Tc * Hkv * D), Vc(Kc.size()), Qc((size_t)Tc * Hq * D);
+    orc_randn_f16(Kc.data(), (int64_t)Kc.size(), 10, 1);
+    orc_randn_f16(Vc.data(), (int64_t)Vc.size(), 10, 2);
+    orc_randn_f16(Qc.data(), (int64_t)Qc.size(), 10, 3);
+    Dev<uint16_t> dKc(Kc), dVc(Vc), dQc(Qc), dOc(Qc.size());
+    AttentionMetadata mc = dm.upload(hc, BS, nullptr);
+    be.store_kv(dKc.p, dVc.p, mgr.key_cache_ptr(0), mgr.value_cache_ptr(0), mc.slot_mapping, Tc, Hkv, D, BS,
+                0, nullptr);
+    be.forward_prefill(dOc.p, dQc.p, dKc.p, dVc.p, mgr.key_cache_ptr(0), mgr.value_cache_ptr(0), mc, Hq, Hkv,
+                       D, 1.0f / std::sqrt((float)D), BS, ScalarType::FLOAT16, nullptr);
+    HIP_CHECK(hipDeviceSynchronize());
+    gk = pool_bytes(mgr.key_cache_ptr(0), pool_n);
+    gv = pool_bytes(mgr.value_cache_ptr(0), pool_n);
+    const int mb = hc.max_num_blocks_per_req;
+    std::vector<int32_t> bt_rows((size_t)Tc * mb), len_rows(Tc);
+    for (int t = 0; t < Tc; ++t) {
+        const int sq = hc.token_to_seq[t];
+        std::copy(hc.block_tables.begin() + (size_t)sq * mb, hc.block_tables.begin() + (size_t)(sq + 1) * mb,
+                  bt_rows.begin() + (size_t)t * mb);
+        len_rows[t] = hc.token_positions[t] + 1;
+    }
+    std::vector<float> qcf(Qc.size());
+    orc_f16_to_f32_n(Qc.data(), qcf.data(), (int64_t)Qc.size());
+    std::vector<double> exc(Qc.size());
+    orc_paged_decode_exact(exc.data(), qcf.data(), gk.data(), gv.data(), fmt, layout == "hnd", bt_rows.data(),
+                           len_rows.data(), Tc, Hq, Hkv, D, 1.0 / std::sqrt((double)D), BS, mb, 0);
+    CHECK(close(dOc.get(), exc, &err));
+    std::printf("  chunked prefill over the cache max err %.3g\n", err);
 }
 
 // vm_c::fused_qk_norm_rope_store through the host layer: q/k in place and the

@@ -60,6 +60,9 @@ def load():
     L.vmc_paged_attention_decode.restype = _I
     L.vmc_paged_attention_decode.argtypes = [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F,
                                              _I, _I, _I, _I, _P, _SZ, _P]
+    L.vmc_paged_attention_prefill.restype = _I
+    L.vmc_paged_attention_prefill.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _P, _P, _P,
+                                              _I, _I, _I, _I, _P, _SZ, _P]
     L.vmc_tq_config_from_method.restype = _I
     L.vmc_tq_config_from_method.argtypes = [_I, C.c_char_p, C.POINTER(TQConfig)]
     L.vmc_tq_host_tables.restype = _I
@@ -248,3 +251,23 @@ def fused_qk_norm_rope_store(q, k, v, q_norm_weight, k_norm_weight, cos_sin_cach
         eps, int(bool(is_neox)), block_size, cache_stride, kv_format, layout,
         None if tq_cfg is None else C.byref(tq_cfg), _dtype_code(q), _stream(stream))
     _check(rc, "vmc_fused_qk_norm_rope_store")
+
+
+def paged_attention_prefill(out, query, key_cache, value_cache, block_tables, token_to_seq,
+                            token_positions, num_kv_heads, scale, block_size=16, kv_format=KV_F16,
+                            layout=LAYOUT_NHD, workspace=None, max_splits=1, stream=None):
+    """query/out [T][Hq][D]: token t attends positions 0 .. token_positions[t] of
+    sequence token_to_seq[t] in the paged cache."""
+    import torch
+    T, Hq, D = query.shape
+    max_blocks = block_tables.shape[1]
+    ws_bytes = paged_decode_workspace_size(T, Hq, num_kv_heads, D, max_blocks, block_size, max_splits)
+    if workspace is None and ws_bytes > 0:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=query.device)
+    rc = load().vmc_paged_attention_prefill(
+        _ptr(out), _ptr(query), _ptr(key_cache), _ptr(value_cache), T, Hq, num_kv_heads, D, scale,
+        block_size, max_blocks, _ptr(block_tables), _ptr(token_to_seq), _ptr(token_positions),
+        _dtype_code(query), kv_format, layout, max_splits, _ptr(workspace),
+        0 if workspace is None else workspace.numel() * workspace.element_size(), _stream(stream))
+    _check(rc, "vmc_paged_attention_prefill")
+    return out

@@ -170,12 +170,17 @@ struct DecodeParams {
     TQTables tab;
     uint32_t sgn[4];     // per-32-group variant: bit i set = rotation sign of dim i is -1
     int fp8_e4b15;       // turboquant_k8v4 keys: e4b15 (1) or e4m3 (0) codes
+    // paged prefill: query row b is token b of sequence row_seq[b] at
+    // position row_pos[b] (it attends positions 0 .. row_pos[b]); null =
+    // row b is sequence b with seq_lens[b] tokens
+    const int32_t* row_seq;
+    const int32_t* row_pos;
 };
 
 // ------------------------------------------------------------------ layout
 
 __device__ __forceinline__ int seq_pages(const DecodeParams& p, int b, int* L_out) {
-    const int L = min(p.seq_lens[b], p.max_blocks * kBs);
+    const int L = min(p.row_seq ? p.row_pos[b] + 1 : p.seq_lens[b], p.max_blocks * kBs);
     *L_out = L;
     return L > 0 ? (L + kBs - 1) / kBs : 0;
 }
@@ -1299,7 +1304,7 @@ paged_decode_kernel(DecodeParams p) {
             }
             const int b = seg_b[lo], L = seg_L[lo], pp = gp - seg_ps[lo];
             const int pages_b = (L + kBs - 1) / kBs;
-            const int32_t blk = p.bt[(int64_t)b * p.max_blocks + pp];
+            const int32_t blk = p.bt[(int64_t)(p.row_seq ? p.row_seq[b] : b) * p.max_blocks + pp];
             const int nv = blk < 0 ? 0 : min(kBs, L - pp * kBs);
             const int ends = pp == pages_b - 1 || gp == p_hi - 1;
             bt_lds[i] = blk;
@@ -1653,19 +1658,20 @@ extern "C" size_t vmc_turboquant_decode_workspace_size(int batch_size, int num_h
                                            (int)block_size, max_num_kv_splits);
 }
 
-extern "C" int vmc_paged_attention_decode(void* out, const void* query, const void* key_cache,
-                                          const void* value_cache, const int32_t* block_tables,
-                                          const int32_t* seq_lens, int batch_size, int num_heads,
-                                          int num_kv_heads, int head_dim, int block_size,
-                                          int max_num_blocks_per_req, float scale, int q_dtype,
-                                          int kv_format, int layout, int max_num_kv_splits,
-                                          void* workspace, size_t workspace_bytes,
-                                          vmc_stream_t stream) {
+namespace {
+int paged_decode_rows(void* out, const void* query, const void* key_cache, const void* value_cache,
+                      const int32_t* block_tables, const int32_t* seq_lens, const int32_t* row_seq,
+                      const int32_t* row_pos, int batch_size, int num_heads, int num_kv_heads,
+                      int head_dim, int block_size, int max_num_blocks_per_req, float scale,
+                      int q_dtype, int kv_format, int layout, int max_num_kv_splits, void* workspace,
+                      size_t workspace_bytes, vmc_stream_t stream) {
     DecodeParams prm = {};
     int rc = setup_common(prm, out, query, block_tables, seq_lens, batch_size, num_heads,
                           num_kv_heads, head_dim, block_size, max_num_blocks_per_req, scale,
                           max_num_kv_splits, workspace, workspace_bytes);
     if (rc != VMC_OK) return rc;
+    prm.row_seq = row_seq;
+    prm.row_pos = row_pos;
     if (q_dtype != VMC_DTYPE_F16 && q_dtype != VMC_DTYPE_BF16) return VMC_EINVAL;
     if (layout != VMC_LAYOUT_NHD && layout != VMC_LAYOUT_HND) return VMC_EINVAL;
     const int64_t E = vmc_kv_entry_bytes(kv_format, head_dim);
@@ -1689,6 +1695,40 @@ extern "C" int vmc_paged_attention_decode(void* out, const void* query, const vo
         case VMC_KV_Q4_0: return launch_decode<FMT_Q4_0, 0, 0, false>(prm, s);
         default: return VMC_EINVAL;
     }
+}
+}  // namespace
+
+extern "C" int vmc_paged_attention_decode(void* out, const void* query, const void* key_cache,
+                                          const void* value_cache, const int32_t* block_tables,
+                                          const int32_t* seq_lens, int batch_size, int num_heads,
+                                          int num_kv_heads, int head_dim, int block_size,
+                                          int max_num_blocks_per_req, float scale, int q_dtype,
+                                          int kv_format, int layout, int max_num_kv_splits,
+                                          void* workspace, size_t workspace_bytes,
+                                          vmc_stream_t stream) {
+    return paged_decode_rows(out, query, key_cache, value_cache, block_tables, seq_lens, nullptr,
+                             nullptr, batch_size, num_heads, num_kv_heads, head_dim, block_size,
+                             max_num_blocks_per_req, scale, q_dtype, kv_format, layout,
+                             max_num_kv_splits, workspace, workspace_bytes, stream);
+}
+
+extern "C" int vmc_paged_attention_prefill(void* out, const void* query, const void* key_cache,
+                                           const void* value_cache, int num_tokens, int num_heads,
+                                           int num_kv_heads, int head_dim, float scale,
+                                           int block_size, int max_num_blocks_per_req,
+                                           const int32_t* block_tables,
+                                           const int32_t* token_to_seq,
+                                           const int32_t* token_positions, int q_dtype,
+                                           int kv_format, int layout, int max_num_kv_splits,
+                                           void* workspace, size_t workspace_bytes,
+                                           vmc_stream_t stream) {
+    if (num_tokens > 0 && (!token_to_seq || !token_positions)) return VMC_EINVAL;
+    // token_positions stands in for seq_lens (not read when rows are indirect)
+    return paged_decode_rows(out, query, key_cache, value_cache, block_tables, token_positions,
+                             token_to_seq, token_positions, num_tokens, num_heads, num_kv_heads,
+                             head_dim, block_size, max_num_blocks_per_req, scale, q_dtype,
+                             kv_format, layout, max_num_kv_splits, workspace, workspace_bytes,
+                             stream);
 }
 
 extern "C" int vmc_turboquant_decode_attention(void* output, const void* query, const void* kv_cache,

@@ -48,6 +48,19 @@ void reshape_and_cache(const void* key, const void* value, void* key_cache, void
                        const void* v_scale, ScalarType dtype, hipStream_t stream = nullptr,
                        const std::string& layout = "nhd");
 
+// Prefill over the paged cache (cached prefix + this step's appended tokens):
+// token t attends positions 0 .. token_positions[t] of sequence
+// token_to_seq[t] (attention_kernels.cu:416-436).  seq_lens and num_reqs are
+// accepted for signature compatibility; no workspace (one pass per token).
+void paged_attention_prefill(void* out, const void* query, const void* key_cache,
+                             const void* value_cache, int num_tokens, int num_heads,
+                             int num_kv_heads, int head_dim, float scale, int64_t block_size,
+                             int64_t max_num_blocks_per_req, const int32_t* block_tables,
+                             const int32_t* seq_lens, const int32_t* token_to_seq,
+                             const int32_t* token_positions, int num_reqs,
+                             const std::string& kv_cache_dtype, ScalarType dtype,
+                             hipStream_t stream = nullptr, const std::string& layout = "nhd");
+
 // One pass per sequence (no split, no workspace): one workgroup per request.
 void paged_attention_v1(void* out, const void* query, const void* key_cache,
                         const void* value_cache, const AttentionParams& params,

@@ -47,9 +47,16 @@ void PagedAttentionBackend::forward_prefill(void* output, const void* query, con
                                             int num_heads, int num_kv_heads, int head_dim,
                                             float scale, int64_t block_size, ScalarType dtype,
                                             hipStream_t stream) {
-    (void)key_cache;
-    (void)value_cache;
-    (void)block_size;
+    if (meta.num_computed_tokens > 0 && meta.num_decode_tokens == 0) {
+        // a cached prefix: attend through the pages (store_kv has appended
+        // this step's tokens), as the reference's paged prefill does
+        paged_attention_prefill(output, query, key_cache, value_cache, meta.num_tokens, num_heads,
+                                num_kv_heads, head_dim, scale, block_size, meta.max_num_blocks_per_req,
+                                meta.block_tables, meta.seq_lens, meta.token_to_seq,
+                                meta.token_positions, meta.num_reqs, kv_cache_dtype_, dtype, stream,
+                                kv_cache_layout_);
+        return;
+    }
     require_no_cached_prefix(meta, "PagedAttentionBackend::forward_prefill");
     if (!key || !value) throw std::runtime_error("PagedAttentionBackend::forward_prefill: needs the step's K/V");
     flash_attention_prefill_local(output, query, key, value, meta.num_tokens, num_heads, num_kv_heads,
