@@ -227,6 +227,24 @@ int vmc_turboquant_decode_attention(void* output, const void* query, const void*
                                     size_t workspace_bytes, vmc_stream_t stream);
 
 /*
+ * Prefill attention over packed TurboQuant pages with a cached prefix: token
+ * t is token_positions[t] of sequence token_to_seq[t] and attends positions
+ * 0 .. token_positions[t] through its block_tables row (this step's tokens
+ * already stored).  No counterpart in the reference, whose TurboQuant prefill
+ * attends only the step's local K/V (attention_backend.cpp:153-196); the
+ * arithmetic is that of vmc_turboquant_decode_attention with one row per
+ * token (workspace: vmc_turboquant_decode_workspace_size(num_tokens, ...),
+ * none when max_num_kv_splits == 1).
+ */
+int vmc_turboquant_prefill_attention(void* output, const void* query, const void* kv_cache,
+                                     const int32_t* block_tables, const int32_t* token_to_seq,
+                                     const int32_t* token_positions, int num_tokens, int num_heads,
+                                     int num_kv_heads, int head_dim, float scale, int64_t block_size,
+                                     int64_t max_num_blocks_per_req, const vmc_tq_config* cfg,
+                                     int half_dtype, int max_num_kv_splits, void* workspace,
+                                     size_t workspace_bytes, vmc_stream_t stream);
+
+/*
  * Causal flash-attention prefill over contiguous ("local") K/V, bf16 or fp16,
  * MFMA for QK^T and PV, fp32 softmax.  Each sequence's tokens are contiguous
  * with positions 0..n-1, so token t attends tokens [t - pos(t), t].

@@ -163,6 +163,43 @@ static void test_turboquant_backend(const char* method) {
                             hd.num_reqs, Hq, Hkv, D, scale, BS, hd.max_num_blocks_per_req, &L, C.data(), 0, 0);
     CHECK(close(dO1.get(), exd, &err));
     std::printf("  decode max err %.3g\n", err);
+    if (!g32) {
+        // a prefill chunk over the cached context: through the packed pages
+        std::vector<ScheduledRequest> ch(lens.size());
+        for (size_t i = 0; i < lens.size(); ++i) {
+            ch[i].request_id = "r" + std::to_string(i);
+            ch[i].num_computed_tokens = lens[i] + 1;
+            ch[i].num_scheduled_tokens = 3 + (int)i;
+            ch[i].is_prefill = true;
+        }
+        HostBatchMetadata hc = build_batch_metadata(mgr, ch);
+        CHECK(hc.ok && hc.num_computed_tokens > 0);
+        const int Tc = hc.num_tokens;
+        std::vector<uint16_t> Kc((size_t)Tc * Hkv * D), Vc(Kc.size()), Qc((size_t)Tc * Hq * D);
+        orc_randn_f16(Kc.data(), (int64_t)Kc.size(), 12, 1);
+        orc_randn_f16(Vc.data(), (int64_t)Vc.size(), 12, 2);
+        orc_randn_f16(Qc.data(), (int64_t)Qc.size(), 12, 3);
+        Dev<uint16_t> dKc(Kc), dVc(Vc), dQc(Qc), dOc(Qc.size());
+        AttentionMetadata mc = dm.upload(hc, BS, nullptr);
+        be.store_kv(dKc.p, dVc.p, pool, nullptr, mc.slot_mapping, Tc, Hkv, D, BS, 0, nullptr);
+        be.forward_prefill(dOc.p, dQc.p, dKc.p, dVc.p, pool, nullptr, mc, Hq, Hkv, D, scale, BS,
+                           ScalarType::FLOAT16, nullptr);
+        HIP_CHECK(hipDeviceSynchronize());
+        got = pool_bytes(pool, pool_n);
+        const int mb = hc.max_num_blocks_per_req;
+        std::vector<int32_t> bt_rows((size_t)Tc * mb), len_rows(Tc);
+        for (int t = 0; t < Tc; ++t) {
+            const int sq = hc.token_to_seq[t];
+            std::copy(hc.block_tables.begin() + (size_t)sq * mb, hc.block_tables.begin() + (size_t)(sq + 1) * mb,
+                      bt_rows.begin() + (size_t)t * mb);
+            len_rows[t] = hc.token_positions[t] + 1;
+        }
+        std::vector<double> exc(Qc.size());
+        orc_tq_decode_exact(exc.data(), Qc.data(), got.data(), bt_rows.data(), len_rows.data(), Tc, Hq, Hkv, D,
+                            scale, BS, mb, &L, C.data(), 0, 0);
+        CHECK(close(dOc.get(), exc, &err));
+        std::printf("  chunked prefill over the cache max err %.3g\n", err);
+    }
     for (size_t i = 0; i < lens.size(); ++i) mgr.free_slots("r" + std::to_string(i));
     CHECK(mgr.num_free_gpu_blocks() == 63);
 }

@@ -49,3 +49,39 @@ def test_paged_prefill_over_cached_prefix(dev, fmt, hnd, splits):
                               w.bt[tok_seq], tok_pos + 1, Hkv, float(w.scale), BS, hnd=hnd)
     ok, err = close_report(out.float().cpu().numpy(), ex, 2e-3, 1e-2)
     assert ok, f"max err {err}"
+
+
+@pytest.mark.parametrize("method", ["turboquant_3bit_nc", "turboquant_4bit_g32", "turboquant_k8v4"])
+def test_turboquant_prefill_over_cached_prefix(dev, method):
+    """vmc_turboquant_prefill_attention (no reference counterpart: the
+    reference's TurboQuant prefill attends only the step's local K/V)."""
+    import torch
+    from vm_c_amd import capi
+    prefix = np.array([100, 0, 513])
+    new = np.array([37, 20, 64])
+    lens = prefix + new
+    Hq, Hkv = 16, 4
+    w = make_workload(lens, Hq=Hq, Hkv=Hkv, seed=41, pool_slack=2)
+    cfg = capi.tq_config(128, method)
+    cache = torch.zeros(w.num_blocks * BS * Hkv * cfg.slot_size_aligned, dtype=torch.uint8, device=dev)
+    capi.turboquant_store(torch.from_numpy(w.K).to(dev), torch.from_numpy(w.V).to(dev), cache,
+                          torch.from_numpy(w.slots).to(dev), BS, cfg)
+    tok_seq = np.concatenate([np.full(new[b], b) for b in range(len(lens))]).astype(np.int32)
+    tok_pos = np.concatenate([np.arange(prefix[b], lens[b]) for b in range(len(lens))]).astype(np.int32)
+    T = tok_seq.size
+    q = np.random.default_rng(6).standard_normal((T, Hq, 128)).astype(np.float16)
+    out = torch.full((T, Hq, 128), float("nan"), dtype=torch.float16, device=dev)
+    capi.turboquant_prefill_attention(out, torch.from_numpy(q).to(dev), cache, torch.from_numpy(w.bt).to(dev),
+                                      torch.from_numpy(tok_seq).to(dev), torch.from_numpy(tok_pos).to(dev),
+                                      Hkv, float(w.scale), cfg, block_size=BS)
+    torch.cuda.synchronize()
+    got = cache.cpu().numpy()
+    bt_rows, len_rows = w.bt[tok_seq], (tok_pos + 1).astype(np.int32)
+    if method.endswith("_g32"):
+        ex = O.g32_decode_exact(bits16(q), got, bt_rows, len_rows, Hkv, float(w.scale), BS, 4, 0)
+    else:
+        L = O.tq_layout(method)
+        c, _ = O.tq_tables(128, 4 if L.key_fp8 else L.key_quant_bits)
+        ex = O.tq_decode_exact(bits16(q), got, bt_rows, len_rows, Hkv, float(w.scale), BS, L, c)
+    ok, err = close_report(out.float().cpu().numpy(), ex, 2e-3, 1e-2)
+    assert ok, f"max err {err}"

@@ -63,6 +63,9 @@ def load():
     L.vmc_paged_attention_prefill.restype = _I
     L.vmc_paged_attention_prefill.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _P, _P, _P,
                                               _I, _I, _I, _I, _P, _SZ, _P]
+    L.vmc_turboquant_prefill_attention.restype = _I
+    L.vmc_turboquant_prefill_attention.argtypes = [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I64,
+                                                   _I64, C.POINTER(TQConfig), _I, _I, _P, _SZ, _P]
     L.vmc_tq_config_from_method.restype = _I
     L.vmc_tq_config_from_method.argtypes = [_I, C.c_char_p, C.POINTER(TQConfig)]
     L.vmc_tq_host_tables.restype = _I
@@ -270,4 +273,16 @@ def paged_attention_prefill(out, query, key_cache, value_cache, block_tables, to
         _dtype_code(query), kv_format, layout, max_splits, _ptr(workspace),
         0 if workspace is None else workspace.numel() * workspace.element_size(), _stream(stream))
     _check(rc, "vmc_paged_attention_prefill")
+    return out
+
+
+def turboquant_prefill_attention(out, query, kv_cache, block_tables, token_to_seq, token_positions,
+                                 num_kv_heads, scale, cfg, block_size=16, stream=None):
+    """One row per token over the packed pages (cached prefix + appended step)."""
+    T, Hq, D = query.shape
+    rc = load().vmc_turboquant_prefill_attention(
+        _ptr(out), _ptr(query), _ptr(kv_cache), _ptr(block_tables), _ptr(token_to_seq),
+        _ptr(token_positions), T, Hq, num_kv_heads, D, scale, block_size, block_tables.shape[1],
+        C.byref(cfg), _dtype_code(query), 1, None, 0, _stream(stream))
+    _check(rc, "vmc_turboquant_prefill_attention")
     return out

@@ -1731,14 +1731,12 @@ extern "C" int vmc_paged_attention_prefill(void* out, const void* query, const v
                              stream);
 }
 
-extern "C" int vmc_turboquant_decode_attention(void* output, const void* query, const void* kv_cache,
-                                               const int32_t* block_tables, const int32_t* seq_lens,
-                                               int batch_size, int num_heads, int num_kv_heads,
-                                               int head_dim, float scale, int64_t block_size,
-                                               int64_t max_num_blocks_per_req,
-                                               const vmc_tq_config* cfg, int half_dtype,
-                                               int max_num_kv_splits, void* workspace,
-                                               size_t workspace_bytes, vmc_stream_t stream) {
+namespace {
+int tq_decode_rows(void* output, const void* query, const void* kv_cache, const int32_t* block_tables,
+                   const int32_t* seq_lens, const int32_t* row_seq, const int32_t* row_pos, int batch_size,
+                   int num_heads, int num_kv_heads, int head_dim, float scale, int64_t block_size,
+                   int64_t max_num_blocks_per_req, const vmc_tq_config* cfg, int half_dtype,
+                   int max_num_kv_splits, void* workspace, size_t workspace_bytes, vmc_stream_t stream) {
     if (!tq_config_valid(cfg) || cfg->head_dim != head_dim) return VMC_EINVAL;
     if (half_dtype != VMC_DTYPE_F16 && half_dtype != VMC_DTYPE_BF16) return VMC_EINVAL;
     if (max_num_blocks_per_req > 0x7fffffff) return VMC_EINVAL;
@@ -1751,6 +1749,8 @@ extern "C" int vmc_turboquant_decode_attention(void* output, const void* query, 
                               num_kv_heads, head_dim, (int)block_size, (int)max_num_blocks_per_req,
                               scale, max_num_kv_splits, workspace, workspace_bytes);
         if (rc != VMC_OK) return rc;
+        prm.row_seq = row_seq;
+        prm.row_pos = row_pos;
         if (batch_size == 0) return VMC_OK;
         if (!kv_cache) return VMC_EINVAL;
         prm.kc = reinterpret_cast<const uint8_t*>(kv_cache);
@@ -1774,6 +1774,8 @@ extern "C" int vmc_turboquant_decode_attention(void* output, const void* query, 
                               num_kv_heads, head_dim, (int)block_size, (int)max_num_blocks_per_req,
                               scale, max_num_kv_splits, workspace, workspace_bytes);
         if (rc != VMC_OK) return rc;
+        prm.row_seq = row_seq;
+        prm.row_pos = row_pos;
         if (batch_size == 0) return VMC_OK;
         if (!kv_cache) return VMC_EINVAL;
         prm.kc = reinterpret_cast<const uint8_t*>(kv_cache);
@@ -1789,6 +1791,8 @@ extern "C" int vmc_turboquant_decode_attention(void* output, const void* query, 
                           num_kv_heads, head_dim, (int)block_size, (int)max_num_blocks_per_req,
                           scale, max_num_kv_splits, workspace, workspace_bytes);
     if (rc != VMC_OK) return rc;
+    prm.row_seq = row_seq;
+    prm.row_pos = row_pos;
     if (batch_size == 0) return VMC_OK;
     if (!kv_cache) return VMC_EINVAL;
     // stored norm/scale/zero are half_dtype; the kernel reads them as fp16
@@ -1815,4 +1819,34 @@ extern "C" int vmc_turboquant_decode_attention(void* output, const void* query, 
     if (kb == 3 && vb == 4)
         return half ? launch_decode<FMT_TQ, 3, 4, false, true>(prm, s) : launch_decode<FMT_TQ, 3, 4, false>(prm, s);
     return VMC_EINVAL;
+}
+}  // namespace
+
+extern "C" int vmc_turboquant_decode_attention(void* output, const void* query, const void* kv_cache,
+                                               const int32_t* block_tables, const int32_t* seq_lens,
+                                               int batch_size, int num_heads, int num_kv_heads,
+                                               int head_dim, float scale, int64_t block_size,
+                                               int64_t max_num_blocks_per_req,
+                                               const vmc_tq_config* cfg, int half_dtype,
+                                               int max_num_kv_splits, void* workspace,
+                                               size_t workspace_bytes, vmc_stream_t stream) {
+    return tq_decode_rows(output, query, kv_cache, block_tables, seq_lens, nullptr, nullptr, batch_size,
+                          num_heads, num_kv_heads, head_dim, scale, block_size, max_num_blocks_per_req, cfg,
+                          half_dtype, max_num_kv_splits, workspace, workspace_bytes, stream);
+}
+
+extern "C" int vmc_turboquant_prefill_attention(void* output, const void* query, const void* kv_cache,
+                                                const int32_t* block_tables, const int32_t* token_to_seq,
+                                                const int32_t* token_positions, int num_tokens,
+                                                int num_heads, int num_kv_heads, int head_dim, float scale,
+                                                int64_t block_size, int64_t max_num_blocks_per_req,
+                                                const vmc_tq_config* cfg, int half_dtype,
+                                                int max_num_kv_splits, void* workspace,
+                                                size_t workspace_bytes, vmc_stream_t stream) {
+    if (num_tokens > 0 && (!token_to_seq || !token_positions)) return VMC_EINVAL;
+    // token_positions stands in for seq_lens (not read when rows are indirect)
+    return tq_decode_rows(output, query, kv_cache, block_tables, token_positions, token_to_seq,
+                          token_positions, num_tokens, num_heads, num_kv_heads, head_dim, scale, block_size,
+                          max_num_blocks_per_req, cfg, half_dtype, max_num_kv_splits, workspace,
+                          workspace_bytes, stream);
 }

@@ -157,9 +157,18 @@ void TurboQuantBackend::forward_prefill(void* output, const void* query, const v
                                         const void* value_cache, const AttentionMetadata& meta,
                                         int num_heads, int num_kv_heads, int head_dim, float scale,
                                         int64_t block_size, ScalarType dtype, hipStream_t stream) {
-    (void)key_cache;
     (void)value_cache;
-    (void)block_size;
+    if (meta.num_computed_tokens > 0 && meta.num_decode_tokens == 0) {
+        // a cached prefix: one row per token through the packed pages
+        // (store_kv has appended this step's tokens); the reference attends
+        // only the local K/V here
+        const vmc_tq_config c = config_.to_c();
+        VMC_CALL(vmc_turboquant_prefill_attention(
+            output, query, key_cache, meta.block_tables, meta.token_to_seq, meta.token_positions,
+            meta.num_tokens, num_heads, num_kv_heads, head_dim, scale, block_size,
+            meta.max_num_blocks_per_req, &c, vmc_dtype_of(dtype), 1, nullptr, 0, stream));
+        return;
+    }
     require_no_cached_prefix(meta, "TurboQuantBackend::forward_prefill");
     flash_attention_prefill_local(output, query, key, value, meta.num_tokens, num_heads, num_kv_heads,
                                   head_dim, scale, meta.token_to_seq, meta.token_positions, dtype, stream);
