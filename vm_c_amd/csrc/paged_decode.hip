@@ -1135,16 +1135,49 @@ paged_decode_kernel(DecodeParams p) {
                 // or (code - 4) * d (3-bit); MFMA j takes values 8j .. 8j+7
                 constexpr int BE = FMT == FMT_G4 ? 20 : 14;
                 const uint8_t* kb = ke + BE * grp;
-                const uint32_t d16 = lds16(kb), m16 = FMT == FMT_G4 ? lds16(kb + 2) : 0u;
-                const f16x2 d2 = __builtin_bit_cast(f16x2, d16 | (d16 << 16));
-                const f16x2 m2 = __builtin_bit_cast(f16x2, m16 | (m16 << 16));
+                if constexpr (FMT == FMT_G4) {
+                    // 20-byte blocks, 4-byte aligned: d | m, then bytes 0-15
+                    // (value v < 16: low nibble of byte v, else high nibble of
+                    // byte v - 16); MFMA j: values 8j .. 8j+7
+                    const uint32_t dm = lds32(kb);
+                    const uint32_t q[4] = {lds32(kb + 4), lds32(kb + 8), lds32(kb + 12), lds32(kb + 16)};
+                    const f16x2 d2 = __builtin_bit_cast(f16x2, (dm & 0xffffu) * 0x10001u);
+                    const f16x2 m2 = __builtin_bit_cast(f16x2, (dm >> 16) * 0x10001u);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const uint32_t cw = g32_codes8<FMT>(kb, j);
-                    u32x4 kw;
+                    for (int j = 0; j < 4; ++j) {
+                        u32x4 kw;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) kw[e] = g32_pair_f16<FMT>(cw, e, d2, m2);
-                    a[j] = __builtin_bit_cast(AT, kw);
+                        for (int e = 0; e < 4; ++e) {
+                            const uint32_t w = q[2 * (j & 1) + (e >> 1)];
+                            const uint32_t sp = __builtin_amdgcn_perm(0u, w, (e & 1) ? 0x0c030c02u : 0x0c010c00u);
+                            const uint32_t z = ((sp >> (j >= 2 ? 4 : 0)) & 0x000f000fu) | 0x64006400u;
+                            const f16x2 c = __builtin_bit_cast(f16x2, z) - f16x2{(_Float16)1024.0f, (_Float16)1024.0f};
+                            kw[e] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c, d2, m2));
+                        }
+                        a[j] = __builtin_bit_cast(AT, kw);
+                    }
+                } else {
+                    // 14-byte blocks, 2-byte aligned: four dwords from the
+                    // 4-byte floor (inside the 112-byte entry), realigned so
+                    // c0..c2 hold the 12 code bytes
+                    const bool off2 = ((uint32_t)(uintptr_t)kb & 2u) != 0u;
+                    const uint32_t* aw4 = reinterpret_cast<const uint32_t*>(kb - (off2 ? 2 : 0));
+                    const uint32_t a0 = aw4[0], a1 = aw4[1], a2 = aw4[2], a3 = aw4[3];
+                    const uint32_t d16 = off2 ? a0 >> 16 : a0 & 0xffffu;
+                    const uint32_t c0 = off2 ? a1 : __builtin_amdgcn_alignbyte(a1, a0, 2);
+                    const uint32_t c1 = off2 ? a2 : __builtin_amdgcn_alignbyte(a2, a1, 2);
+                    const uint32_t c2 = off2 ? a3 : __builtin_amdgcn_alignbyte(a3, a2, 2);
+                    const uint32_t g24[4] = {c0 & 0xffffffu, (c0 >> 24) | ((c1 & 0xffffu) << 8),
+                                             (c1 >> 16) | ((c2 & 0xffu) << 16), c2 >> 8};
+                    const f16x2 d2 = __builtin_bit_cast(f16x2, d16 * 0x10001u);
+                    const f16x2 m2 = {};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        u32x4 kw;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) kw[e] = g32_pair_f16<FMT>(g24[j], e, d2, m2);
+                        a[j] = __builtin_bit_cast(AT, kw);
+                    }
                 }
                 // V of tokens 4*grp + i, dims 8*r16 .. +7: block r16 / 4, values 8 (r16 % 4) ..
 #pragma unroll
