@@ -1195,18 +1195,32 @@ paged_decode_kernel(DecodeParams p) {
                 // GGUF blocks: lane group grp owns block grp (dims 32*grp .. +31)
                 constexpr int BE = FMT == FMT_Q8_0 ? 34 : 18;
                 const uint8_t* kb = ke + BE * grp;
-                const uint32_t d16 = lds16(kb);
-                const f16x2 d2 = __builtin_bit_cast(f16x2, d16 | (d16 << 16));
+                // the block (2-byte aligned) read as 4-byte words from its
+                // 4-byte floor and realigned: c[] = the code bytes (the read
+                // ends at most 2 bytes past the block, inside the buffer)
+                constexpr int NC = FMT == FMT_Q8_0 ? 8 : 4;  // code dwords
+                const bool off2 = ((uint32_t)(uintptr_t)kb & 2u) != 0u;
+                const uint32_t* kw4 = reinterpret_cast<const uint32_t*>(kb - (off2 ? 2 : 0));
+                uint32_t av[NC + 1], c[NC];
+#pragma unroll
+                for (int i = 0; i <= NC; ++i) av[i] = kw4[i];
+#pragma unroll
+                for (int i = 0; i < NC; ++i) c[i] = off2 ? av[i + 1] : __builtin_amdgcn_alignbyte(av[i + 1], av[i], 2);
+                const uint32_t d16 = off2 ? av[0] >> 16 : av[0] & 0xffffu;
+                const f16x2 d2 = __builtin_bit_cast(f16x2, d16 * 0x10001u);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     u32x4 kw;
 #pragma unroll
-                    for (int e = 0; e < 8; e += 2) {
-                        const int jj = 8 * j + e;  // index inside the 32-block
+                    for (int e = 0; e < 4; ++e) {
                         if constexpr (FMT == FMT_Q8_0) {
-                            kw[e / 2] = q8_pair_f16(lds16(kb + 2 + jj), d2);
+                            // values 8j + 2e, +1: bytes of dword 2j + e/2
+                            const uint32_t w = c[2 * j + (e >> 1)];
+                            kw[e] = q8_pair_f16((e & 1) ? w >> 16 : w, d2);
                         } else {
-                            kw[e / 2] = q4_pair_f16(lds16(kb + 2 + (jj & 15)), jj < 16 ? 0 : 4, d2);
+                            // byte i = value i | value i + 16 << 4
+                            const uint32_t w = c[2 * (j & 1) + (e >> 1)];
+                            kw[e] = q4_pair_f16((e & 1) ? w >> 16 : w, j >= 2 ? 4 : 0, d2);
                         }
                     }
                     a[j] = __builtin_bit_cast(AT, kw);
