@@ -15,7 +15,7 @@ Also measured in the same run (extra fields of the same line):
     format, turboquant_3bit_g32 (random-sign Walsh-Hadamard, 3-bit codes and
     a 16-bit scale per 32 values, 112-byte slots);
   * decode_other_configs: the attention operator on batch 32 x 8192 with
-    4-bit TurboQuant, and on batch 16 (lengths in [512, 4096]) with q8_0
+    4-bit TurboQuant and with its per-32-group 4-bit variant, and on batch 16 (lengths in [512, 4096]) with q8_0
     K/V pages -> GB/s;
   * causal prefill: batch 4 x 4096 tokens, 32/8 heads, bf16, fused q8_0
     quantize-on-append into the paged cache -> TFLOP/s;
@@ -158,10 +158,12 @@ def bench_decode(args, torch, capi, dev, method="turboquant_3bit_nc", sign_seed=
 def bench_decode_cfg(args, torch, capi, dev, kind):
     """The other two decode configurations, attention operator only:
     "tq4_32x8192": batch 32 x 8192 tokens, 32/8 heads, turboquant_4bit_nc
-    (134 B slots), seed 2; "q8_0_batch16": batch 16, lengths uniform in
+    (134 B slots), seed 2; "g32_4bit_32x8192": the same batch with the
+    configuration text's 4-bit per-32-group variant (160 B slots, signs
+    seed 2); "q8_0_batch16": batch 16, lengths uniform in
     [512, 4096] (seed 1), 32/8 heads, q8_0 K and V pages (136 B per
     token-head each).  Pools replicated to >= 2 GiB and rotated."""
-    if kind == "tq4_32x8192":
+    if kind in ("tq4_32x8192", "g32_4bit_32x8192"):
         seed, B, Hq, Hkv = 2, 32, 32, 8
         lens = np.full(B, 8192, np.int32)
     else:
@@ -181,9 +183,10 @@ def bench_decode_cfg(args, torch, capi, dev, kind):
     slots = torch.from_numpy(slots_for(bt, lens, (b_all, p_all))).to(dev)
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
-    tq = kind == "tq4_32x8192"
+    tq = kind in ("tq4_32x8192", "g32_4bit_32x8192")
     if tq:
-        cfg = capi.tq_config(D, "turboquant_4bit_nc")
+        cfg = (capi.tq_config(D, "turboquant_4bit_nc") if kind == "tq4_32x8192"
+               else capi.tq_config(D, "turboquant_4bit_g32", sign_seed=2))
         entry = cfg.slot_size_aligned
         pool_bytes = nblk * BS * Hkv * entry
     else:
@@ -446,7 +449,7 @@ def main():
         del v
         torch.cuda.empty_cache()
     others = [] if args.skip_variant else [bench_decode_cfg(args, torch, capi, dev, k)
-                                           for k in ("tq4_32x8192", "q8_0_batch16")]
+                                           for k in ("tq4_32x8192", "g32_4bit_32x8192", "q8_0_batch16")]
     pre = None if args.skip_prefill else bench_prefill(args, torch, capi, dev)
     fused = None if args.skip_prefill else bench_fused_norm_rope(args, torch, capi, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline(dec, torch)

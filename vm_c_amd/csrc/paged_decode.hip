@@ -1184,12 +1184,30 @@ paged_decode_kernel(DecodeParams p) {
                 for (int i2 = 0; i2 < 4; ++i2) {
                     const bool ok = 4 * grp + i2 < nv;
                     const uint8_t* vb = vpage + v_off[i2] + BE * (r16 >> 2);
-                    const uint32_t dv16 = lds16(vb), mv16 = FMT == FMT_G4 ? lds16(vb + 2) : 0u;
-                    const f16x2 dv2 = __builtin_bit_cast(f16x2, dv16 | (dv16 << 16));
-                    const f16x2 mv2 = __builtin_bit_cast(f16x2, mv16 | (mv16 << 16));
-                    const uint32_t cw = g32_codes8<FMT>(vb, r16 & 3);
+                    if constexpr (FMT == FMT_G4) {
+                        // 20-byte block, 4-byte aligned: d | m, then the 8 code
+                        // bytes of values 8l .. 8l+7 (l = r16 % 4) as two words
+                        const int l = r16 & 3;
+                        const uint32_t dm = lds32(vb);
+                        const uint32_t q0 = lds32(vb + 4 + 8 * (l & 1)), q1 = lds32(vb + 8 + 8 * (l & 1));
+                        const f16x2 dv2 = __builtin_bit_cast(f16x2, (dm & 0xffffu) * 0x10001u);
+                        const f16x2 mv2 = __builtin_bit_cast(f16x2, (dm >> 16) * 0x10001u);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) vw[i2][e] = ok ? g32_pair_f16<FMT>(cw, e, dv2, mv2) : 0u;
+                        for (int e = 0; e < 4; ++e) {
+                            const uint32_t w = (e >> 1) ? q1 : q0;
+                            const uint32_t sp = __builtin_amdgcn_perm(0u, w, (e & 1) ? 0x0c030c02u : 0x0c010c00u);
+                            const uint32_t z = ((sp >> (l >= 2 ? 4 : 0)) & 0x000f000fu) | 0x64006400u;
+                            const f16x2 c = __builtin_bit_cast(f16x2, z) - f16x2{(_Float16)1024.0f, (_Float16)1024.0f};
+                            vw[i2][e] = ok ? __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c, dv2, mv2)) : 0u;
+                        }
+                    } else {
+                        const uint32_t dv16 = lds16(vb);
+                        const f16x2 dv2 = __builtin_bit_cast(f16x2, dv16 | (dv16 << 16));
+                        const f16x2 mv2 = {};
+                        const uint32_t cw = g32_codes8<FMT>(vb, r16 & 3);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) vw[i2][e] = ok ? g32_pair_f16<FMT>(cw, e, dv2, mv2) : 0u;
+                    }
                 }
             } else {
                 // GGUF blocks: lane group grp owns block grp (dims 32*grp .. +31)
