@@ -161,34 +161,36 @@ __device__ __forceinline__ void unpack8(const u32x4 w, float* x) {
 // token); groups 0 .. T*Hkv/R-1 are the K rows (norm, RoPE, append of K and
 // V), the rest the Q rows; 16 groups per 256-thread workgroup.  Every load of
 // the group's rows is issued before the first row is processed.
-template <bool BF16, int ST, int KB, int VB, int R>
+template <bool BF16, int ST, int KB, int VB, int R, int RQ>
 __global__ void __launch_bounds__(256)
 fused_norm_rope_kernel(FusedParams p) {
     __shared__ __attribute__((aligned(16))) float sq[16][128];  // TurboQuant norm chain, per group
     const int lane = threadIdx.x & 63, j = lane & 15;
     const int gi = threadIdx.x >> 4;
     const int64_t nk = (int64_t)p.T * (p.Hkv / R);
-    const int64_t ng = nk + (int64_t)p.T * (p.Hq / R);
+    const int64_t ng = nk + (int64_t)p.T * (p.Hq / RQ);
     const int64_t g0 = (int64_t)blockIdx.x * 16 + gi;
     const bool live = g0 < ng;
     const int64_t g = live ? g0 : 0;  // dead groups repeat row 0 without writing
     const bool is_k = g < nk;
     const int H = is_k ? p.Hkv : p.Hq;
-    const int64_t r0 = (is_k ? g : g - nk) * R;  // row t*H + h0
+    const int nr = is_k ? R : RQ;  // rows of this group
+    const int64_t r0 = is_k ? g * R : (g - nk) * RQ;  // row t*H + h0
     const int64_t t = r0 / H;
     const int h0 = (int)(r0 % H);
     uint16_t* rows = (is_k ? p.k : p.q) + r0 * 128;
     const uint16_t* w = is_k ? p.kw : p.qw;
 
     // ---- loads
-    u32x4 xr[R], wr_[R], vr[R];
+    u32x4 xr[RQ], wr_[RQ], vr[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) xr[r] = *reinterpret_cast<const u32x4*>(rows + r * 128 + 8 * j);
+    for (int r = 0; r < RQ; ++r)
+        if (r < nr) xr[r] = *reinterpret_cast<const u32x4*>(rows + r * 128 + 8 * j);
     if constexpr (ST != ST_NONE) {
         if (is_k) {
 #pragma unroll
             for (int r = 0; r < R; ++r)
-                vr[r] = *reinterpret_cast<const u32x4*>(p.v + (r0 + r) * 128 + 8 * j);
+                vr[r & (R - 1)] = *reinterpret_cast<const u32x4*>(p.v + (r0 + r) * 128 + 8 * j);
         }
     }
     const uint16_t* cs = p.cs + p.pos[t] * 128;
@@ -211,8 +213,8 @@ fused_norm_rope_kernel(FusedParams p) {
     }
     if (w) {  // the same in the whole group
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            wr_[r] = *reinterpret_cast<const u32x4*>(w + (int64_t)(h0 + r) * 128 + 8 * j);
+        for (int r = 0; r < RQ; ++r)
+            if (r < nr) wr_[r] = *reinterpret_cast<const u32x4*>(w + (int64_t)(h0 + r) * 128 + 8 * j);
     }
     int64_t slot = -1;
     if constexpr (ST != ST_NONE) {
@@ -220,7 +222,8 @@ fused_norm_rope_kernel(FusedParams p) {
     }
 
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
+    for (int r = 0; r < RQ; ++r) {
+        if (r >= nr) break;  // K groups: R rows (r < R below)
         const int h = h0 + r;
         float x[8];
         unpack8<BF16>(xr[r], x);
@@ -272,7 +275,7 @@ fused_norm_rope_kernel(FusedParams p) {
                 const bool wr = slot >= 0;
                 float vv[8];
                 if constexpr (ST == ST_TQ || ST == ST_G32 || ST == ST_K8) {
-                    unpack8<BF16>(vr[r], vv);
+                    unpack8<BF16>(vr[r & (R - 1)], vv);
                     const int64_t blk = slot / p.bs, off = slot % p.bs;
                     uint8_t* sp = p.kc + blk * p.bs * p.Hkv * p.SA + off * p.Hkv * p.SA + (int64_t)h * p.SA;
                     if constexpr (ST == ST_K8) {
@@ -292,9 +295,9 @@ fused_norm_rope_kernel(FusedParams p) {
                     const int64_t eo = kv_entry_offset(wr ? slot : 0, h, p.bs, p.Hkv, p.E, p.stride, p.hnd != 0);
                     if constexpr (ST == ST_F16 || ST == ST_BF16) {
                         constexpr bool DB = ST == ST_BF16;
-                        u32x4 vw = vr[r], kw = yw;
+                        u32x4 vw = vr[r & (R - 1)], kw = yw;
                         if constexpr (DB != BF16) {
-                            unpack8<BF16>(vr[r], vv);
+                            unpack8<BF16>(vr[r & (R - 1)], vv);
                             vw = pack8<DB>(vv);
                             kw = pack8<DB>(y);
                         }
@@ -303,7 +306,7 @@ fused_norm_rope_kernel(FusedParams p) {
                             *reinterpret_cast<u32x4*>(p.vc + eo + 16 * j) = vw;
                         }
                     } else {
-                        unpack8<BF16>(vr[r], vv);
+                        unpack8<BF16>(vr[r & (R - 1)], vv);
                         gguf_block4<ST>(y, j, p.kc + eo, wr);
                         gguf_block4<ST>(vv, j, p.vc + eo, wr);
                     }
@@ -313,25 +316,27 @@ fused_norm_rope_kernel(FusedParams p) {
     }
 }
 
-template <bool BF16, int ST, int KB, int VB, int R>
+template <bool BF16, int ST, int KB, int VB, int R, int RQ>
 int launch_r(const FusedParams& prm, hipStream_t s) {
-    const int64_t ng = (int64_t)prm.T * (prm.Hq / R + prm.Hkv / R);
+    const int64_t ng = (int64_t)prm.T * (prm.Hq / RQ + prm.Hkv / R);
     const int64_t grid = (ng + 15) / 16;
     if (grid > 0x7fffffff) return VMC_EINVAL;
     if (grid == 0) return VMC_OK;
-    hipLaunchKernelGGL((fused_norm_rope_kernel<BF16, ST, KB, VB, R>), dim3((unsigned)grid), dim3(256), 0, s,
+    hipLaunchKernelGGL((fused_norm_rope_kernel<BF16, ST, KB, VB, R, RQ>), dim3((unsigned)grid), dim3(256), 0, s,
                        prm);
     VMC_LAUNCH_CHECK();
     return VMC_OK;
 }
 
-// rows per group: 4 when both head counts allow it (four 16-byte loads in
-// flight per lane), else 2, else 1
+// rows per group: Q groups 4 when Hq allows it (four 16-byte loads in flight
+// per lane); K groups, which also append (more registers), 2 -- fewer
+// registers for the whole kernel, so more waves for the Q rows -- or 4 when
+// there is no append; else 2, else 1
 template <bool BF16, int ST, int KB = 0, int VB = 0>
 int launch_fused(const FusedParams& prm, hipStream_t s) {
-    if (prm.Hq % 4 == 0 && prm.Hkv % 4 == 0) return launch_r<BF16, ST, KB, VB, 4>(prm, s);
-    if (prm.Hq % 2 == 0 && prm.Hkv % 2 == 0) return launch_r<BF16, ST, KB, VB, 2>(prm, s);
-    return launch_r<BF16, ST, KB, VB, 1>(prm, s);
+    if (prm.Hq % 4 == 0 && prm.Hkv % 2 == 0) return launch_r<BF16, ST, KB, VB, ST == ST_NONE ? 4 : 2, 4>(prm, s);
+    if (prm.Hq % 2 == 0 && prm.Hkv % 2 == 0) return launch_r<BF16, ST, KB, VB, 2, 2>(prm, s);
+    return launch_r<BF16, ST, KB, VB, 1, 1>(prm, s);
 }
 
 template <bool BF16>
