@@ -3,6 +3,7 @@
 // TurboQuantBackend operators, checked against the oracle (oracle/vmc_oracle.h):
 // appended bytes bit-exact, attention within |d| <= 2e-3 + 1e-2 |ref|.
 // Built by __graft_entry__.build(); run by tests/test_gpu_host_cpp.py.
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -356,6 +357,74 @@ static void test_fused_norm_rope(const std::string& dtype) {
     CHECK(dk.get() == rk);
 }
 
+// page movement on HIP memory: a request's q8_0 pages swapped out to the CPU
+// pool and back (device copies clobbered meanwhile, other requests take the
+// blocks), and swap_blocks between device pools and to pinned host memory;
+// every byte compared
+static void test_page_movement() {
+    std::printf("case: page movement (swap_request_slots / swap_blocks)\n");
+    std::fflush(stdout);
+    CacheConfig cc;
+    cc.kv_cache_dtype = "q8_0";
+    KVCacheManager m(cc, ModelConfig{}, 2, Hkv, D);
+    m.allocate_gpu_blocks_for_group(0, 6);
+    m.allocate_cpu_blocks_for_group(0, 4);
+    auto ids = [&](const std::string& r) {
+        std::vector<int64_t> v;
+        for (const auto& sl : m.request_slots().at(r))
+            if (v.empty() || v.back() != sl.block_id) v.push_back(sl.block_id);
+        return v;
+    };
+    m.allocate_slots("r", 32);
+    const std::vector<int64_t> s = ids("r");
+    CHECK(s.size() == 2);
+    const size_t bb = m.group(0).bytes_per_block;
+    auto fill = [&](int l, int64_t b, bool key) { return (int)((key ? 10 : 50) + 7 * l + b); };
+    for (int l = 0; l < 2; ++l)
+        for (int64_t b : s) {
+            HIP_CHECK(hipMemset(static_cast<uint8_t*>(m.key_cache_ptr(l)) + b * bb, fill(l, b, true), bb));
+            HIP_CHECK(hipMemset(static_cast<uint8_t*>(m.value_cache_ptr(l)) + b * bb, fill(l, b, false), bb));
+        }
+    HIP_CHECK(hipDeviceSynchronize());
+    m.swap_request_slots("r");
+    CHECK(m.num_free_cpu_blocks() == 2);
+    for (int l = 0; l < 2; ++l)
+        for (int64_t b : s) HIP_CHECK(hipMemset(static_cast<uint8_t*>(m.key_cache_ptr(l)) + b * bb, 0xEE, bb));
+    m.allocate_slots("other", 32);
+    m.swap_back_request_slots("r");
+    HIP_CHECK(hipDeviceSynchronize());
+    const std::vector<int64_t> now = ids("r");
+    CHECK(now.size() == 2 && m.num_free_cpu_blocks() == 4);
+    for (int l = 0; l < 2 && now.size() == 2; ++l)
+        for (size_t i = 0; i < now.size(); ++i) {
+            const auto k = pool_bytes(static_cast<uint8_t*>(m.key_cache_ptr(l)) + now[i] * bb, bb);
+            const auto v = pool_bytes(static_cast<uint8_t*>(m.value_cache_ptr(l)) + now[i] * bb, bb);
+            CHECK(k == std::vector<uint8_t>(bb, (uint8_t)fill(l, s[i], true)));
+            CHECK(v == std::vector<uint8_t>(bb, (uint8_t)fill(l, s[i], false)));
+        }
+    // swap_blocks: device pool -> device pool and -> pinned host, (src, dst) pairs
+    const int64_t nb = 4;
+    Dev<uint8_t> a((size_t)nb * bb), c((size_t)nb * bb);
+    std::vector<uint8_t> ha((size_t)nb * bb);
+    for (size_t i = 0; i < ha.size(); ++i) ha[i] = (uint8_t)(i * 131 + 7);
+    a.put(ha);
+    HIP_CHECK(hipMemset(c.p, 0, (size_t)nb * bb));
+    const int64_t map[4] = {1, 3, 2, 0};  // block 1 -> 3, block 2 -> 0
+    swap_blocks(a.p, c.p, (int64_t)bb, map, 2, 0, 0, nullptr);
+    uint8_t* host = nullptr;
+    HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&host), (size_t)nb * bb, 0));
+    std::memset(host, 0, (size_t)nb * bb);
+    const int64_t map2[2] = {3, 1};
+    swap_blocks(a.p, host, (int64_t)bb, map2, 1, 0, -1, nullptr);
+    HIP_CHECK(hipDeviceSynchronize());
+    const auto hc = c.get();
+    CHECK(std::memcmp(hc.data() + 3 * bb, ha.data() + 1 * bb, bb) == 0);
+    CHECK(std::memcmp(hc.data() + 0 * bb, ha.data() + 2 * bb, bb) == 0);
+    CHECK(std::all_of(hc.begin() + bb, hc.begin() + 3 * bb, [](uint8_t x) { return x == 0; }));
+    CHECK(std::memcmp(host + 1 * bb, ha.data() + 3 * bb, bb) == 0);
+    HIP_CHECK(hipHostFree(host));
+}
+
 int main() {
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || n < 1) {
@@ -371,6 +440,7 @@ int main() {
         test_paged_backend("fp16", "hnd");
         test_fused_norm_rope("q4_0");
         test_fused_norm_rope("auto");
+        test_page_movement();
     } catch (const std::exception& e) {
         std::printf("FAIL exception: %s\n", e.what());
         return 1;
