@@ -8,7 +8,7 @@
  * with its default --fmad=true, so the places where nvcc contracted are
  * written as explicit fmaf() and cited.
  *
- * Parity status per function is recorded in vmc_oracle.h and DESIGN.md.
+ * Parity status per function is recorded beside its declaration in vmc_oracle.h.
  */
 #include "vmc_oracle.h"
 
