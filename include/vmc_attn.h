@@ -213,7 +213,10 @@ int vmc_fused_qk_norm_rope_store(void* q_buf, void* k_buf, const void* v_buf,
  * reconstructed from centroids (norm-corrected, times the stored norm), V =
  * code*scale + zero, fp32 online softmax, LSE merge.  The caller provides the
  * workspace (the reference grew it inside the call); max_num_kv_splits and
- * limits as for vmc_paged_attention_decode; half_dtype must be VMC_DTYPE_F16.
+ * limits as for vmc_paged_attention_decode.  half_dtype (VMC_DTYPE_F16 or
+ * VMC_DTYPE_BF16) is the dtype of query, output and the stored norms, scales
+ * and zeros (the reference dispatches on its compute dtype,
+ * turboquant_kernels.cu:966; the per-32-group and fp8-key layouts take fp16).
  */
 size_t vmc_turboquant_decode_workspace_size(int batch_size, int num_heads, int num_kv_heads,
                                             int head_dim, int64_t max_num_blocks_per_req,

@@ -206,6 +206,86 @@ static void test_turboquant_backend(const char* method) {
 }
 
 // append + decode of GGUF pages through PagedAttentionBackend
+// bf16 activations through TurboQuantBackend: store_kv writes bf16 norms,
+// scales and zeros (the backend's activation dtype), forward_decode reads bf16
+// q and writes bf16 rows; a query dtype other than the backend's throws.
+static void test_turboquant_backend_bf16(const char* method) {
+    std::printf("case: TurboQuantBackend %s bf16\n", method);
+    std::fflush(stdout);
+    CacheConfig cc;
+    cc.kv_cache_quant_method = method;
+    KVCacheManager mgr(cc, ModelConfig{}, 1, Hkv, D);
+    mgr.allocate_gpu_blocks_for_group(0, 64);
+    TurboQuantBackend be(D, method, Hq, Hkv, 0, ScalarType::BFLOAT16);
+    be.ensure_workspace(512, 8, Hq, Hkv, D, 0);
+    const size_t ws = be.workspace_size();
+    const std::vector<int> lens = {40, 17, 300};
+    std::vector<ScheduledRequest> pre(lens.size());
+    for (size_t i = 0; i < lens.size(); ++i) {
+        pre[i].request_id = "r" + std::to_string(i);
+        pre[i].num_scheduled_tokens = lens[i] + 1;
+        pre[i].is_prefill = true;
+    }
+    HostBatchMetadata hp = build_batch_metadata(mgr, pre);
+    CHECK(hp.ok);
+    const int T = hp.num_tokens;
+    std::vector<uint16_t> K((size_t)T * Hkv * D), V(K.size()), Q((size_t)lens.size() * Hq * D);
+    orc_randn_bf16(K.data(), (int64_t)K.size(), 9, 1);
+    orc_randn_bf16(V.data(), (int64_t)V.size(), 9, 2);
+    orc_randn_bf16(Q.data(), (int64_t)Q.size(), 9, 3);
+    Dev<uint16_t> dK(K), dV(V), dQ(Q), dO(Q.size());
+    DeviceBatchMetadata dm(8, 512, 64);
+    AttentionMetadata mp = dm.upload(hp, BS, nullptr);
+    void* pool = mgr.key_cache_ptr(0);
+    const size_t pool_n = (size_t)64 * mgr.group(0).bytes_per_block;
+    HIP_CHECK(hipMemset(pool, 0, pool_n));
+    be.store_kv(dK.p, dV.p, pool, nullptr, mp.slot_mapping, T, Hkv, D, BS, 0, nullptr);
+    HIP_CHECK(hipDeviceSynchronize());
+    orc_tq_layout L;
+    std::vector<float> C(16), M(15);
+    CHECK(orc_tq_layout_from_method(D, method, &L) == 0);
+    orc_tq_lloyd_max(C.data(), D, L.key_quant_bits);
+    orc_tq_midpoints(C.data(), L.n_centroids, M.data());
+    std::vector<uint8_t> ref(pool_n, 0);
+    orc_tq_store(K.data(), V.data(), ref.data(), hp.slot_mapping.data(), T, Hkv, D, BS, &L, M.data(), 1);
+    const std::vector<uint8_t> got = pool_bytes(pool, pool_n);
+    CHECK(got == ref);
+    // decode over the stored contexts (the last stored token is each
+    // request's current one)
+    std::vector<ScheduledRequest> dec(lens.size());
+    for (size_t i = 0; i < lens.size(); ++i) {
+        dec[i].request_id = "r" + std::to_string(i);
+        dec[i].num_computed_tokens = lens[i];
+    }
+    HostBatchMetadata hd = build_batch_metadata(mgr, dec);
+    CHECK(hd.ok && hd.num_reqs == (int)lens.size());
+    AttentionMetadata md = dm.upload(hd, BS, nullptr);
+    const float scale = 1.0f / std::sqrt((float)D);
+    be.forward_decode(dO.p, dQ.p, pool, nullptr, md, Hq, Hkv, D, scale, BS, ScalarType::BFLOAT16, nullptr);
+    HIP_CHECK(hipDeviceSynchronize());
+    CHECK(be.workspace_size() == ws);  // pre-sized: the decode call allocated nothing
+    std::vector<double> exd((size_t)hd.num_reqs * Hq * D);
+    orc_tq_decode_exact(exd.data(), Q.data(), ref.data(), hd.block_tables.data(), hd.seq_lens.data(),
+                        hd.num_reqs, Hq, Hkv, D, scale, BS, hd.max_num_blocks_per_req, &L, C.data(), 1, 0);
+    const std::vector<uint16_t> o = dO.get();
+    double err = 0;
+    bool ok = true;
+    for (size_t i = 0; i < exd.size(); ++i) {
+        const double e = std::fabs((double)orc_bf16_to_f32(o[i]) - exd[i]);
+        err = std::max(err, e);
+        ok = ok && e <= 2e-3 + 1e-2 * std::fabs(exd[i]);
+    }
+    CHECK(ok);
+    std::printf("  bf16 decode max err %.3g\n", err);
+    bool threw = false;
+    try {
+        be.forward_decode(dO.p, dQ.p, pool, nullptr, md, Hq, Hkv, D, scale, BS, ScalarType::FLOAT16, nullptr);
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    CHECK(threw);
+}
+
 static void test_paged_backend(const std::string& dtype, const std::string& layout) {
     std::printf("case: PagedAttentionBackend %s %s\n", dtype.c_str(), layout.c_str());
     std::fflush(stdout);
@@ -435,6 +515,7 @@ int main() {
         for (const char* m : {"turboquant_3bit_nc", "turboquant_4bit_nc", "turboquant_3bit_g32",
                               "turboquant_4bit_g32", "turboquant_k8v4"})
             test_turboquant_backend(m);
+        for (const char* m : {"turboquant_3bit_nc", "turboquant_4bit_nc"}) test_turboquant_backend_bf16(m);
         test_paged_backend("q8_0", "nhd");
         test_paged_backend("q4_0", "hnd");
         test_paged_backend("fp16", "hnd");

@@ -97,3 +97,24 @@ def test_argument_validation_without_gpu():
     assert L.vmc_paged_attention_decode(C.c_void_p(16), C.c_void_p(16), C.c_void_p(16), C.c_void_p(16),
                                         C.c_void_p(16), C.c_void_p(16), 1, 8, 8, 128, 16, 4,
                                         C.c_float(0.1), 0, 0, 0, 0, C.c_void_p(16), 8, None) == capi.VMC_ENOMEM
+
+
+def test_null_and_stride_validation_without_gpu():
+    """Null buffers and too-small page strides are rejected before any launch:
+    the fp8-key TurboQuant store checks its pointers like every other method,
+    and the fused norm/RoPE append checks the page stride and the 16-byte
+    alignment of f16/bf16 pages as vmc_reshape_and_cache does."""
+    from vm_c_amd import capi
+    L = capi.load()
+    c8 = capi.tq_config(128, "turboquant_k8v4")
+    p = C.c_void_p(256)
+    for key, val, cache, slots in ((None, p, p, p), (p, None, p, p), (p, p, None, p), (p, p, p, None)):
+        assert L.vmc_turboquant_store(key, val, cache, slots, 4, 8, 128, 16, C.byref(c8), 0,
+                                      None) == capi.VMC_EINVAL
+    fused = L.vmc_fused_qk_norm_rope_store
+    args = lambda stride, fmt: (p, p, p, None, None, p, p, p, p, p, 4, 32, 8, 128, C.c_float(1e-6), 1,
+                                16, stride, fmt, 0, None, 0, None)
+    # one page of 16 tokens x 8 heads of 136-byte q8_0 entries needs 17408 bytes
+    assert fused(*args(17407, capi.KV_Q8_0)) == capi.VMC_EINVAL
+    # f16 pages are written 16 bytes at a time
+    assert fused(*args(16 * 8 * 256 + 8, capi.KV_F16)) == capi.VMC_EINVAL

@@ -152,3 +152,46 @@ def test_tq_decode(dev, method, case):
                                    num_splits=32))
     ok, err = close_report(got, ref, ATOL, RTOL)
     assert ok, f"vs reference restatement: max err {err}"
+
+
+@pytest.mark.parametrize("method", ["turboquant_4bit_nc", "turboquant_3bit_nc", "turboquant_k3v4_nc"])
+@pytest.mark.parametrize("case", ["cfg5_small", "ragged", "gqa16"])
+@pytest.mark.parametrize("max_splits", [0, 1])
+def test_tq_decode_bf16(dev, method, case, max_splits):
+    """bf16 activations: the store writes bf16 norms/scales/zeros (the
+    reference's compute-dtype dispatch, turboquant_kernels.cu:808, :966) and
+    the decode reads bf16 q and those pages and writes bf16 rows (its USE_BF16
+    stage 1, :353, :445-461).  Pool bytes bit-exact against the oracle's bf16
+    store; output against fp64 attention over the same pages and against the
+    oracle's two-stage restatement with bf16 halves."""
+    import torch
+    from kvgen import f32_to_bf16_bits
+    from vm_c_amd import capi
+    w = make_workload(seed=len(case) * 11 + max_splits, **TQ_CASES[case])
+    kb16, vb16, qb16 = (f32_to_bf16_bits(x.astype(np.float32)) for x in (w.K, w.V, w.Q))
+    L = O.tq_layout(method)
+    cfg = capi.tq_config(w.D, method)
+    cache = torch.zeros(w.num_blocks * BS * w.Hkv * cfg.slot_size_aligned, dtype=torch.uint8, device=dev)
+    as_bf16 = lambda b: torch.from_numpy(b.view(np.int16)).to(dev).view(torch.bfloat16)
+    if w.K.shape[0]:
+        capi.turboquant_store(as_bf16(kb16), as_bf16(vb16), cache, torch.from_numpy(w.slots).to(dev), BS, cfg)
+    q = as_bf16(qb16)
+    out = torch.full_like(q, float("nan"))
+    capi.turboquant_decode_attention(out, q, cache, torch.from_numpy(w.bt).to(dev),
+                                     torch.from_numpy(w.seq_lens).to(dev), w.Hkv, float(w.scale), cfg,
+                                     block_size=BS, max_splits=max_splits)
+    torch.cuda.synchronize()
+    got_cache = cache.cpu().numpy()
+    c, m = O.tq_tables(128, L.key_quant_bits)
+    ref_cache = np.zeros_like(got_cache)
+    O.tq_store(kb16, vb16, w.slots, ref_cache, BS, L, m, bf16=True)
+    assert np.array_equal(got_cache, ref_cache), "bf16 TurboQuant store bytes differ from the oracle"
+    got = out.float().cpu().numpy()
+    ex = O.tq_decode_exact(qb16, ref_cache, w.bt, w.seq_lens, w.Hkv, w.scale, BS, L, c, bf16=True)
+    ok, err = close_report(got, ex, ATOL, RTOL)
+    assert ok, f"vs exact: max err {err}"
+    ref = O.tq_decode(qb16, ref_cache, w.bt, w.seq_lens, w.Hkv, np.float32(w.scale), BS, L, c,
+                      num_splits=32, bf16=True)
+    ref = (ref.astype(np.uint32) << 16).view(np.float32)
+    ok, err = close_report(got, ref, ATOL, RTOL)
+    assert ok, f"vs reference restatement: max err {err}"

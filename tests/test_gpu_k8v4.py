@@ -6,7 +6,10 @@ src/cuda/turboquant_kernels.cu:47-143, :188-245, :407-415):
   skipped slots and untouched bytes;
 * decode: against the oracle's float64 attention over the same pages (keys
   decoded from fp8, q not rotated, no norm), ragged lengths, GQA 2..16, both
-  split modes;
+  split modes.  This pins the intended fp8-key semantics, not the
+  reference's output: its stage 1 also multiplies each fp8 key by the fp16
+  it reads at +mse_bytes (turboquant_kernels.cu:443-450), which in the k8v4
+  slot is the first two V code bytes, not a norm;
 * the fused norm + RoPE + append writing k8v4 slots.
 Tolerance: |got - ref| <= 2e-3 + 1e-2 |ref|.
 """

@@ -421,6 +421,11 @@ extern "C" int vmc_fused_qk_norm_rope_store(void* q_buf, void* k_buf, const void
             prm.vc = reinterpret_cast<uint8_t*>(value_cache);
             prm.E = E;
             prm.stride = cache_stride > 0 ? cache_stride : block_size * num_kv_heads * E;
+            // a page must hold block_size * num_kv_heads entries, and f16/bf16
+            // pages are written with 16-byte stores
+            if (prm.stride < block_size * num_kv_heads * E) return VMC_EINVAL;
+            if ((kv_format == VMC_KV_F16 || kv_format == VMC_KV_BF16) && (prm.stride % 16) != 0)
+                return VMC_EINVAL;
             prm.hnd = layout == VMC_LAYOUT_HND;
             st = kv_format == VMC_KV_F16 ? ST_F16 : kv_format == VMC_KV_BF16 ? ST_BF16
                : kv_format == VMC_KV_Q8_0 ? ST_Q8_0 : ST_Q4_0;

@@ -402,8 +402,13 @@ struct alignas(16) DecodeLds {
 template <int FMT, int KB, int VB, bool MBF16, bool HALF>
 __global__ void __launch_bounds__(512)
 paged_decode_kernel(DecodeParams p) {
-    using AT = typename std::conditional<MBF16, bf16x8, f16x8>::type;
-    using PT = typename std::conditional<MBF16, s16x4, f16x4>::type;
+    // TurboQuant: MBF16 says that q, out and the stored norms, scales and
+    // zeros are bf16 (the reference's USE_BF16 instantiation,
+    // turboquant_kernels.cu:353, :445-461); its MFMA operands stay fp16
+    // (centroids and exact codes)
+    constexpr bool kTqBf16 = FMT == FMT_TQ && MBF16;
+    using AT = typename std::conditional<MBF16 && FMT != FMT_TQ, bf16x8, f16x8>::type;
+    using PT = typename std::conditional<MBF16 && FMT != FMT_TQ, s16x4, f16x4>::type;
     __shared__ DecodeLds<FMT, KB, VB> lds;
     uint8_t* const smem = lds.ring;
     WGPlan& plan = lds.plan;
@@ -871,7 +876,7 @@ paged_decode_kernel(DecodeParams p) {
             for (int j = 0; j < 4; ++j) gram = mfma16x16x32(a[pp][j], a[pp][j], gram);
             const float csq = sel_bits(sel_bits(gram[0], gram[1], odd_mask), sel_bits(gram[2], gram[3], odd_mask),
                                        hi_mask);
-            const float nrm = f16_bits_to_f32((uint16_t)lds16(ke + GE::mse));
+            const float nrm = half_to_f32<kTqBf16>((uint16_t)lds16(ke + GE::mse));
             rowf[pp] = p.scale_log2 * nrm * __builtin_amdgcn_rsqf(csq + 1e-16f);
             // V: the four bytes around token 4*grp + i's code run, its scale
             // and zero
@@ -988,8 +993,8 @@ paged_decode_kernel(DecodeParams p) {
         for (int i2 = 0; i2 < 4; ++i2) {
             const float pv = __builtin_amdgcn_exp2f(sv[i2] - m_use);
             psum += pv;
-            zsum = __builtin_fmaf(pv, (float)__builtin_bit_cast(_Float16, hz[i2]), zsum);
-            pw[i2] = (_Float16)__builtin_fmaf(pv, (float)__builtin_bit_cast(_Float16, hs[i2]), 0.0f);
+            zsum = __builtin_fmaf(pv, half_to_f32<kTqBf16>(hz[i2]), zsum);
+            pw[i2] = (_Float16)__builtin_fmaf(pv, half_to_f32<kTqBf16>(hs[i2]), 0.0f);
         }
         l_part += psum;
         z_part += zsum;
@@ -1062,8 +1067,8 @@ paged_decode_kernel(DecodeParams p) {
 #pragma unroll
             for (int i2 = 0; i2 < 4; ++i2) {
                 const float pv = __builtin_amdgcn_exp2f(sv[pp][i2] - m_use);
-                const float sc = (float)__builtin_bit_cast(_Float16, vsc[pp][i2]);
-                const float zr = (float)__builtin_bit_cast(_Float16, vzr[pp][i2]);
+                const float sc = half_to_f32<kTqBf16>(vsc[pp][i2]);
+                const float zr = half_to_f32<kTqBf16>(vzr[pp][i2]);
                 psum += pv;
                 zsum = __builtin_fmaf(pv, zr, zsum);
                 pa[4 * pp + i2] = (_Float16)__builtin_fmaf(pv, sc, 0.0f);
@@ -1797,6 +1802,17 @@ extern "C" int vmc_paged_attention_prefill(void* out, const void* query, const v
 }
 
 namespace {
+template <bool BF>
+int launch_tq(DecodeParams& prm, int kb, int vb, bool half, hipStream_t s) {
+    if (kb == 4 && vb == 4)
+        return half ? launch_decode<FMT_TQ, 4, 4, BF, true>(prm, s) : launch_decode<FMT_TQ, 4, 4, BF>(prm, s);
+    if (kb == 3 && vb == 3)
+        return half ? launch_decode<FMT_TQ, 3, 3, BF, true>(prm, s) : launch_decode<FMT_TQ, 3, 3, BF>(prm, s);
+    if (kb == 3 && vb == 4)
+        return half ? launch_decode<FMT_TQ, 3, 4, BF, true>(prm, s) : launch_decode<FMT_TQ, 3, 4, BF>(prm, s);
+    return VMC_EINVAL;
+}
+
 int tq_decode_rows(void* output, const void* query, const void* kv_cache, const int32_t* block_tables,
                    const int32_t* seq_lens, const int32_t* row_seq, const int32_t* row_pos, int batch_size,
                    int num_heads, int num_kv_heads, int head_dim, float scale, int64_t block_size,
@@ -1860,11 +1876,11 @@ int tq_decode_rows(void* output, const void* query, const void* kv_cache, const 
     prm.row_pos = row_pos;
     if (batch_size == 0) return VMC_OK;
     if (!kv_cache) return VMC_EINVAL;
-    // stored norm/scale/zero are half_dtype; the kernel reads them as fp16
-    if (half_dtype != VMC_DTYPE_F16) return VMC_EINVAL;
+    // q, out and the stored norm/scale/zero are half_dtype
+    const bool bf = half_dtype == VMC_DTYPE_BF16;
     prm.kc = reinterpret_cast<const uint8_t*>(kv_cache);
     prm.vc = prm.kc;
-    prm.q_bf16 = 0;
+    prm.q_bf16 = bf ? 1 : 0;
     prm.entry_bytes = cfg->slot_size_aligned;
     prm.page_bytes = (int64_t)kBs * num_kv_heads * cfg->slot_size_aligned;
     prm.hnd = 0;
@@ -1877,13 +1893,7 @@ int tq_decode_rows(void* output, const void* query, const void* kv_cache, const 
     const int kb = cfg->key_quant_bits, vb = cfg->value_quant_bits;
     // at most 8 query heads per KV head: two pages share the S tile's columns
     const bool half = prm.G <= 8;
-    if (kb == 4 && vb == 4)
-        return half ? launch_decode<FMT_TQ, 4, 4, false, true>(prm, s) : launch_decode<FMT_TQ, 4, 4, false>(prm, s);
-    if (kb == 3 && vb == 3)
-        return half ? launch_decode<FMT_TQ, 3, 3, false, true>(prm, s) : launch_decode<FMT_TQ, 3, 3, false>(prm, s);
-    if (kb == 3 && vb == 4)
-        return half ? launch_decode<FMT_TQ, 3, 4, false, true>(prm, s) : launch_decode<FMT_TQ, 3, 4, false>(prm, s);
-    return VMC_EINVAL;
+    return bf ? launch_tq<true>(prm, kb, vb, half, s) : launch_tq<false>(prm, kb, vb, half, s);
 }
 }  // namespace
 

@@ -153,6 +153,7 @@ extern "C" int vmc_turboquant_store(const void* key, const void* value, void* kv
     if (num_tokens < 0 || num_kv_heads <= 0 || block_size <= 0) return VMC_EINVAL;
     if (half_dtype != VMC_DTYPE_F16 && half_dtype != VMC_DTYPE_BF16) return VMC_EINVAL;
     if (num_tokens == 0) return VMC_OK;
+    if (!key || !value || !kv_cache || !slot_mapping) return VMC_EINVAL;
     if (cfg->key_fp8) {
         const int64_t grid = ((int64_t)num_tokens * num_kv_heads + 15) / 16;
         if (grid > 0x7fffffff) return VMC_EINVAL;
@@ -168,7 +169,6 @@ extern "C" int vmc_turboquant_store(const void* key, const void* value, void* kv
         VMC_LAUNCH_CHECK();
         return VMC_OK;
     }
-    if (!key || !value || !kv_cache || !slot_mapping) return VMC_EINVAL;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const bool bf = half_dtype == VMC_DTYPE_BF16;
     if (cfg->group_size != 0)

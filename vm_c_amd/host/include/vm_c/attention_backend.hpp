@@ -5,8 +5,10 @@
 // quantized on append) in "nhd" or "hnd" layout.  TurboQuantBackend: packed
 // rotated low-bit slots (value_cache is null).  forward_decode uses
 // meta.num_reqs query rows (one token per request).  forward_prefill runs the
-// causal prefill over this step's contiguous K/V; a prefix already in the
-// cache (meta.num_computed_tokens > 0) is outside this path and throws.
+// causal prefill over this step's contiguous K/V when nothing is cached yet;
+// with a cached prefix (meta.num_computed_tokens > 0) every step token attends
+// its sequence's positions 0 .. its own through the block table (the step's
+// K/V are stored first).
 #pragma once
 
 #include <cstddef>
@@ -85,8 +87,12 @@ private:
 
 class TurboQuantBackend : public AttentionBackend {
 public:
+    // activation_dtype (no counterpart in vm_c, which reads the process-wide
+    // compute dtype): the dtype of key/value in store_kv, and so of the
+    // stored norms, scales and zeros
     TurboQuantBackend(int head_dim, const std::string& quant_method, int num_attention_heads,
-                      int num_kv_heads, int gpu_device);
+                      int num_kv_heads, int gpu_device,
+                      ScalarType activation_dtype = ScalarType::FLOAT16);
     ~TurboQuantBackend() override;
 
     void store_kv(const void* key, const void* value, void* key_cache, void* value_cache,
@@ -115,6 +121,7 @@ private:
     TQConfig config_;
     TQWorkspace workspace_;
     int gpu_device_;
+    ScalarType activation_dtype_;
     int max_num_batched_tokens_ = 0;
     int max_num_seqs_ = 0;
     int num_attention_heads_ = 0;

@@ -10,11 +10,19 @@
 //     (the rotation is an in-register Walsh-Hadamard transform and the
 //     codebook travels in the kernel arguments).
 //   * TQWorkspace holds only the decode workspace (split partials); the store
-//     is one fused kernel without scratch.  It is sized by ensure_decode and
-//     grows, if a call needs more, before the launch (vm_c grew it inside
-//     the call as well, turboquant_kernels.cu:704-741).
-//   * "turboquant_k8v4" (fp8 keys) is not implemented: from_method builds
-//     its layout, the kernels reject it with std::runtime_error.
+//     is one fused kernel without scratch.  It is sized by ensure_decode;
+//     TurboQuantBackend::ensure_workspace sizes it for max_num_seqs requests
+//     of any length, so its decode calls never allocate.  A direct call that
+//     needs more grows it before the launch (vm_c grew it inside the call,
+//     turboquant_kernels.cu:704-741).
+//   * The activation dtype is an argument (trailing, defaulted to fp16) of
+//     turboquant_store and turboquant_decode_attention: vm_c reads it from
+//     the process-wide gpu().compute_dtype() (turboquant_kernels.cu:808,
+//     :966).  Norms, scales and zeros are stored in that dtype.
+//   * "turboquant_k8v4" (fp8 keys): the decode reads no norm for fp8 keys;
+//     the reference multiplies them by the two bytes at +mse_bytes, which
+//     for this layout are the first V code bytes (turboquant_kernels.cu:
+//     443-450), and that is not reproduced.
 #pragma once
 
 #include <cstddef>
@@ -94,7 +102,8 @@ void turboquant_decode_attention(void* output, const void* query, const void* kv
                                  float scale, int64_t block_size, int64_t max_num_blocks_per_req,
                                  const TQConfig& config, const TQBuffers& buffers,
                                  TQWorkspace& workspace, int max_num_kv_splits,
-                                 hipStream_t stream = nullptr);
+                                 hipStream_t stream = nullptr,
+                                 ScalarType dtype = ScalarType::FLOAT16);
 
 // Sylvester Hadamard matrix times 1/sqrt(d) (turboquant_kernels.cu:551-570)
 void build_hadamard_on_host(float* out, int d);

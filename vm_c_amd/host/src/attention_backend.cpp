@@ -113,9 +113,12 @@ void PagedAttentionBackend::ensure_workspace(int max_num_batched_tokens, int max
 
 // attention_backend.cpp:101-113
 TurboQuantBackend::TurboQuantBackend(int head_dim, const std::string& quant_method,
-                                     int num_attention_heads, int num_kv_heads, int gpu_device)
-    : gpu_device_(gpu_device), num_attention_heads_(num_attention_heads), num_kv_heads_(num_kv_heads),
-      head_dim_(head_dim) {
+                                     int num_attention_heads, int num_kv_heads, int gpu_device,
+                                     ScalarType activation_dtype)
+    : gpu_device_(gpu_device), activation_dtype_(activation_dtype),
+      num_attention_heads_(num_attention_heads), num_kv_heads_(num_kv_heads), head_dim_(head_dim) {
+    if (activation_dtype != ScalarType::FLOAT16 && activation_dtype != ScalarType::BFLOAT16)
+        throw std::runtime_error("TurboQuantBackend: activations must be fp16 or bf16");
     HIP_CHECK(hipSetDevice(gpu_device_));
     config_ = TQConfig::from_method(head_dim, quant_method.c_str(), gpu_device_);
     // fp8 keys (turboquant_k8v4) use no codebook and no rotation
@@ -128,7 +131,9 @@ TurboQuantBackend::~TurboQuantBackend() {
 }
 
 // attention_backend.cpp:120-136: the decode workspace for max_num_seqs
-// requests of up to 32768 tokens; longer contexts grow it on demand
+// requests of any length (the split count, and so the workspace, stops
+// growing with the context once every CU has a page range), so no decode
+// call of up to max_num_seqs requests allocates
 void TurboQuantBackend::ensure_workspace(int max_num_batched_tokens, int max_num_seqs,
                                          int num_attention_heads, int num_kv_heads, int head_dim,
                                          int gpu_device) {
@@ -137,8 +142,8 @@ void TurboQuantBackend::ensure_workspace(int max_num_batched_tokens, int max_num
     num_attention_heads_ = num_attention_heads;
     num_kv_heads_ = num_kv_heads;
     head_dim_ = head_dim;
-    workspace_.ensure_decode(max_num_seqs, num_attention_heads, num_kv_heads, head_dim, 32768 / 16, 16,
-                             config_.max_num_kv_splits, gpu_device);
+    workspace_.ensure_decode(max_num_seqs, num_attention_heads, num_kv_heads, head_dim,
+                             int64_t{1} << 26, 16, config_.max_num_kv_splits, gpu_device);
 }
 
 void TurboQuantBackend::store_kv(const void* key, const void* value, void* key_cache,
@@ -148,7 +153,7 @@ void TurboQuantBackend::store_kv(const void* key, const void* value, void* key_c
     (void)value_cache;
     (void)cache_stride;
     turboquant_store(key, value, key_cache, slot_mapping, num_tokens, num_kv_heads, head_dim,
-                     block_size, config_, buffers_, workspace_, stream);
+                     block_size, config_, buffers_, workspace_, stream, activation_dtype_);
 }
 
 // attention_backend.cpp:153-197: prefill runs on the step's local K/V
@@ -180,11 +185,13 @@ void TurboQuantBackend::forward_decode(void* output, const void* query, const vo
                                        int num_heads, int num_kv_heads, int head_dim, float scale,
                                        int64_t block_size, ScalarType dtype, hipStream_t stream) {
     (void)value_cache;
-    (void)dtype;
+    if (dtype != activation_dtype_)
+        throw std::runtime_error("TurboQuantBackend::forward_decode: query dtype differs from the "
+                                 "activation dtype the pages were stored in");
     turboquant_decode_attention(output, query, key_cache, meta.block_tables, meta.seq_lens,
                                 meta.num_reqs, num_heads, num_kv_heads, head_dim, scale, block_size,
                                 meta.max_num_blocks_per_req, config_, buffers_, workspace_,
-                                config_.max_num_kv_splits, stream);
+                                config_.max_num_kv_splits, stream, dtype);
 }
 
 size_t TurboQuantBackend::workspace_size() const { return workspace_.decode_bytes; }

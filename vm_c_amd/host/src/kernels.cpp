@@ -192,7 +192,7 @@ void turboquant_decode_attention(void* output, const void* query, const void* kv
                                  float scale, int64_t block_size, int64_t max_num_blocks_per_req,
                                  const TQConfig& config, const TQBuffers& buffers,
                                  TQWorkspace& workspace, int max_num_kv_splits,
-                                 hipStream_t stream) {
+                                 hipStream_t stream, ScalarType dtype) {
     (void)buffers;
     int dev = 0;
     HIP_CHECK(hipGetDevice(&dev));
@@ -201,7 +201,7 @@ void turboquant_decode_attention(void* output, const void* query, const void* kv
     const vmc_tq_config c = config.to_c();
     VMC_CALL(vmc_turboquant_decode_attention(
         output, query, kv_cache, block_tables, seq_lens, batch_size, num_heads, num_kv_heads,
-        head_dim, scale, block_size, max_num_blocks_per_req, &c, VMC_DTYPE_F16, max_num_kv_splits,
+        head_dim, scale, block_size, max_num_blocks_per_req, &c, vmc_dtype_of(dtype), max_num_kv_splits,
         workspace.decode_workspace, workspace.decode_bytes, stream));
 }
 
