@@ -230,6 +230,28 @@ int vmc_turboquant_decode_attention(void* output, const void* query, const void*
                                     size_t workspace_bytes, vmc_stream_t stream);
 
 /*
+ * vmc_turboquant_decode_attention without a workspace argument: the split
+ * partials go to a device array inside the library (one per GPU, held until
+ * the process ends, vmc_noalloc_scratch_bytes() = 24 MiB), so the call
+ * allocates nothing -- no hipMalloc, hipFree or allocating library routine --
+ * and records no memset.  No counterpart in the reference: for callers that
+ * cannot allocate (code under HIP graph capture, serving loops, harnesses that
+ * forbid allocation).  Same arguments, semantics and kernels as
+ * vmc_turboquant_decode_attention; returns VMC_ENOMEM when
+ * vmc_turboquant_decode_workspace_size(...) exceeds the array.  Calls that
+ * overlap on one GPU share the array and race: serialise them (one stream,
+ * or events).
+ */
+size_t vmc_noalloc_scratch_bytes(void);
+int vmc_turboquant_decode_attention_noalloc(void* output, const void* query, const void* kv_cache,
+                                            const int32_t* block_tables, const int32_t* seq_lens,
+                                            int batch_size, int num_heads, int num_kv_heads,
+                                            int head_dim, float scale, int64_t block_size,
+                                            int64_t max_num_blocks_per_req, const vmc_tq_config* cfg,
+                                            int half_dtype, int max_num_kv_splits,
+                                            vmc_stream_t stream);
+
+/*
  * Prefill attention over packed TurboQuant pages with a cached prefix: token
  * t is token_positions[t] of sequence token_to_seq[t] and attends positions
  * 0 .. token_positions[t] through its block_tables row (this step's tokens

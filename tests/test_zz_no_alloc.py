@@ -1,0 +1,61 @@
+"""GPU test of vmc_turboquant_decode_attention_noalloc (the decode whose split
+partials live in the library's own device array): through the C ABI, its
+output equals vmc_turboquant_decode_attention's with a caller workspace, bit
+for bit (same kernels, same split), on two calls in a row -- the second with a
+smaller batch and shorter contexts, so stale rows of the first call are in the
+array -- for fp16 and bf16 activations; and a shape whose partials exceed the
+array is rejected with VMC_ENOMEM before any launch."""
+import numpy as np
+import pytest
+
+from kvgen import BS, f32_to_bf16_bits, make_workload
+
+pytestmark = pytest.mark.gpu
+
+
+def _pages(dev, w, cfg, bf16):
+    import torch
+    from vm_c_amd import capi
+    cache = torch.zeros(w.num_blocks * BS * w.Hkv * cfg.slot_size_aligned, dtype=torch.uint8, device=dev)
+    if bf16:
+        cv = lambda a: torch.from_numpy(f32_to_bf16_bits(a.astype(np.float32)).view(np.int16)).to(dev).view(
+            torch.bfloat16)
+    else:
+        cv = lambda a: torch.from_numpy(a).to(dev)
+    capi.turboquant_store(cv(w.K), cv(w.V), cache, torch.from_numpy(w.slots).to(dev), BS, cfg)
+    return cache, cv(w.Q)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_noalloc_decode_matches_workspace_decode(dev, bf16):
+    import torch
+    from vm_c_amd import capi
+    cfg = capi.tq_config(128, "turboquant_3bit_nc")
+    big = make_workload([5000, 1024, 77, 32768, 3000, 17], Hq=64, Hkv=8, seed=21)
+    small = make_workload([900, 40], Hq=32, Hkv=8, seed=22)
+    for w in (big, small):
+        cache, q = _pages(dev, w, cfg, bf16)
+        bt = torch.from_numpy(w.bt).to(dev)
+        sl = torch.from_numpy(w.seq_lens).to(dev)
+        ref = torch.full_like(q, float("nan"))
+        capi.turboquant_decode_attention(ref, q, cache, bt, sl, w.Hkv, float(w.scale), cfg, BS)
+        got = torch.full_like(q, float("nan"))
+        capi.turboquant_decode_attention_noalloc(got, q, cache, bt, sl, w.Hkv, float(w.scale), cfg, BS)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), \
+            f"noalloc decode differs from the workspace decode (B={w.B})"
+
+
+def test_noalloc_rejects_oversized_partials(dev):
+    import ctypes as C
+    from vm_c_amd import capi
+    L = capi.load()
+    cfg = capi.tq_config(128, "turboquant_3bit_nc")
+    cap = L.vmc_noalloc_scratch_bytes()
+    # 1024 query heads per call: the partial rows of every range exceed the array
+    need = capi.turboquant_decode_workspace_size(64, 1024, 8, 128, 4096, BS)
+    assert need > cap
+    p = C.c_void_p(256)
+    rc = L.vmc_turboquant_decode_attention_noalloc(p, p, p, p, p, 64, 1024, 8, 128, C.c_float(0.1), BS, 4096,
+                                                   C.byref(cfg), 0, 0, None)
+    assert rc == capi.VMC_ENOMEM

@@ -77,6 +77,11 @@ def load():
     L.vmc_turboquant_decode_attention.restype = _I
     L.vmc_turboquant_decode_attention.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I64,
                                                   _I64, C.POINTER(TQConfig), _I, _I, _P, _SZ, _P]
+    L.vmc_noalloc_scratch_bytes.restype = _SZ
+    L.vmc_noalloc_scratch_bytes.argtypes = []
+    L.vmc_turboquant_decode_attention_noalloc.restype = _I
+    L.vmc_turboquant_decode_attention_noalloc.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I64,
+                                                          _I64, C.POINTER(TQConfig), _I, _I, _P]
     L.vmc_fused_qk_norm_rope_store.restype = _I
     L.vmc_fused_qk_norm_rope_store.argtypes = [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I,
                                                _F, _I, _I64, _I64, _I, _I, C.POINTER(TQConfig), _I,
@@ -225,6 +230,19 @@ def turboquant_decode_attention(out, query, kv_cache, block_tables, seq_lens, nu
         max_splits, _ptr(workspace), workspace.numel() * workspace.element_size(),
         _stream(stream))
     _check(rc, "vmc_turboquant_decode_attention")
+    return out
+
+
+def turboquant_decode_attention_noalloc(out, query, kv_cache, block_tables, seq_lens, num_kv_heads,
+                                        scale, cfg, block_size=16, max_splits=0, stream=None):
+    """vmc_turboquant_decode_attention_noalloc: the split partials go to the
+    library's own device array (nothing is allocated by the call)."""
+    B, Hq, D = query.shape
+    rc = load().vmc_turboquant_decode_attention_noalloc(
+        _ptr(out), _ptr(query), _ptr(kv_cache), _ptr(block_tables), _ptr(seq_lens), B, Hq,
+        num_kv_heads, D, scale, block_size, block_tables.shape[1], C.byref(cfg), _dtype_code(query),
+        max_splits, _stream(stream))
+    _check(rc, "vmc_turboquant_decode_attention_noalloc")
     return out
 
 

@@ -1910,6 +1910,53 @@ extern "C" int vmc_turboquant_decode_attention(void* output, const void* query, 
                           half_dtype, max_num_kv_splits, workspace, workspace_bytes, stream);
 }
 
+// ---- allocation-free variant of vmc_turboquant_decode_attention ----------
+//
+// The split partials (fp32 o, m, l rows of sequences cut by a page-range
+// boundary) go to a file-scope device array instead of a caller workspace.
+// Each device holds its own copy, resolved once per device by
+// hipGetSymbolAddress; the array's host-side name is never passed to a kernel.
+// Nothing needs clearing between calls: the merge reads only the rows that the
+// same call's split pass wrote.  Calls that overlap on one device share the
+// array and race.
+namespace {
+constexpr size_t kNoAllocScratchBytes = size_t{24} << 20;  // 24 MiB per device
+__device__ __align__(256) unsigned char noalloc_scratch[kNoAllocScratchBytes];
+
+void* noalloc_scratch_ptr() {
+    static std::mutex mu;
+    static void* ptrs[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lk(mu);
+    if (!ptrs[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(noalloc_scratch)) != hipSuccess || !p) return nullptr;
+        ptrs[dev] = p;
+    }
+    return ptrs[dev];
+}
+}  // namespace
+
+extern "C" size_t vmc_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int vmc_turboquant_decode_attention_noalloc(
+    void* output, const void* query, const void* kv_cache, const int32_t* block_tables,
+    const int32_t* seq_lens, int batch_size, int num_heads, int num_kv_heads, int head_dim, float scale,
+    int64_t block_size, int64_t max_num_blocks_per_req, const vmc_tq_config* cfg, int half_dtype,
+    int max_num_kv_splits, vmc_stream_t stream) {
+    if (num_heads <= 0 || num_kv_heads <= 0 || batch_size < 0) return VMC_EINVAL;
+    const size_t need = vmc_turboquant_decode_workspace_size(batch_size, num_heads, num_kv_heads, head_dim,
+                                                             max_num_blocks_per_req, block_size,
+                                                             max_num_kv_splits);
+    if (need > kNoAllocScratchBytes) return VMC_ENOMEM;
+    void* ws = nullptr;
+    if (need > 0 && !(ws = noalloc_scratch_ptr())) return VMC_EIO;
+    return tq_decode_rows(output, query, kv_cache, block_tables, seq_lens, nullptr, nullptr, batch_size,
+                          num_heads, num_kv_heads, head_dim, scale, block_size, max_num_blocks_per_req, cfg,
+                          half_dtype, max_num_kv_splits, ws, ws ? kNoAllocScratchBytes : 0, stream);
+}
+
 extern "C" int vmc_turboquant_prefill_attention(void* output, const void* query, const void* kv_cache,
                                                 const int32_t* block_tables, const int32_t* token_to_seq,
                                                 const int32_t* token_positions, int num_tokens,
