@@ -17,12 +17,22 @@ Also measured in the same run (extra fields of the same line):
   * decode_other_configs: the attention operator on batch 32 x 8192 with
     4-bit TurboQuant and with its per-32-group 4-bit variant, and on batch 16 (lengths in [512, 4096]) with q8_0
     K/V pages -> GB/s;
+  * decode_other_configs also holds batch 1 x 2048 fp16 pages (the
+    configuration the reference's CPU path runs);
   * causal prefill: batch 4 x 4096 tokens, 32/8 heads, bf16, fused q8_0
     quantize-on-append into the paged cache -> TFLOP/s;
   * fused_norm_rope: Q/K RMSNorm + RoPE + q8_0 append of the same prefill
     batch (16384 tokens, 32/8 heads, bf16) in one launch -> GB/s;
+  * hbm_ceiling_measured: a 2 GiB copy and a 4 GiB read on the same GPU;
   * cpu_baseline: the CPU restatement of the TurboQuant decode (OpenMP over
-    all host cores) on a bounded sample of the same workload.
+    all host cores) on the headline workload (the reference has no CPU
+    TurboQuant path), plus reference_ggml_cpu: the reference's own ggml CPU
+    flash-attention (built from its sources into oracle/_ref) on the
+    fp16 decode, q8_0 decode and bf16 prefill configurations.
+Each timed loop records a HIP event per call on the kernels' stream: means
+over the timed region (the headline step: exactly --steps calls) and the
+median call are reported; the attention operator alone is timed over
+max(50, --steps) calls.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 """
@@ -66,6 +76,23 @@ def decode_workload():
         bt[b, :pages[b]] = perm[k:k + pages[b]]
         k += pages[b]
     return dict(B=B, Hq=Hq, Hkv=Hkv, lens=lens, bt=bt, nblk=nblk, max_blocks=max_blocks)
+
+
+def time_loop(torch, fn, n, warm, stream):
+    """`warm` untimed calls, then `n` timed ones with a HIP event after each
+    on `stream` (the stream the kernels run on); returns (mean ms over the
+    timed region, median ms of the individual calls)."""
+    for i in range(warm):
+        fn(i)
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    ev[0].record(stream)
+    for i in range(n):
+        fn(warm + i)
+        ev[i + 1].record(stream)
+    ev[n].synchronize()
+    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(n)]
+    return ev[0].elapsed_time(ev[n]) / n, float(np.median(per))
 
 
 def slots_for(bt, lens, positions_of):
@@ -124,21 +151,9 @@ def bench_decode(args, torch, capi, dev, method="turboquant_3bit_nc", sign_seed=
         capi.turboquant_decode_attention(out, q, pools[i % npool], bt_d, lens_d, Hkv, scale, cfg,
                                          BS, workspace=ws, stream=stream)
 
-    def timed(fn, n, warm):
-        for i in range(warm):
-            fn(i)
-        torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for i in range(n):
-            fn(warm + i)
-        e1.record(stream)
-        e1.synchronize()
-        return e0.elapsed_time(e1) / n  # ms
-
-    ms_step = timed(step, args.steps, args.warmup)
-    ms_attn = timed(attn_only, args.steps, args.warmup)
+    ms_step, med_step = time_loop(torch, step, args.steps, args.warmup, stream)
+    n_attn = max(50, args.steps)
+    ms_attn, med_attn = time_loop(torch, attn_only, n_attn, args.warmup, stream)
     assert torch.isfinite(out.float()).all().item(), "decode produced non-finite values"
 
     sum_l = int(lens.sum())
@@ -148,27 +163,38 @@ def bench_decode(args, torch, capi, dev, method="turboquant_3bit_nc", sign_seed=
     attn_bytes = kv_bytes + qo_bytes + table_bytes
     append_bytes = B * Hkv * (2 * D * 2 + slot_bytes) + B * 8
     step_bytes = attn_bytes + append_bytes
-    res = dict(w=w, ms_step=ms_step, ms_attn=ms_attn, attn_bytes=attn_bytes, step_bytes=step_bytes,
-               kv_bytes=kv_bytes, sum_l=sum_l, q=q, pools=pools, bt=bt, lens=lens, cfg=cfg)
+    res = dict(w=w, ms_step=ms_step, ms_attn=ms_attn, med_step=med_step, med_attn=med_attn, n_attn=n_attn,
+               attn_bytes=attn_bytes, step_bytes=step_bytes, kv_bytes=kv_bytes, sum_l=sum_l, q=q,
+               pools=pools, bt=bt, lens=lens, cfg=cfg)
     log(f"decode step {ms_step * 1e3:.1f} us, attention {ms_attn * 1e3:.1f} us, "
         f"{attn_bytes / ms_attn / 1e6:.0f} GB/s attention-only")
     return res
 
 
+DECODE_CFGS = {
+    # kind: (seed, batch, Hq, Hkv, lengths, KV format)
+    "f16_single2048": (0, 1, 32, 8, "2048", "fp16"),
+    "tq4_32x8192": (2, 32, 32, 8, "8192", "turboquant_4bit_nc"),
+    "g32_4bit_32x8192": (2, 32, 32, 8, "8192", "turboquant_4bit_g32"),
+    "q8_0_batch16": (1, 16, 32, 8, "u512_4096", "q8_0"),
+}
+
+
 def bench_decode_cfg(args, torch, capi, dev, kind):
-    """The other two decode configurations, attention operator only:
+    """The other decode configurations, attention operator only:
+    "f16_single2048": batch 1, 2048 tokens, 32/8 heads, fp16 K/V pages, block
+    table a permutation of 128 pages (seed 0) -- 8.4 MB, launch-bound;
     "tq4_32x8192": batch 32 x 8192 tokens, 32/8 heads, turboquant_4bit_nc
     (134 B slots), seed 2; "g32_4bit_32x8192": the same batch with the
     configuration text's 4-bit per-32-group variant (160 B slots, signs
-    seed 2); "q8_0_batch16": batch 16, lengths uniform in
-    [512, 4096] (seed 1), 32/8 heads, q8_0 K and V pages (136 B per
-    token-head each).  Pools replicated to >= 2 GiB and rotated."""
-    if kind in ("tq4_32x8192", "g32_4bit_32x8192"):
-        seed, B, Hq, Hkv = 2, 32, 32, 8
-        lens = np.full(B, 8192, np.int32)
-    else:
-        seed, B, Hq, Hkv = 1, 16, 32, 8
+    seed 2); "q8_0_batch16": batch 16, lengths uniform in [512, 4096]
+    (seed 1), 32/8 heads, q8_0 K and V pages (136 B per token-head each).
+    Pools replicated to >= 2 GiB and rotated."""
+    seed, B, Hq, Hkv, lspec, fmt = DECODE_CFGS[kind]
+    if lspec == "u512_4096":
         lens = np.random.default_rng(seed).integers(512, 4097, B).astype(np.int32)
+    else:
+        lens = np.full(B, int(lspec), np.int32)
     rng = np.random.default_rng(seed)
     pages = (lens + BS - 1) // BS
     nblk = int(pages.sum())
@@ -183,18 +209,19 @@ def bench_decode_cfg(args, torch, capi, dev, kind):
     slots = torch.from_numpy(slots_for(bt, lens, (b_all, p_all))).to(dev)
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
-    tq = kind in ("tq4_32x8192", "g32_4bit_32x8192")
+    tq = fmt.startswith("turboquant")
     if tq:
-        cfg = (capi.tq_config(D, "turboquant_4bit_nc") if kind == "tq4_32x8192"
-               else capi.tq_config(D, "turboquant_4bit_g32", sign_seed=2))
+        cfg = capi.tq_config(D, fmt, sign_seed=2 if fmt.endswith("_g32") else 0)
         entry = cfg.slot_size_aligned
         pool_bytes = nblk * BS * Hkv * entry
     else:
-        entry = capi.kv_entry_bytes(capi.KV_Q8_0, D)
+        kvf = capi.KV_FORMATS[fmt]
+        entry = capi.kv_entry_bytes(kvf, D)
         pool_bytes = 2 * nblk * BS * Hkv * entry
     npool = max(2, math.ceil(2 * 1024 ** 3 / pool_bytes))
     pools = [torch.empty(pool_bytes, dtype=torch.uint8, device=dev) for _ in range(npool)]
     T = int(lens.sum())
+    half = pool_bytes // 2
     for s0 in range(0, T, 65536):
         n = min(65536, T - s0)
         kk = torch.randn((n, Hkv, D), generator=gen, device=dev).half()
@@ -202,9 +229,8 @@ def bench_decode_cfg(args, torch, capi, dev, kind):
         if tq:
             capi.turboquant_store(kk, vv, pools[0], slots[s0:s0 + n], BS, cfg)
         else:
-            half = pool_bytes // 2
             capi.reshape_and_cache(kk, vv, pools[0][:half], pools[0][half:], slots[s0:s0 + n], BS,
-                                   kv_format=capi.KV_Q8_0)
+                                   kv_format=kvf)
     for i in range(1, npool):
         pools[i].copy_(pools[0])
     q = torch.randn((B, Hq, D), generator=gen, device=dev).half()
@@ -225,78 +251,67 @@ def bench_decode_cfg(args, torch, capi, dev, kind):
             capi.turboquant_decode_attention(out, q, pool, bt_d, lens_d, Hkv, scale, cfg, BS,
                                              workspace=ws, stream=stream)
         else:
-            half = pool_bytes // 2
             capi.paged_attention_decode(out, q, pool[:half], pool[half:], bt_d, lens_d, Hkv, scale,
-                                        block_size=BS, kv_format=capi.KV_Q8_0, workspace=ws,
-                                        stream=stream)
+                                        block_size=BS, kv_format=kvf, workspace=ws, stream=stream)
 
-    for i in range(args.warmup):
-        run(i)
-    torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for i in range(args.steps):
-        run(args.warmup + i)
-    e1.record(stream)
-    e1.synchronize()
-    ms = e0.elapsed_time(e1) / args.steps
+    ms, med = time_loop(torch, run, max(50, args.steps), args.warmup, stream)
     assert torch.isfinite(out.float()).all().item(), f"{kind} decode produced non-finite values"
     kv = T * Hkv * entry * (1 if tq else 2)
     nbytes = kv + 2 * B * Hq * D * 2 + nblk * 4 + B * 4
     gbs = nbytes / (ms * 1e-3) / 1e9
-    log(f"decode {kind}: {ms * 1e3:.1f} us, {gbs:.0f} GB/s")
+    log(f"decode {kind}: {ms * 1e3:.1f} us (median {med * 1e3:.1f}), {gbs:.0f} GB/s")
     del pools
     torch.cuda.empty_cache()
-    return {"workload": kind, "batch": B, "num_heads": Hq, "num_kv_heads": Hkv,
-            "sum_ctx": T, "ms": round(ms, 4), "gbs": round(gbs, 1),
-            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes}
+    return {"workload": kind, "kv": fmt, "batch": B, "num_heads": Hq, "num_kv_heads": Hkv,
+            "sum_ctx": T, "ms": round(ms, 4), "ms_median": round(med, 4), "gbs": round(gbs, 1),
+            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes,
+            "tokens_per_s": round(B / (ms * 1e-3), 1)}
 
 
 # ------------------------------------------------------------------ prefill
 
 def bench_prefill(args, torch, capi, dev):
+    """Causal prefill of 4 x 4096 tokens, 32/8 heads, bf16, the q8_0 pages
+    written in the same launch.  Sets of q/k/v/out/pages (370 MB each) are
+    replicated past 1 GiB and rotated, so the 256 MB last-level cache holds
+    no set from one call to the next."""
     B, S, Hq, Hkv = 4, 4096, 32, 8
     T = B * S
     gen = torch.Generator(device=dev)
     gen.manual_seed(3)
-    q = torch.randn((T, Hq, D), generator=gen, device=dev).bfloat16()
-    k = torch.randn((T, Hkv, D), generator=gen, device=dev).bfloat16()
-    v = torch.randn((T, Hkv, D), generator=gen, device=dev).bfloat16()
-    pos = torch.arange(S, dtype=torch.int32, device=dev).repeat(B)
+    E = capi.kv_entry_bytes(capi.KV_Q8_0, D)
     nblk = T // BS
+    set_bytes = T * (2 * Hq + 2 * Hkv) * D * 2 + 2 * nblk * BS * Hkv * E
+    nset = max(2, math.ceil(1024 ** 3 / set_bytes))
+    sets = []
+    for _ in range(nset):
+        q = torch.randn((T, Hq, D), generator=gen, device=dev).bfloat16()
+        k = torch.randn((T, Hkv, D), generator=gen, device=dev).bfloat16()
+        v = torch.randn((T, Hkv, D), generator=gen, device=dev).bfloat16()
+        kc = torch.empty(nblk * BS * Hkv * E, dtype=torch.uint8, device=dev)
+        sets.append((q, k, v, torch.empty_like(q), kc, torch.empty_like(kc)))
+    pos = torch.arange(S, dtype=torch.int32, device=dev).repeat(B)
     perm = torch.randperm(nblk, generator=torch.Generator().manual_seed(3)).to(dev)
     t = torch.arange(T, device=dev)
     slots = (perm[t // BS] * BS + t % BS).to(torch.int64)
-    E = capi.kv_entry_bytes(capi.KV_Q8_0, D)
-    kc = torch.empty(nblk * BS * Hkv * E, dtype=torch.uint8, device=dev)
-    vc = torch.empty_like(kc)
-    out = torch.empty_like(q)
     scale = 1.0 / math.sqrt(D)
     stream = torch.cuda.current_stream()
 
-    def run():
+    def run(i):
+        q, k, v, out, kc, vc = sets[i % nset]
         capi.flash_attention_prefill(out, q, k, v, pos, Hkv, scale, key_cache=kc, value_cache=vc,
                                      slot_mapping=slots, block_size=BS, kv_format=capi.KV_Q8_0,
                                      stream=stream)
 
-    for _ in range(max(2, args.warmup // 2)):
-        run()
-    torch.cuda.synchronize()
-    n = max(5, args.steps // 2)
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(n):
-        run()
-    e1.record(stream)
-    e1.synchronize()
-    ms = e0.elapsed_time(e1) / n
+    n = max(20, args.steps)
+    ms, med = time_loop(torch, run, n, max(2, args.warmup // 2), stream)
     flops = 4.0 * B * Hq * D * S * (S + 1) / 2
     tflops = flops / (ms * 1e-3) / 1e12
-    assert torch.isfinite(out.float()).all().item(), "prefill produced non-finite values"
-    log(f"prefill {ms * 1e3:.1f} us, {tflops:.1f} TFLOP/s")
-    return dict(ms=ms, tflops=tflops, flops=flops)
+    assert all(torch.isfinite(st[3].float()).all().item() for st in sets), "prefill produced non-finite values"
+    log(f"prefill {ms * 1e3:.1f} us (median {med * 1e3:.1f}), {tflops:.1f} TFLOP/s, {nset} rotated sets")
+    del sets
+    torch.cuda.empty_cache()
+    return dict(ms=ms, med=med, tflops=tflops, flops=flops, n=n)
 
 
 # ------------------------------------------------------------------ fused norm + RoPE + append
@@ -305,60 +320,95 @@ def bench_fused_norm_rope(args, torch, capi, dev):
     """One launch over the prefill batch: q/k RMSNorm + neox RoPE in place,
     K (rotated) and V appended as q8_0 pages.  Algorithmic bytes: q and k read
     and written, v read, the page entries written, slots and positions read,
-    the distinct cos/sin rows and the norm weights read once."""
+    the distinct cos/sin rows and the norm weights read once.  Sets of
+    q/k/v/pages (~270 MB each) are replicated past 1 GiB and rotated."""
     B, S, Hq, Hkv = 4, 4096, 32, 8
     T = B * S
     gen = torch.Generator(device=dev)
     gen.manual_seed(5)
-    q = torch.randn((T, Hq, D), generator=gen, device=dev).bfloat16()
-    k = torch.randn((T, Hkv, D), generator=gen, device=dev).bfloat16()
-    v = torch.randn((T, Hkv, D), generator=gen, device=dev).bfloat16()
+    E = capi.kv_entry_bytes(capi.KV_Q8_0, D)
+    nblk = T // BS
+    set_bytes = T * (Hq + 2 * Hkv) * D * 2 + 2 * nblk * BS * Hkv * E
+    nset = max(2, math.ceil(1024 ** 3 / set_bytes))
+    sets = []
+    for _ in range(nset):
+        q = torch.randn((T, Hq, D), generator=gen, device=dev).bfloat16()
+        k = torch.randn((T, Hkv, D), generator=gen, device=dev).bfloat16()
+        v = torch.randn((T, Hkv, D), generator=gen, device=dev).bfloat16()
+        kc = torch.empty(nblk * BS * Hkv * E, dtype=torch.uint8, device=dev)
+        sets.append((q, k, v, kc, torch.empty_like(kc)))
     qw = (1.0 + 0.1 * torch.randn(Hq * D, generator=gen, device=dev)).bfloat16()
     kw = (1.0 + 0.1 * torch.randn(Hkv * D, generator=gen, device=dev)).bfloat16()
     theta = 10000.0 ** (-torch.arange(D // 2, device=dev, dtype=torch.float64) * 2.0 / D)
     ang = torch.arange(S, device=dev, dtype=torch.float64)[:, None] * theta[None, :]
     cs = torch.cat([ang.cos(), ang.sin()], dim=1).bfloat16().contiguous()
     pos = torch.arange(S, dtype=torch.int64, device=dev).repeat(B)
-    nblk = T // BS
     perm = torch.randperm(nblk, generator=torch.Generator().manual_seed(5)).to(dev)
     t = torch.arange(T, device=dev)
     slots = (perm[t // BS] * BS + t % BS).to(torch.int64)
-    E = capi.kv_entry_bytes(capi.KV_Q8_0, D)
-    kc = torch.empty(nblk * BS * Hkv * E, dtype=torch.uint8, device=dev)
-    vc = torch.empty_like(kc)
     stream = torch.cuda.current_stream()
 
-    def run():
+    def run(i):
+        q, k, v, kc, vc = sets[i % nset]
         capi.fused_qk_norm_rope_store(q, k, v, qw, kw, cs, pos, kc, vc, slots, BS, eps=1e-6,
                                       is_neox=True, kv_format=capi.KV_Q8_0, stream=stream)
 
-    for _ in range(max(2, args.warmup // 2)):
-        run()
-    torch.cuda.synchronize()
-    n = max(5, args.steps // 2)
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(n):
-        run()
-    e1.record(stream)
-    e1.synchronize()
-    ms = e0.elapsed_time(e1) / n
+    n = max(20, args.steps)
+    ms, med = time_loop(torch, run, n, max(2, args.warmup // 2), stream)
     per_token = 2 * 2 * (Hq + Hkv) * D + 2 * Hkv * D + 2 * Hkv * E + 16
     nbytes = T * per_token + S * D * 2 + (Hq + Hkv) * D * 2
     gbs = nbytes / (ms * 1e-3) / 1e9
-    assert torch.isfinite(q.float()).all().item(), "fused norm/RoPE produced non-finite values"
-    log(f"fused norm+rope+append {ms * 1e3:.1f} us, {gbs:.0f} GB/s")
-    return dict(ms=ms, gbs=gbs, bytes=nbytes)
+    assert all(torch.isfinite(st[0].float()).all().item() for st in sets), "fused norm/RoPE produced non-finite values"
+    log(f"fused norm+rope+append {ms * 1e3:.1f} us (median {med * 1e3:.1f}), {gbs:.0f} GB/s, {nset} rotated sets")
+    del sets
+    torch.cuda.empty_cache()
+    return dict(ms=ms, med=med, gbs=gbs, bytes=nbytes)
+
+
+def bench_hbm_ceiling(torch, dev):
+    """Measured HBM ceilings next to the 8 TB/s datasheet figure: a 2 GiB
+    device-to-device copy (read + write bytes / time) and a read-only 4 GiB
+    reduction (torch's sum), median of 10 each."""
+    stream = torch.cuda.current_stream()
+    n = 2 << 30
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    _, med_copy = time_loop(torch, lambda i: dst.copy_(src), 10, 3, stream)
+    del src, dst
+    x = torch.ones((4 << 30) // 4, dtype=torch.float32, device=dev)
+    _, med_read = time_loop(torch, lambda i: x.sum(), 10, 3, stream)
+    del x
+    torch.cuda.empty_cache()
+    res = {"copy_gbs": round(2 * n / (med_copy * 1e-3) / 1e9, 1),
+           "read_gbs": round((4 << 30) / (med_read * 1e-3) / 1e9, 1),
+           "method": "2 GiB torch copy_ (read+write) and 4 GiB fp32 torch sum (read), median of 10"}
+    log(f"HBM ceiling: copy {res['copy_gbs']} GB/s, read {res['read_gbs']} GB/s")
+    return res
 
 
 # ------------------------------------------------------------------ CPU baseline
 
-def cpu_baseline(dec, torch):
+def cpu_host_info(nthreads):
+    """CPU model, SIMD extensions and the thread count the CPU legs use."""
+    model, flags = "unknown", set()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name") and model == "unknown":
+                model = line.split(":", 1)[1].strip()
+            elif line.startswith("flags") and not flags:
+                flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    simd = [f for f in ("sse4_2", "avx", "avx2", "fma", "f16c", "avx512f", "avx512_bf16", "amx_tile")
+            if f in flags]
+    return {"cpu_model": model, "simd": simd, "threads": nthreads, "logical_cpus": os.cpu_count()}
+
+
+def cpu_baseline(dec, torch, nthreads):
     """The reference has no CPU path for TurboQuant (its ggml CPU op aborts),
-    so the baseline is the CPU restatement of its two-stage decode (oracle,
-    OpenMP over the host cores) on the same pages: the whole 64-sequence
-    batch, repeated until about 10 s of wall time."""
+    so the headline baseline is the CPU restatement of its two-stage decode
+    (oracle, OpenMP over the host cores) on the same pages: the whole
+    64-sequence batch, repeated until about 10 s of wall time."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O
     lens, bt = dec["lens"], dec["bt"]
@@ -366,7 +416,6 @@ def cpu_baseline(dec, torch):
     qb = dec["q"].cpu().numpy().view(np.uint16)
     L = O.tq_layout("turboquant_3bit_nc")
     c, _ = O.tq_tables(D, 3)
-    nthreads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
     reps, t0 = 0, time.time()
     while True:
         O.tq_decode(qb, cache, bt, lens, dec["w"]["Hkv"], np.float32(1 / math.sqrt(D)), BS, L, c,
@@ -380,6 +429,83 @@ def cpu_baseline(dec, torch):
                 sample=f"the full 64-sequence batch ({dec['sum_l']} tokens), {reps} passes, "
                        f"{dt:.2f} s each; two-stage TurboQuant decode restated in C (no CPU path "
                        f"exists in the reference for this format)")
+
+
+def cpu_reference_ggml(nthreads):
+    """The reference's own CPU path: ggml_flash_attn_ext of its vendored ggml
+    (ggml-cpu/ops.cpp:8214-8957), compiled from its sources with vm_c's CPU
+    flags into oracle/_ref, on the configurations it can run -- 1 (fp16
+    decode, batch 1 x 2048), 2 (q8_0 decode, batch 16, lengths U[512, 4096],
+    K/V rows from ggml's own q8_0 encoder) and 4 (bf16 causal prefill, a
+    sample: the last 512 query rows of one 4096-token sequence, all 32
+    heads).  K/V are contiguous per sequence (the CPU operator's input; the
+    block-table gather is not timed); the timed region is ggml_graph_compute
+    only, repeated to ~2-4 s per configuration.  Bytes and FLOPs are the
+    GPU's algorithmic counts for the same work.  None without oracle/_ref."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+    import kvgen
+    if not O.ref_available():
+        return None
+    res = []
+    scale = np.float32(1 / math.sqrt(D))
+
+    def rows(fmt, x):  # [Hkv][n][D] fp32 values -> the reference's row encoding
+        H, n, _ = x.shape
+        if fmt == O.KV_F16:
+            return x.astype(np.float16).view(np.uint8).reshape(H, n, 2 * D)
+        if fmt == O.KV_BF16:
+            return kvgen.f32_to_bf16_bits(x).view(np.uint8).reshape(H, n, 2 * D)
+        return O.ref_quantize(fmt, np.ascontiguousarray(x).reshape(-1)).reshape(H, n, O.entry_bytes(fmt, D))
+
+    def timed(q, K, V, fmt, n, Hkv, causal=False, budget=2.0):
+        _, t1 = O.ref_flash_attn_timed(q, K, V, fmt, n, Hkv, scale, causal, nthreads, 1)
+        reps = max(1, min(200, int(budget / max(t1, 1e-6))))
+        _, t = O.ref_flash_attn_timed(q, K, V, fmt, n, Hkv, scale, causal, nthreads, reps)
+        return t, reps
+
+    # configuration 1
+    w = kvgen.single_seq_fp16_workload()
+    K = rows(O.KV_F16, np.ascontiguousarray(w.K.astype(np.float32).transpose(1, 0, 2)))
+    V = rows(O.KV_F16, np.ascontiguousarray(w.V.astype(np.float32).transpose(1, 0, 2)))
+    t, reps = timed(w.Q[0].astype(np.float32)[:, None, :], K, V, O.KV_F16, 2048, 8)
+    nbytes = 8405508
+    res.append({"config": 1, "workload": "fp16 decode, batch 1 x 2048 tokens, 32/8 heads", "kind": "reference",
+                "ms": round(t * 1e3, 4), "gbs": round(nbytes / t / 1e9, 3), "tokens_per_s": round(1 / t, 1),
+                "sample": f"whole workload, {reps} computes"})
+    # configuration 2
+    w = kvgen.batched_q8_0_workload()
+    starts = np.concatenate([[0], np.cumsum(w.seq_lens)])
+    tot, reps_min = 0.0, 10 ** 9
+    for b in range(w.B):
+        n = int(w.seq_lens[b])
+        K = rows(O.KV_Q8_0, np.ascontiguousarray(w.K[starts[b]:starts[b] + n].astype(np.float32).transpose(1, 0, 2)))
+        V = rows(O.KV_Q8_0, np.ascontiguousarray(w.V[starts[b]:starts[b] + n].astype(np.float32).transpose(1, 0, 2)))
+        t, reps = timed(w.Q[b].astype(np.float32)[:, None, :], K, V, O.KV_Q8_0, n, 8, budget=0.2)
+        tot += t
+        reps_min = min(reps_min, reps)
+    sum_l = int(w.seq_lens.sum())
+    nbytes = sum_l * 2176 + 2 * w.B * 32 * D * 2 + int(((w.seq_lens + 15) // 16).sum()) * 4 + w.B * 4
+    res.append({"config": 2, "workload": "q8_0 decode, batch 16, lengths U[512, 4096] seed 1, 32/8 heads",
+                "kind": "reference", "ms": round(tot * 1e3, 4), "gbs": round(nbytes / tot / 1e9, 3),
+                "tokens_per_s": round(w.B / tot, 1),
+                "sample": f"whole batch (sum of the 16 sequences' compute times, >= {reps_min} computes each)"})
+    # configuration 4 (sample)
+    qb, kb, vb, _, _ = kvgen.prefill_inputs([4096], 32, 8, seed=3)
+    n_q, n_kv = 512, 4096
+    q = np.ascontiguousarray(O.bf16_to_f32(qb[n_kv - n_q:]).transpose(1, 0, 2))
+    K = np.ascontiguousarray(kb.reshape(n_kv, 8, D).transpose(1, 0, 2)).view(np.uint8).reshape(8, n_kv, 2 * D)
+    V = np.ascontiguousarray(vb.reshape(n_kv, 8, D).transpose(1, 0, 2)).view(np.uint8).reshape(8, n_kv, 2 * D)
+    t, reps = timed(q, K, V, O.KV_BF16, n_kv, 8, causal=True, budget=4.0)
+    keys = sum(n_kv - n_q + i + 1 for i in range(n_q))
+    flops = 4.0 * 32 * D * keys
+    res.append({"config": 4, "workload": "bf16 causal prefill, 32/8 heads", "kind": "reference",
+                "ms": round(t * 1e3, 3), "tflops": round(flops / t / 1e12, 5),
+                "sample": f"the last {n_q} query rows of one 4096-token sequence ({flops:.3g} FLOP), "
+                          f"{reps} computes"})
+    for r in res:
+        log(f"reference ggml CPU, config {r['config']}: {r['ms']} ms")
+    return res
 
 
 # ------------------------------------------------------------------ traffic
@@ -411,6 +537,9 @@ def main():
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--skip-variant", action="store_true",
                     help="skip the per-32-group 3-bit variant's decode (turboquant_3bit_g32)")
+    ap.add_argument("--only", choices=("decode", "prefill", "fused", "configs"),
+                    help="profiling runs: only this part (decode: the headline operator; configs: "
+                         "the other decode configurations), one JSON line of its numbers")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy 5 times (the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -434,6 +563,20 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes": n, "launches": 5}), flush=True)
         return
+    if args.only:
+        if args.only == "decode":
+            r = bench_decode(args, torch, capi, dev)
+            r = {"ms_step": r["ms_step"], "ms_attn": r["ms_attn"], "ms_attn_median": r["med_attn"],
+                 "attn_bytes": r["attn_bytes"]}
+        elif args.only == "prefill":
+            r = bench_prefill(args, torch, capi, dev)
+        elif args.only == "fused":
+            r = bench_fused_norm_rope(args, torch, capi, dev)
+        else:
+            r = {"configs": [bench_decode_cfg(args, torch, capi, dev, k) for k in DECODE_CFGS]}
+        print(json.dumps({"only": args.only, **{k: v for k, v in r.items() if not hasattr(v, "shape")}}),
+              flush=True)
+        return
     dec = bench_decode(args, torch, capi, dev)
     var = None
     if not args.skip_variant:
@@ -448,11 +591,18 @@ def main():
                "tokens_per_s": round(v["w"]["B"] / (v["ms_step"] * 1e-3), 1)}
         del v
         torch.cuda.empty_cache()
-    others = [] if args.skip_variant else [bench_decode_cfg(args, torch, capi, dev, k)
-                                           for k in ("tq4_32x8192", "g32_4bit_32x8192", "q8_0_batch16")]
+    kinds = ("f16_single2048",) + (() if args.skip_variant else
+                                    ("tq4_32x8192", "g32_4bit_32x8192", "q8_0_batch16"))
+    others = [bench_decode_cfg(args, torch, capi, dev, k) for k in kinds]
     pre = None if args.skip_prefill else bench_prefill(args, torch, capi, dev)
     fused = None if args.skip_prefill else bench_fused_norm_rope(args, torch, capi, dev)
-    cpu = None if args.no_cpu_baseline else cpu_baseline(dec, torch)
+    ceiling = bench_hbm_ceiling(torch, dev)
+    cpu = None
+    if not args.no_cpu_baseline:
+        nthreads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+        cpu = cpu_baseline(dec, torch, nthreads)
+        cpu["host"] = cpu_host_info(nthreads)
+        cpu["reference_ggml_cpu"] = cpu_reference_ggml(nthreads)
 
     ms_step = dec["ms_step"]
     gbs_step = dec["step_bytes"] / (ms_step * 1e-3) / 1e9
@@ -483,7 +633,11 @@ def main():
                      "traffic": measured_traffic(),
                      "kernel": "turboquant_decode_attention: paged_decode_kernel + "
                                "decode_merge_kernel (one operator, two launches)",
-                     "ms": round(dec["ms_attn"], 4), "bytes": dec["attn_bytes"]},
+                     "ms": round(dec["ms_attn"], 4), "ms_median": round(dec["med_attn"], 4),
+                     "launches_timed": dec["n_attn"], "bytes": dec["attn_bytes"],
+                     "frac_of_measured_read_ceiling": round(gbs_attn / ceiling["read_gbs"], 4)},
+        "ms_per_step_median": round(dec["med_step"], 4),
+        "hbm_ceiling_measured": ceiling,
         "cpu_baseline": cpu,
     }
     if var is not None:
@@ -492,12 +646,13 @@ def main():
         line["decode_other_configs"] = others
     if pre is not None:
         line["prefill"] = {"workload": "causal prefill B=4 S=4096 Hq=32 Hkv=8 bf16, fused q8_0 append",
-                           "ms": round(pre["ms"], 4), "tflops": round(pre["tflops"], 1),
+                           "ms": round(pre["ms"], 4), "ms_median": round(pre["med"], 4),
+                           "launches_timed": pre["n"], "tflops": round(pre["tflops"], 1),
                            "pct_peak_mfma_bf16": round(100 * pre["tflops"] / MFMA_BF16_PEAK_TFLOPS, 2)}
     if fused is not None:
         line["fused_norm_rope"] = {
             "workload": "q/k RMSNorm + neox RoPE + q8_0 K/V append, 16384 tokens, Hq=32 Hkv=8 bf16",
-            "ms": round(fused["ms"], 4), "gbs": round(fused["gbs"], 1),
+            "ms": round(fused["ms"], 4), "ms_median": round(fused["med"], 4), "gbs": round(fused["gbs"], 1),
             "frac_hbm": round(fused["gbs"] / HBM_PEAK_GBS, 4), "bytes": fused["bytes"]}
     print(json.dumps(line), flush=True)
 

@@ -124,6 +124,10 @@ def ref():
         R.ref_flash_attn.restype = C.c_int
         R.ref_flash_attn.argtypes = [_P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int,
                                      C.c_int, C.c_int, C.c_float, C.c_int, C.c_int]
+        R.ref_flash_attn_timed.restype = C.c_int
+        R.ref_flash_attn_timed.argtypes = [_P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int,
+                                           C.c_int, C.c_int, C.c_float, C.c_int, C.c_int, C.c_int,
+                                           C.POINTER(C.c_double)]
         _ref = R
     return _ref
 
@@ -373,3 +377,17 @@ def ref_flash_attn(q, k_rows, v_rows, fmt, n_kv, Hkv, scale, causal=False, n_thr
                               scale, int(causal), n_threads)
     assert rc == 0, rc
     return out
+
+
+def ref_flash_attn_timed(q, k_rows, v_rows, fmt, n_kv, Hkv, scale, causal=False, n_threads=1, reps=1):
+    """ref_flash_attn computed `reps` times on one built graph; returns
+    (out fp32 [n_q][Hq][D], mean seconds of one graph compute)."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    Hq, n_q, D = q.shape
+    out = np.zeros((n_q, Hq, D), dtype=np.float32)
+    secs = C.c_double(0.0)
+    rc = ref().ref_flash_attn_timed(_ptr(out), _ptr(q), _ptr(np.ascontiguousarray(k_rows)),
+                                    _ptr(np.ascontiguousarray(v_rows)), fmt, n_q, n_kv, Hq, Hkv, D,
+                                    scale, int(causal), n_threads, reps, C.byref(secs))
+    assert rc == 0, rc
+    return out, secs.value
