@@ -8,8 +8,7 @@ is defined in vmc_attn.h and restated by the oracle).
 * decode: against the oracle's fp64 attention over the same pages, split-KV
   and per-sequence modes, ragged lengths, GQA 2..16;
 * the benchmark shapes: batch 32 x 8192 (4-bit, seed 2) and the ragged
-  32k batch (3-bit, seed 4), store bit-exact on a chunk, decode of selected
-  sequences.
+  32k batch (3-bit, seed 4): every pool byte bit-exact, every output row.
 Tolerance: |got - ref| <= 2e-3 + 1e-2 |ref|.
 """
 import numpy as np
@@ -136,13 +135,11 @@ def test_g32_benchmark_shapes(dev, method, shape):
     if shape == "cfg3":
         seed, Hq, Hkv = 2, 32, 8
         lens = np.full(32, 8192)
-        check = [0, 31]
     else:
         seed, Hq, Hkv = 4, 64, 8
         rng = np.random.default_rng(seed)
         lens = np.exp(rng.uniform(np.log(1024), np.log(32768), 64)).astype(np.int64)
         lens[0] = 32768
-        check = [0, 1, int(np.argmin(lens))]
     bt, slots, nblk = _layout(lens, seed)
     cfg = capi.tq_config(128, method, sign_seed=seed)
     S = cfg.slot_size_aligned
@@ -152,35 +149,28 @@ def test_g32_benchmark_shapes(dev, method, shape):
     T = slots.size
     chunk = 65536
     print(f"{method}: B={len(lens)} T={T} store", flush=True)
-    first = None
+    ref = np.zeros(cache.numel(), np.uint8)
     for s0 in range(0, T, chunk):
         n = min(chunk, T - s0)
         k = torch.randn((n, Hkv, 128), generator=gen, device=dev).half()
         v = torch.randn((n, Hkv, 128), generator=gen, device=dev).half()
         sl = torch.from_numpy(slots[s0:s0 + n]).to(dev)
         capi.turboquant_store(k, v, cache, sl, BS, cfg)
-        if first is None:
-            first = (k.cpu().numpy(), v.cpu().numpy(), slots[s0:s0 + n])
+        O.g32_store(bits16(k.cpu().numpy()), bits16(v.cpu().numpy()), slots[s0:s0 + n], ref, BS, bits, seed)
     torch.cuda.synchronize()
-    # store: the first chunk's slots bit-exact (a fresh pool holding only them)
-    k0, v0, sl0 = first
-    ref = np.zeros(cache.numel(), np.uint8)
-    O.g32_store(bits16(k0), bits16(v0), sl0, ref, BS, bits, seed)
+    # store: every byte of the pool, against the oracle storing the same chunks
     got = cache.cpu().numpy()
-    blk, off = sl0 // BS, sl0 % BS
-    idx = ((blk * BS + off) * Hkv)[:, None] * S + np.arange(Hkv * S)[None, :]
-    assert np.array_equal(got[idx], ref[idx]), "store differs on the first chunk"
-    # decode of the whole batch, checked on selected sequences
+    bad = np.flatnonzero(got != ref)
+    assert bad.size == 0, f"store differs at {bad.size} of {got.size} bytes"
+    # decode of the whole batch, every row
     q = torch.randn((len(lens), Hq, 128), generator=gen, device=dev).half()
     out = torch.full_like(q, float("nan"))
     capi.turboquant_decode_attention(out, q, cache, torch.from_numpy(bt).to(dev),
                                      torch.from_numpy(lens.astype(np.int32)).to(dev), Hkv,
                                      1.0 / np.sqrt(128.0), cfg, block_size=BS)
     torch.cuda.synchronize()
-    print(f"{method}: decode checked on sequences {check}", flush=True)
+    print(f"{method}: decode checked on all {len(lens)} sequences", flush=True)
     qn = q.cpu().numpy()
-    for b in check:
-        ex = O.g32_decode_exact(bits16(qn[b:b + 1]), got, bt[b:b + 1], lens[b:b + 1].astype(np.int32),
-                                Hkv, 1.0 / np.sqrt(128.0), BS, bits, seed)
-        ok, err = close_report(out[b:b + 1].float().cpu().numpy(), ex, ATOL, RTOL)
-        assert ok, f"sequence {b} (len {lens[b]}): max err {err}"
+    ex = O.g32_decode_exact(bits16(qn), got, bt, lens.astype(np.int32), Hkv, 1.0 / np.sqrt(128.0), BS, bits, seed)
+    ok, err = close_report(out.float().cpu().numpy(), ex, ATOL, RTOL)
+    assert ok, f"max err {err}"
