@@ -107,3 +107,43 @@ def test_prefill_config4_full_size(dev):
     vr = np.zeros(nbytes, np.uint8)
     O.kv_append(kb, vb, slots, kr, vr, BS, O.KV_Q8_0, src_bf16=True)
     assert np.array_equal(kc, kr) and np.array_equal(vc, vr)
+
+
+def test_prefill_bf16_v_outside_fp16_range(dev):
+    """bf16 V that fp16 cannot hold: one sequence at 2^100 scale (fp16
+    overflows), one at 2^-20 (fp16 subnormals keep 4 bits) with bf16
+    subnormals mixed in, one N(0,1) with sparse +-1e30 and +-1e-38 spikes
+    (these three take the kernel's exact mode), and one N(0,1) with sparse
+    2^-20 and +-1e-38 values only (the fp16 path, whose rounding of them is
+    below 2^-25).  Each sequence's rows are compared with exact fp64
+    attention after dividing both by the sequence's magnitude, so the usual
+    tolerance is relative to that scale."""
+    from kvgen import f32_to_bf16_bits
+    seq_lens, Hq, Hkv = [300, 77, 129, 200], 8, 2
+    qb, kb, _, pos, cu = _inputs(seq_lens, Hq, Hkv, seed=21)
+    T = qb.shape[0]
+    rng = np.random.default_rng(22)
+    v = rng.standard_normal((T, Hkv, 128)).astype(np.float64)
+    mag = np.ones(T)
+    mag[cu[0]:cu[1]] = 2.0 ** 100
+    mag[cu[1]:cu[2]] = 2.0 ** -20
+    v *= mag[:, None, None]
+    tiny = rng.random(v[cu[1]:cu[2]].shape) < 0.05
+    v[cu[1]:cu[2]][tiny] = 2.0 ** -130 * rng.choice([-1, 1], int(tiny.sum()))
+    for b, vals in ((2, [-1e30, 1e30, -1e-38, 1e-38]), (3, [-2.0 ** -20, 2.0 ** -20, -1e-38, 1e-38])):
+        seg = v[cu[b]:cu[b + 1]].reshape(-1)
+        spikes = np.flatnonzero(rng.random(seg.size) < 2e-3)
+        seg[spikes] = rng.choice(vals, spikes.size)
+        v[cu[b]:cu[b + 1]] = seg.reshape(v[cu[b]:cu[b + 1]].shape)
+    vb = f32_to_bf16_bits(v.astype(np.float32))
+    scale = 1.0 / np.sqrt(128)
+    got = _run(dev, qb, kb, vb, pos, Hkv, scale).reshape(T * Hq, 128)
+    assert np.isfinite(got).all()
+    toks = np.repeat(np.arange(T), Hq)
+    heads = np.tile(np.arange(Hq), T)
+    ex = O.prefill_exact_rows(qb, kb, vb, cu, Hkv, scale, toks, heads)
+    rs = mag[toks][:, None]
+    for b in range(len(seq_lens)):
+        sel = (toks >= cu[b]) & (toks < cu[b + 1])
+        ok, err = close_report(got[sel] / rs[sel], ex[sel] / rs[sel], ATOL, RTOL)
+        assert ok, f"sequence {b}: max scaled err {err}"

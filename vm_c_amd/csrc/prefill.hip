@@ -24,6 +24,11 @@
 //     already holds; V^T stores each 16-key block in that order, so a B
 //     operand is one 16-byte read.
 //   Per-row rescale factors reach the O rows through a small LDS scratch.
+// bf16 V that fp16 would overflow (|v| >= 65536), or rows of V entirely
+// below 2^-8 with values fp16 keeps only on its subnormal grid, are caught
+// in the V^T pass; the workgroup then reruns in an exact mode: raw bf16 V
+// rows as B operands, P in fp32 split into bf16 hi + lo, two bf16 MFMAs per
+// product.
 // Fused append: head group 0 of each KV head writes the block's K/V rows into
 // the paged cache with the same block encoders as vmc_reshape_and_cache
 // (bit-identical pages).
@@ -37,6 +42,7 @@ constexpr int NW = 8;      // waves per workgroup (32 query rows each)
 constexpr int BN = 64;     // kv rows per tile
 constexpr int NSLOT = 3;   // K/V tile slots in LDS
 constexpr float kNegInf = -__builtin_inff();
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 struct PrefillParams {
     uint16_t* out;
@@ -104,6 +110,7 @@ struct PrefillLds {
     uint8_t tile[NSLOT][2][BN * 256];  // [slot][K, V][row][position]
     uint8_t vtr[NSLOT][kD * BN * 2];   // [slot][dim][kv position] fp16 V^T
     float scratch[2][NW][32];          // [alpha, l][wave][row]
+    alignas(8) uint8_t wide[NSLOT][NW];  // bf16: wave w's V rows of the tile need the exact mode
 };
 
 __device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
@@ -204,9 +211,14 @@ prefill_kernel(PrefillParams p) {
     int vt_rd[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) vt_rd[c] = c32 * 128 + 16 * ((2 * c + h) ^ ((c32 >> 1) & 7));
+    // transposing LDS reads: lane (e, q) of a 16-lane group addresses row
+    // base + e, dims 4q .. 4q+3 of a 16-dim block; lane j receives dim j of
+    // the 4 rows
+    const int tq_e = (lane >> 2) & 3, tq_q = lane & 3, tq_j = lane & 15;
 
-    auto process = [&](int t, auto slot_c) __attribute__((always_inline)) {
+    auto process = [&](int t, auto slot_c, auto exact_c) __attribute__((always_inline)) {
         constexpr int SL = decltype(slot_c)::value;
+        constexpr bool EXACT = decltype(exact_c)::value;
         const int k0 = kv_lo + t * BN;
         // skip: tile entirely after this wave's last row, or before its first window
         const bool active = wave_ok && k0 <= wrow1 && k0 + BN - 1 >= wlo0;
@@ -285,27 +297,87 @@ prefill_kernel(PrefillParams p) {
                 for (int i = 0; i < 16; ++i) o[m][i] *= al[i];
         }
         const float m_use = m_run == kNegInf ? 0.0f : m_run;
-        // P = 2^(s c - m) in fp16 (11 bits, also for bf16 inputs) as MFMA A
-        // operands, chunk c = kv rows 16c .. 16c+15; the row sum adds the
-        // rounded values the MFMA uses
-        uint32_t pw[4][4];
-        float psum = 0.0f;
+        if constexpr (EXACT) {
+            // ---- exact mode (bf16 V that fp16 cannot hold): P = 2^(s c - m)
+            // in fp32 splits into bf16 hi + lo (16 significant bits, fp32
+            // range), the row sum adds the same parts, and O += P V runs as two
+            // bf16 MFMAs on the raw bf16 V rows, read by transposing reads:
+            // lane (n = c32, h) gets kv 16c + 4h + 0..3 and 16c + 8 + 4h + 0..3
+            // at dim 32m + n, the k order of the fp16 path.  Row
+            // 16c + 8sec + 4h + e has swz = 4e + ((2 sec + h) & 3), so chunk
+            // 4m + cb sits at 4 (m ^ e) + (cb ^ h ^ 2 sec).  The lane id is
+            // opaque here so that none of this is computed ahead, in
+            // registers the fast pass needs.
+            uint32_t phi[4][4], plo[4][4];
+            float psum = 0.0f;
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
+            for (int c = 0; c < 4; ++c)
 #pragma unroll
-            for (int e = 0; e < 8; e += 2) {
-                const int kb = c >> 1;
-                const int j0 = 4 * (2 * (c & 1) + (e >> 2)) + (e & 3);
-                const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][j0], csc, -m_use));
-                const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][j0 + 1], csc, -m_use));
-                const f16x2 ph = {(_Float16)p0, (_Float16)p1};
-                psum = __builtin_amdgcn_fdot2(ph, f16x2{(_Float16)1.0f, (_Float16)1.0f}, psum, false);
-                pw[c][e >> 1] = __builtin_bit_cast(uint32_t, ph);
+                for (int e = 0; e < 8; e += 2) {
+                    const int kb = c >> 1;
+                    const int j0 = 4 * (2 * (c & 1) + (e >> 2)) + (e & 3);
+                    uint32_t hb[2], lb[2];
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][j0 + u], csc, -m_use));
+                        hb[u] = __builtin_bit_cast(uint32_t, pv) & 0xffff0000u;
+                        const float r = pv - __builtin_bit_cast(float, hb[u]);  // exact
+                        lb[u] = __builtin_bit_cast(uint32_t, r) & 0xffff0000u;
+                        psum += __builtin_bit_cast(float, hb[u]) + __builtin_bit_cast(float, lb[u]);
+                    }
+                    phi[c][e >> 1] = (hb[0] >> 16) | hb[1];
+                    plo[c][e >> 1] = (lb[0] >> 16) | lb[1];
+                }
+            l_part += psum;
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+            const int le = (ln >> 2) & 3, lq = ln & 3, lh = ln >> 5;
+            const int cbh = (2 * ((ln >> 4) & 1) + (lq >> 1)) ^ lh;
+            const uint32_t vbase = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)
+                                       lds.tile[SL][1] +
+                                   (uint32_t)((4 * lh + le) * 256 + 8 * (lq & 1));
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const bf16x8 ah = as_v8<bf16x8>(u32x4{phi[c][0], phi[c][1], phi[c][2], phi[c][3]});
+                const bf16x8 al = as_v8<bf16x8>(u32x4{plo[c][0], plo[c][1], plo[c][2], plo[c][3]});
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    s16x4 part[2];
+#pragma unroll
+                    for (int sec = 0; sec < 2; ++sec) {
+                        const uint32_t a = vbase + (uint32_t)(4096 * c + 2048 * sec + 64 * (m ^ le) +
+                                                              16 * (cbh ^ (2 * sec)));
+                        part[sec] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                            (__attribute__((address_space(3))) s16x4*)(uintptr_t)a);
+                    }
+                    const u32x2 p0 = __builtin_bit_cast(u32x2, part[0]);
+                    const u32x2 p1 = __builtin_bit_cast(u32x2, part[1]);
+                    const bf16x8 vb = as_v8<bf16x8>(u32x4{p0[0], p0[1], p1[0], p1[1]});
+                    o[m] = MT<true>::mma(ah, vb, o[m]);
+                    o[m] = MT<true>::mma(al, vb, o[m]);
+                }
             }
-        l_part += psum;
-        // ---- O += P V (fp16): k = 8h + e <-> kv 16c + 8(e/4) + 4h + e%4 (the
-        // S^T registers' order); V arrives transposed, output column n = dim 32m + n
-        {
+        } else {
+            // P = 2^(s c - m) in fp16 (11 bits, also for bf16 inputs) as MFMA A
+            // operands, chunk c = kv rows 16c .. 16c+15; the row sum adds the
+            // rounded values the MFMA uses
+            uint32_t pw[4][4];
+            float psum = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    const int kb = c >> 1;
+                    const int j0 = 4 * (2 * (c & 1) + (e >> 2)) + (e & 3);
+                    const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][j0], csc, -m_use));
+                    const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb][j0 + 1], csc, -m_use));
+                    const f16x2 ph = {(_Float16)p0, (_Float16)p1};
+                    psum = __builtin_amdgcn_fdot2(ph, f16x2{(_Float16)1.0f, (_Float16)1.0f}, psum, false);
+                    pw[c][e >> 1] = __builtin_bit_cast(uint32_t, ph);
+                }
+            l_part += psum;
+            // ---- O += P V (fp16): k = 8h + e <-> kv 16c + 8(e/4) + 4h + e%4 (the
+            // S^T registers' order); V arrives transposed, output column n = dim 32m + n
             u32x4 vb[4][4];
 #pragma unroll
             for (int c = 0; c < 4; ++c)
@@ -332,12 +404,17 @@ prefill_kernel(PrefillParams p) {
     // transpose reads (16-lane group: 4 rows x 16 dims) and 8-byte writes.
     // Within each 16-key block, kv 8a + 4h + e sits at position 8h + 4a + e,
     // so the PV B operand of lane half h is one contiguous 16-byte chunk.
-    // bf16 inputs are converted to fp16 here (exact for |v| in [2^-14, 65504]).
-    const int tq_e = (lane >> 2) & 3, tq_q = lane & 3, tq_j = lane & 15;
+    // bf16 inputs are converted to fp16 here, which keeps every bit for
+    // 2^-17 <= |v| < 65536 and rounds smaller magnitudes to the subnormal
+    // grid (absolute error <= 2^-25).  The wave's rows are marked in
+    // lds.wide (exact mode for the workgroup) when they hold |v| >= 65536 or
+    // a NaN, or when they hold a value below 2^-17 but none of 2^-8 or more;
+    // otherwise the rounding error is at most 2^-17 of their largest |v|.
     auto v_transpose = [&](auto slot_c) __attribute__((always_inline)) {
         constexpr int SL = decltype(slot_c)::value;
         const uint8_t* vr = lds.tile[SL][1];
         uint8_t* vtt = lds.vtr[SL];
+        u16x2 amax = {0, 0}, amin1 = {0xffff, 0xffff};  // |bits|, |bits| - 1 (0 wraps)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int combo = 4 * i + (lane >> 4);
@@ -350,6 +427,9 @@ prefill_kernel(PrefillParams p) {
             if constexpr (BF16) {
 #pragma unroll
                 for (int e = 0; e < 2; ++e) {
+                    const u16x2 a = __builtin_bit_cast(u16x2, y[e] & 0x7fff7fffu);
+                    amax = __builtin_elementwise_max(amax, a);
+                    amin1 = __builtin_elementwise_min(amin1, a - u16x2{1, 1});
                     const f16x2 hh = {(_Float16)__builtin_bit_cast(float, y[e] << 16),
                                       (_Float16)__builtin_bit_cast(float, y[e] & 0xffff0000u)};
                     y[e] = __builtin_bit_cast(uint32_t, hh);
@@ -359,6 +439,16 @@ prefill_kernel(PrefillParams p) {
             const int ci = 2 * (2 * rs + (w >> 2)) + (w & 1);
             *reinterpret_cast<u32x2*>(vtt + dim * 128 + 16 * (ci ^ ((dim >> 1) & 7)) + 8 * ((w >> 1) & 1)) = y;
         }
+        if constexpr (BF16) {
+            // bf16 bit patterns: 0x477f = 65280 (largest below 2^16),
+            // 0x3700 = 2^-17, 0x3b80 = 2^-8
+            const uint32_t mx = max((uint32_t)amax[0], (uint32_t)amax[1]);
+            const uint32_t mn1 = min((uint32_t)amin1[0], (uint32_t)amin1[1]);
+            const bool ovf = __ballot(mx > 0x477fu) != 0;
+            const bool small = __ballot(mn1 < 0x36ffu) != 0;
+            const bool big = __ballot(mx >= 0x3b80u) != 0;
+            if (lane == 0) lds.wide[SL][w] = ovf || (small && !big);
+        }
     };
 
     // ---- NSLOT LDS slots: tile t in slot t % NSLOT; the next NSLOT - 1 tiles
@@ -367,24 +457,52 @@ prefill_kernel(PrefillParams p) {
     // vmcnt retires loads in order), converts its own V chunks, and the
     // barrier makes the tile visible and shows slot (t-1) % NSLOT free, which
     // then receives tile t + NSLOT - 1.
+    // bf16: when a tile's V is not fp16-exact (a flag every wave reads after
+    // the tile's barrier) the pass returns true and the workgroup starts over
+    // in the exact mode, which skips the V^T pass and multiplies the raw bf16
+    // rows.  The pass runs to its end rather than leaving early: an early
+    // exit costs the common case registers.
     static_assert(NSLOT == 3, "wait counts below assume three slots");
-    load_tile(0, std::integral_constant<int, 0>{});
-    if (1 < ntile) load_tile(1, std::integral_constant<int, 1>{});
-    for (int t0 = 0; t0 < ntile; t0 += NSLOT) {
-        static_for<NSLOT>([&](auto sc) __attribute__((always_inline)) {
-            constexpr int S = decltype(sc)::value;
-            const int t = t0 + S;
-            if (t < ntile) {  // uniform over the workgroup
-                if (t + 1 < ntile) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-                else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-                v_transpose(sc);
-                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-                if (t + 2 < ntile) load_tile(t + 2, std::integral_constant<int, (S + 2) % NSLOT>{});
-                process(t, sc);
-            }
-        });
+    auto run = [&](auto exact_c) __attribute__((always_inline)) {
+        constexpr bool EXACT = decltype(exact_c)::value;
+        bool redo = false;
+        load_tile(0, std::integral_constant<int, 0>{});
+        if (1 < ntile) load_tile(1, std::integral_constant<int, 1>{});
+        for (int t0 = 0; t0 < ntile; t0 += NSLOT) {
+            static_for<NSLOT>([&](auto sc) __attribute__((always_inline)) {
+                constexpr int S = decltype(sc)::value;
+                const int t = t0 + S;
+                if (t < ntile) {  // uniform over the workgroup
+                    if (t + 1 < ntile) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+                    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                    if constexpr (!EXACT) v_transpose(sc);
+                    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                    if constexpr (BF16 && !EXACT) {
+                        const uint64_t wf = *reinterpret_cast<const uint64_t*>(lds.wide[S]);
+                        redo |= (__builtin_amdgcn_readfirstlane((uint32_t)wf) |
+                                 __builtin_amdgcn_readfirstlane((uint32_t)(wf >> 32))) != 0;
+                    }
+                    if (t + 2 < ntile) load_tile(t + 2, std::integral_constant<int, (S + 2) % NSLOT>{});
+                    process(t, sc, exact_c);
+                }
+            });
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        return redo;
+    };
+    if (run(std::false_type{})) {
+        if constexpr (BF16) {
+            __syncthreads();  // every wave is past its last read of the ring
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[m][i] = 0.0f;
+            m_run = kNegInf;
+            m_thr = kNegInf;
+            l_part = 0.0f;
+            run(std::true_type{});
+        }
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     // ---- normalise and store: lane holds rows 8b + 4h + i, dims 32m + c32
     {
