@@ -314,6 +314,65 @@ def bench_prefill(args, torch, capi, dev):
     return dict(ms=ms, med=med, tflops=tflops, flops=flops, n=n)
 
 
+def bench_paged_prefill(args, torch, capi, dev):
+    """Chunked prefill over the paged cache: a 2048-token chunk of one
+    sequence over a 30720-token cached prefix, 32/8 heads, fp16 q, q8_0
+    pages (vmc_flash_attention_prefill_v2).  Four sets of pages + q + out
+    (~105 MB each) rotate past the last-level cache.  The per-token path
+    (vmc_paged_attention_prefill: one decode row per token) is timed on the
+    same input for comparison."""
+    prefix, new, Hq, Hkv = 30720, 2048, 32, 8
+    L = prefix + new
+    E = capi.kv_entry_bytes(capi.KV_Q8_0, D)
+    nblk = L // BS
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(9)
+    nset = 4
+    sets = []
+    for _ in range(nset):
+        kc = torch.randint(-127, 128, (nblk * BS * Hkv * E,), generator=gen, device=dev,
+                           dtype=torch.int8).view(torch.uint8)
+        vc = torch.randint(-127, 128, (nblk * BS * Hkv * E,), generator=gen, device=dev,
+                           dtype=torch.int8).view(torch.uint8)
+        # every 34-byte block's fp16 scale := 1/64 (0x2400), so values are moderate
+        for c in (kc, vc):
+            c.view(-1, 34)[:, 0] = 0x00
+            c.view(-1, 34)[:, 1] = 0x24
+        q = torch.randn((new, Hq, D), generator=gen, device=dev).half()
+        sets.append((q, torch.empty_like(q), kc, vc))
+    perm = torch.randperm(nblk, generator=torch.Generator().manual_seed(9)).to(torch.int32)
+    bt = perm.view(1, -1).to(dev)
+    tok_seq = torch.zeros(new, dtype=torch.int32, device=dev)
+    tok_pos = torch.arange(prefix, L, dtype=torch.int32, device=dev)
+    scale = 1.0 / math.sqrt(D)
+    stream = torch.cuda.current_stream()
+
+    def run(i):
+        q, out, kc, vc = sets[i % nset]
+        capi.flash_attention_prefill_v2(out, q, kc, vc, bt, tok_seq, tok_pos, Hkv, scale, block_size=BS,
+                                        kv_format=capi.KV_Q8_0, stream=stream)
+
+    n = max(20, args.steps)
+    ms, med = time_loop(torch, run, n, max(2, args.warmup // 2), stream)
+    flops = 4.0 * Hq * D * (new * prefix + new * (new + 1) / 2)
+    tflops = flops / (ms * 1e-3) / 1e12
+    assert all(torch.isfinite(st[1].float()).all().item() for st in sets), "paged prefill produced non-finite values"
+    ws = torch.empty(capi.paged_decode_workspace_size(new, Hq, Hkv, D, nblk, BS, 8), dtype=torch.uint8,
+                     device=dev)
+
+    def rows(i):
+        q, out, kc, vc = sets[i % nset]
+        capi.paged_attention_prefill(out, q, kc, vc, bt, tok_seq, tok_pos, Hkv, scale, block_size=BS,
+                                     kv_format=capi.KV_Q8_0, workspace=ws, max_splits=8, stream=stream)
+
+    ms_rows, _ = time_loop(torch, rows, 3, 1, stream)
+    log(f"paged prefill {ms * 1e3:.1f} us (median {med * 1e3:.1f}), {tflops:.1f} TFLOP/s; "
+        f"per-token path {ms_rows * 1e3:.1f} us")
+    del sets
+    torch.cuda.empty_cache()
+    return dict(ms=ms, med=med, tflops=tflops, flops=flops, n=n, ms_rows=ms_rows)
+
+
 # ------------------------------------------------------------------ fused norm + RoPE + append
 
 def bench_fused_norm_rope(args, torch, capi, dev):
@@ -537,7 +596,7 @@ def main():
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--skip-variant", action="store_true",
                     help="skip the per-32-group 3-bit variant's decode (turboquant_3bit_g32)")
-    ap.add_argument("--only", choices=("decode", "prefill", "fused", "configs"),
+    ap.add_argument("--only", choices=("decode", "prefill", "paged_prefill", "fused", "configs"),
                     help="profiling runs: only this part (decode: the headline operator; configs: "
                          "the other decode configurations), one JSON line of its numbers")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -570,6 +629,8 @@ def main():
                  "attn_bytes": r["attn_bytes"]}
         elif args.only == "prefill":
             r = bench_prefill(args, torch, capi, dev)
+        elif args.only == "paged_prefill":
+            r = bench_paged_prefill(args, torch, capi, dev)
         elif args.only == "fused":
             r = bench_fused_norm_rope(args, torch, capi, dev)
         else:
@@ -595,6 +656,7 @@ def main():
                                     ("tq4_32x8192", "g32_4bit_32x8192", "q8_0_batch16"))
     others = [bench_decode_cfg(args, torch, capi, dev, k) for k in kinds]
     pre = None if args.skip_prefill else bench_prefill(args, torch, capi, dev)
+    paged = None if args.skip_prefill else bench_paged_prefill(args, torch, capi, dev)
     fused = None if args.skip_prefill else bench_fused_norm_rope(args, torch, capi, dev)
     ceiling = bench_hbm_ceiling(torch, dev)
     cpu = None
@@ -649,6 +711,14 @@ def main():
                            "ms": round(pre["ms"], 4), "ms_median": round(pre["med"], 4),
                            "launches_timed": pre["n"], "tflops": round(pre["tflops"], 1),
                            "pct_peak_mfma_bf16": round(100 * pre["tflops"] / MFMA_BF16_PEAK_TFLOPS, 2)}
+    if paged is not None:
+        line["paged_prefill"] = {
+            "workload": "chunked prefill: 2048-token chunk over a 30720-token cached prefix, Hq=32 Hkv=8, "
+                        "fp16 q, q8_0 pages (flash_attention_prefill_v2)",
+            "ms": round(paged["ms"], 4), "ms_median": round(paged["med"], 4), "launches_timed": paged["n"],
+            "tflops": round(paged["tflops"], 1),
+            "pct_peak_mfma_fp16": round(100 * paged["tflops"] / MFMA_BF16_PEAK_TFLOPS, 2),
+            "ms_per_token_path": round(paged["ms_rows"], 3)}
     if fused is not None:
         line["fused_norm_rope"] = {
             "workload": "q/k RMSNorm + neox RoPE + q8_0 K/V append, 16384 tokens, Hq=32 Hkv=8 bf16",

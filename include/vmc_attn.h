@@ -163,6 +163,35 @@ int vmc_paged_attention_prefill(void* out, const void* query, const void* key_ca
                                 void* workspace, size_t workspace_bytes, vmc_stream_t stream);
 
 /*
+ * Tiled MFMA prefill over the paged cache (chunked prefill: this step's
+ * tokens, already appended, attend a cached prefix plus themselves).
+ * Replaces vm_c::flash_attention_prefill_v2 (include/vm_c/cuda/
+ * kernels_flash_attn.h:46-66, src/cuda/flash_attn_v2_kernels.cu:194-250;
+ * called from PagedAttentionBackend::forward_prefill,
+ * src/model/attention_backend.cpp:44-64).  Token t is position
+ * token_positions[t] of sequence token_to_seq[t] and attends that sequence's
+ * positions 0 .. token_positions[t] through its block_tables row
+ * [num_reqs][max_num_blocks_per_req]; pages with a negative entry are
+ * skipped; a token whose sequence is outside [0, num_reqs) or whose position
+ * is negative gets zeros.  seq_lens is not read (the positions bound the
+ * keys) and may be NULL.  A workgroup takes 32-row blocks of up to 4 query
+ * heads of one KV head and streams 64-key tiles of the sequence's pages
+ * through LDS once for all of them; rows of several sequences in one block
+ * are processed one sequence at a time.  kv_format: VMC_KV_F16, VMC_KV_BF16
+ * (load-to-LDS rows), VMC_KV_Q8_0, VMC_KV_Q4_0 (dequantized to fp16 as
+ * vmc_paged_attention_decode does); q_dtype VMC_DTYPE_F16 / VMC_DTYPE_BF16,
+ * rounded to the page type when they differ (q8_0 / q4_0: fp16).  Limits:
+ * head_dim 128, block_size 16, pools 16-byte aligned.  No workspace.
+ */
+int vmc_flash_attention_prefill_v2(void* out, const void* query, const void* key_cache,
+                                   const void* value_cache, int num_tokens, int num_heads,
+                                   int num_kv_heads, int head_dim, float scale, int block_size,
+                                   int max_num_blocks_per_req, const int32_t* block_tables,
+                                   const int32_t* seq_lens, const int32_t* token_to_seq,
+                                   const int32_t* token_positions, int num_reqs, int q_dtype,
+                                   int kv_format, int layout, vmc_stream_t stream);
+
+/*
  * Quantize-on-append of K/V into packed TurboQuant slots.
  * Replaces vm_c::turboquant_store (kernels_turboquant.h:107-119;
  * turboquant_kernels.cu:792-860).  key/value [num_tokens][num_kv_heads]

@@ -20,7 +20,8 @@ EXPORTS = [
     "vmc_kv_entry_bytes", "vmc_reshape_and_cache", "vmc_paged_decode_workspace_size",
     "vmc_paged_attention_decode", "vmc_tq_config_from_method", "vmc_tq_host_tables",
     "vmc_turboquant_store", "vmc_turboquant_decode_workspace_size",
-    "vmc_turboquant_decode_attention", "vmc_flash_attention_prefill", "vmc_selftest",
+    "vmc_turboquant_decode_attention", "vmc_flash_attention_prefill",
+    "vmc_flash_attention_prefill_v2", "vmc_selftest",
     "vmc_version",
 ]
 
@@ -63,6 +64,9 @@ def load():
     L.vmc_paged_attention_prefill.restype = _I
     L.vmc_paged_attention_prefill.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _P, _P, _P,
                                               _I, _I, _I, _I, _P, _SZ, _P]
+    L.vmc_flash_attention_prefill_v2.restype = _I
+    L.vmc_flash_attention_prefill_v2.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _P, _P, _P,
+                                                 _P, _I, _I, _I, _I, _P]
     L.vmc_turboquant_prefill_attention.restype = _I
     L.vmc_turboquant_prefill_attention.argtypes = [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I64,
                                                    _I64, C.POINTER(TQConfig), _I, _I, _P, _SZ, _P]
@@ -291,6 +295,22 @@ def paged_attention_prefill(out, query, key_cache, value_cache, block_tables, to
         _dtype_code(query), kv_format, layout, max_splits, _ptr(workspace),
         0 if workspace is None else workspace.numel() * workspace.element_size(), _stream(stream))
     _check(rc, "vmc_paged_attention_prefill")
+    return out
+
+
+def flash_attention_prefill_v2(out, query, key_cache, value_cache, block_tables, token_to_seq,
+                               token_positions, num_kv_heads, scale, block_size=16, kv_format=KV_F16,
+                               layout=LAYOUT_NHD, seq_lens=None, stream=None):
+    """Tiled MFMA prefill over the paged cache: token t attends positions
+    0 .. token_positions[t] of sequence token_to_seq[t] (block_tables
+    [num_reqs][max_blocks]); query/out [T][Hq][D]."""
+    T, Hq, D = query.shape
+    num_reqs, max_blocks = block_tables.shape
+    rc = load().vmc_flash_attention_prefill_v2(
+        _ptr(out), _ptr(query), _ptr(key_cache), _ptr(value_cache), T, Hq, num_kv_heads, D, scale,
+        block_size, max_blocks, _ptr(block_tables), _ptr(seq_lens), _ptr(token_to_seq),
+        _ptr(token_positions), num_reqs, _dtype_code(query), kv_format, layout, _stream(stream))
+    _check(rc, "vmc_flash_attention_prefill_v2")
     return out
 
 

@@ -1,4 +1,5 @@
-// kv_quant.hpp -- GGUF block encoders shared by the append and prefill kernels.
+// kv_quant.hpp -- GGUF block encoders shared by the append and prefill
+// kernels, and the block decoders shared by the decode and prefill kernels.
 //
 // encode_q8_0: ggml/src/ggml-quants.c:234-257 (quantize_row_q8_0_ref)
 //   d = amax/127, id = d ? 1/d : 0, q = roundf(x*id), d stored as fp16.
@@ -114,6 +115,23 @@ __device__ __forceinline__ int64_t kv_entry_offset(int64_t slot, int h, int64_t 
     const int64_t blk = slot / bs, off = slot % bs;
     return hnd ? blk * stride + (int64_t)h * bs * E + off * E
                : blk * stride + off * Hkv * E + (int64_t)h * E;
+}
+
+// Two GGUF values -> packed fp16 x * d, bit-identical to fp16(float(x) * d):
+// x * d is exact in fp32 (8-bit x, 11-bit d), and v_pk_mul_f16 rounds the
+// exact product once, as the conversion does.  x enters as fp16 exactly: the
+// two bytes spread into the 16-bit halves, then 0x64 in the high byte makes
+// 1024 + low byte; q8_0 flips the sign bit first (1024 + x + 128 - 1152 = x),
+// q4_0 takes a nibble (1024 + u - 1032 = u - 8).
+__device__ __forceinline__ uint32_t q8_pair_f16(uint32_t w16, f16x2 d2) {
+    const uint32_t t = __builtin_amdgcn_perm(0u, w16, 0x0c010c00u) ^ 0x64806480u;
+    const f16x2 x = __builtin_bit_cast(f16x2, t) - f16x2{(_Float16)1152.0f, (_Float16)1152.0f};
+    return __builtin_bit_cast(uint32_t, x * d2);
+}
+__device__ __forceinline__ uint32_t q4_pair_f16(uint32_t w16, int sh, f16x2 d2) {
+    const uint32_t t = ((__builtin_amdgcn_perm(0u, w16, 0x0c010c00u) >> sh) & 0x000f000fu) | 0x64006400u;
+    const f16x2 x = __builtin_bit_cast(f16x2, t) - f16x2{(_Float16)1032.0f, (_Float16)1032.0f};
+    return __builtin_bit_cast(uint32_t, x * d2);
 }
 
 }  // namespace vmc

@@ -39,6 +39,7 @@
 // q_rot = H q is a Walsh-Hadamard transform done in registers (the order the
 // oracle and the store kernel share).
 #include "decode_plan.hpp"
+#include "kv_quant.hpp"
 
 #include <mutex>
 #include <utility>
@@ -101,22 +102,6 @@ __device__ __forceinline__ uint16_t fp8_f16_bits(uint32_t b, int e4b15) {
     const uint32_t h = !e4b15 ? (mag ? (mag << 7) + 0x2000u : 0u)
                               : ((mag >> 3) ? (mag << 7) : (m ? 0x200u + (m << 6) : 0u));
     return (uint16_t)(h | ((b & 0x80u) << 8));
-}
-// Two GGUF values -> packed fp16 x * d, bit-identical to fp16(float(x) * d):
-// x * d is exact in fp32 (8-bit x, 11-bit d), and v_pk_mul_f16 rounds the
-// exact product once, as the conversion does.  x enters as fp16 exactly: the
-// two bytes spread into the 16-bit halves, then 0x64 in the high byte makes
-// 1024 + low byte; q8_0 flips the sign bit first (1024 + x + 128 - 1152 = x),
-// q4_0 takes a nibble (1024 + u - 1032 = u - 8).
-__device__ __forceinline__ uint32_t q8_pair_f16(uint32_t w16, f16x2 d2) {
-    const uint32_t t = __builtin_amdgcn_perm(0u, w16, 0x0c010c00u) ^ 0x64806480u;
-    const f16x2 x = __builtin_bit_cast(f16x2, t) - f16x2{(_Float16)1152.0f, (_Float16)1152.0f};
-    return __builtin_bit_cast(uint32_t, x * d2);
-}
-__device__ __forceinline__ uint32_t q4_pair_f16(uint32_t w16, int sh, f16x2 d2) {
-    const uint32_t t = ((__builtin_amdgcn_perm(0u, w16, 0x0c010c00u) >> sh) & 0x000f000fu) | 0x64006400u;
-    const f16x2 x = __builtin_bit_cast(f16x2, t) - f16x2{(_Float16)1032.0f, (_Float16)1032.0f};
-    return __builtin_bit_cast(uint32_t, x * d2);
 }
 // Codes 2e and 2e+1 of an 8-code word of the per-32-group variant -> packed
 // fp16 code * d + m (4-bit, one fused rounding) or (code - 4) * d (3-bit,

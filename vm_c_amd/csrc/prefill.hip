@@ -41,8 +41,14 @@ constexpr int kD = 128;
 constexpr int NW = 8;      // waves per workgroup (32 query rows each)
 constexpr int BN = 64;     // kv rows per tile
 constexpr int NSLOT = 3;   // K/V tile slots in LDS
+constexpr int kBsP = 16;   // tokens per page (paged sources)
 constexpr float kNegInf = -__builtin_inff();
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// K/V sources of the kernel: this step's contiguous rows, or the paged cache
+// (f16 / bf16 pages by load-to-LDS transfers; q8_0 / q4_0 pages dequantized
+// to fp16 through registers)
+constexpr int SRC_LOCAL = 0, SRC_PAGED = 1, SRC_Q8 = 2, SRC_Q4 = 3;
 
 struct PrefillParams {
     uint16_t* out;
@@ -50,6 +56,14 @@ struct PrefillParams {
     const uint16_t* k;
     const uint16_t* v;
     const int32_t* pos;
+    // paged sources: pools, block tables [seq][max_blocks], token -> sequence
+    const uint8_t* kp;
+    const uint8_t* vp;
+    const int32_t* bt;
+    const int32_t* tok_seq;
+    int64_t max_blocks, page_bytes;
+    int num_seqs;        // rows of a sequence outside [0, num_seqs) get no keys
+    int q_bf16;          // paged: q / out are bf16 (else fp16)
     int T, Hq, Hkv, G;
     float scale_log2;
     int ntiles;          // query blocks of qb rows
@@ -115,15 +129,24 @@ struct PrefillLds {
 
 __device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
+__device__ __forceinline__ int wave_max_int(int v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = max(v, __shfl_xor(v, m, kWave));
+    return v;
+}
+
 // Workgroup = 8 waves = hw query heads of one KV head x rb blocks of 32
 // query rows (hw * rb = 8): every K/V tile in LDS serves 256 query rows,
 // which halves the tile traffic from L2 against 4-wave, one-head
 // workgroups.  Grid: query block (largest first) x KV head x head group.
-template <bool BF16, int APPEND_FMT>
+// BF16 is the type of the S MFMA and of V (paged: the page type; q8_0 /
+// q4_0 pages dequantize to fp16).
+template <bool BF16, int APPEND_FMT, int SRC>
 __global__ void __launch_bounds__(512, 1)
 prefill_kernel(PrefillParams p) {
     using M = MT<BF16>;
     using V8 = typename M::v8;
+    constexpr bool kPaged = SRC != SRC_LOCAL;
     __shared__ PrefillLds lds;
 
     const int tid = threadIdx.x;
@@ -136,27 +159,36 @@ prefill_kernel(PrefillParams p) {
     const int hq = g * p.G + hgrp * p.hw + w / p.rb;  // this wave's query head
     const int T = p.T;
     const int q0 = qblk * p.qb;
+    const int q_end = min(q0 + p.qb, T);
+    // q / out dtype: the MFMA type for local rows, the caller's for pages
+    const bool qbf = kPaged ? p.q_bf16 != 0 : BF16;
 
-    // kv range of the whole workgroup
-    const int kv_lo = max(0, q0 - p.pos[q0]);
-    const int kv_end = min(q0 + p.qb, T);
-    const int ntile = (kv_end - kv_lo + BN - 1) / BN;
-
-    // this lane's query row and its key window [lo, row]
+    // this lane's query row
     const int wr = 32 * (w % p.rb);  // this wave's rows: q0 + wr .. +31
     const int row = q0 + wr + c32;
     const bool row_ok = row < T;
-    const int lo = row_ok ? row - p.pos[row] : 0;
-    // wave-uniform bounds
     const int wrow0 = q0 + wr;
-    const bool wave_ok = wrow0 < T;
-    const int wrow1 = min(wrow0 + 31, T - 1);
-    const int wlo0 = wave_ok ? wrow0 - p.pos[wrow0] : 0;
-    const int wlo1 = wave_ok ? wrow1 - p.pos[wrow1] : 0;
+
+    // pass state: the workgroup's kv range [kv_lo, kv_end) in ntile tiles,
+    // this lane's key window [lo, hi] (hi < 0: none) and the wave's bounds of
+    // both; rows [cur, rend) are the pass's.  Local rows: one pass, kv index =
+    // token index, window [row - pos(row), row].  Pages: one pass per
+    // sequence among the workgroup's rows, kv index = position, window
+    // [0, pos(row)] through that sequence's block table.
+    int kv_lo = 0, kv_end = 0, ntile = 0, lo = 0, hi = -1;
+    int wlo_min = 0, wlo_max = 0, whi_min = -1, whi_max = -1;
+    int cur = q0, rend = q_end;
+    // block-table row of the pass's sequence, read through the constant
+    // address space so that wave-uniform lookups are scalar loads (a vector
+    // load would need a vmcnt wait, which also waits for the tile transfers)
+    using cint = const __attribute__((address_space(4))) int32_t;
+    cint* bt_row = (cint*)p.bt;
+    int last_page = 0;
 
     // ---- Q^T operand: lane (col = row, half h) holds dims 16s + 8h .. +7.
     // A negative scale flips Q's sign bits (exact) so that c = |scale| log2 e
-    // is positive and the largest raw score is the largest scaled one.
+    // is positive and the largest raw score is the largest scaled one.  Paged
+    // q of the other half type is rounded to the MFMA type.
     const float csc = fabsf(p.scale_log2);
     const uint32_t qflip = p.scale_log2 < 0.0f ? 0x80008000u : 0u;
     V8 qb[8];
@@ -166,6 +198,17 @@ prefill_kernel(PrefillParams p) {
         for (int s = 0; s < 8; ++s) {
             u32x4 wv = {0u, 0u, 0u, 0u};
             if (row_ok) wv = *reinterpret_cast<const u32x4*>(qp + 16 * s);
+            if constexpr (kPaged) {
+                if (qbf != BF16) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float f0 = qbf ? __builtin_bit_cast(float, wv[e] << 16) : f16_bits_to_f32(wv[e] & 0xffff);
+                        const float f1 = qbf ? __builtin_bit_cast(float, wv[e] & 0xffff0000u) : f16_bits_to_f32(wv[e] >> 16);
+                        wv[e] = BF16 ? ((uint32_t)f32_to_bf16_bits(f0) | ((uint32_t)f32_to_bf16_bits(f1) << 16))
+                                     : ((uint32_t)f32_to_f16_bits(f0) | ((uint32_t)f32_to_f16_bits(f1) << 16));
+                    }
+                }
+            }
             qb[s] = as_v8<V8>(u32x4{wv[0] ^ qflip, wv[1] ^ qflip, wv[2] ^ qflip, wv[3] ^ qflip});
         }
     }
@@ -187,6 +230,19 @@ prefill_kernel(PrefillParams p) {
     const int64_t row_stride = (int64_t)p.Hkv * kD * 2;  // bytes between kv rows
     const uint8_t* kg = reinterpret_cast<const uint8_t*>(p.k) + (int64_t)g * kD * 2 + ld_col;
     const uint8_t* vg = reinterpret_cast<const uint8_t*>(p.v) + (int64_t)g * kD * 2 + ld_col;
+    // pages: the 4 rows a 16-lane group covers lie in one page, so round i's
+    // page is wave-uniform (a scalar block-table read); a hole reads page 0
+    // and its keys are masked
+    const int wu = __builtin_amdgcn_readfirstlane(w);
+    auto page_at = [&](int k) __attribute__((always_inline)) {
+        const int32_t pg = bt_row[min(k >> 4, last_page)];
+        return max(pg, 0);
+    };
+    // byte offset of kv row k (< kv_end) inside its page
+    auto row_in_page = [&](int k) __attribute__((always_inline)) {
+        const int r = k & (kBsP - 1);
+        return p.hnd ? (int64_t)(g * kBsP + r) * p.E : (int64_t)(r * p.Hkv + g) * p.E;
+    };
     auto load_tile = [&](int t, auto slot_c) __attribute__((always_inline)) {
         constexpr int SL = decltype(slot_c)::value;
         const int k0 = kv_lo + t * BN;
@@ -194,9 +250,73 @@ prefill_kernel(PrefillParams p) {
         for (int i = 0; i < 2; ++i) {
             // rows past the range re-read the last row (masked later)
             const int kk = min(k0 + 32 * i + ld_row, kv_end - 1);
-            const int64_t off = (int64_t)kk * row_stride;
-            dma16(kg + off, &lds.tile[SL][0][1024 * (8 * i + w)]);
-            dma16(vg + off, &lds.tile[SL][1][1024 * (8 * i + w)]);
+            if constexpr (SRC == SRC_LOCAL) {
+                const int64_t off = (int64_t)kk * row_stride;
+                dma16(kg + off, &lds.tile[SL][0][1024 * (8 * i + w)]);
+                dma16(vg + off, &lds.tile[SL][1][1024 * (8 * i + w)]);
+            } else {
+                const int64_t off = (int64_t)page_at(min(k0 + 32 * i + 4 * wu, kv_end - 1)) * p.page_bytes +
+                                    row_in_page(kk) + ld_col;
+                dma16(p.kp + off, &lds.tile[SL][0][1024 * (8 * i + w)]);
+                dma16(p.vp + off, &lds.tile[SL][1][1024 * (8 * i + w)]);
+            }
+        }
+    };
+    // q8_0 / q4_0 pages: lane L of wave w holds 32-dim block L & 3 of row
+    // 32 (r >> 2) + 4 w + (r & 3), r = (L >> 2) & 7, of K (L < 32) or V --
+    // the rows whose V this wave transposes -- as the block's bytes read
+    // from their 4-byte floor (a block is 2-byte aligned; the read stays in
+    // the entry)
+    constexpr int kBE = SRC == SRC_Q8 ? 34 : 18;        // block bytes
+    constexpr int kNW = SRC == SRC_Q8 ? 9 : 5;          // dwords read per block
+    const int qr = 32 * ((lane >> 4) & 1) + 4 * w + ((lane >> 2) & 3);
+    const int qblk_ = lane & 3;
+    uint32_t qraw[kPaged && SRC != SRC_PAGED ? kNW : 1];
+    auto issue_q = [&](int t) __attribute__((always_inline)) {
+        if constexpr (SRC == SRC_Q8 || SRC == SRC_Q4) {
+            const int k0 = kv_lo + t * BN;
+            const int kk = min(k0 + qr, kv_end - 1);
+            const int pg0 = page_at(min(k0 + 4 * wu, kv_end - 1));
+            const int pg1 = page_at(min(k0 + 32 + 4 * wu, kv_end - 1));
+            const int pg = (lane & 16) ? pg1 : pg0;
+            // entries are whole dwords (136 / 72 bytes), so block b starts
+            // 2 (b & 1) bytes past a dword
+            const uint8_t* src = (lane < 32 ? p.kp : p.vp) + (int64_t)pg * p.page_bytes + row_in_page(kk) +
+                                 kBE * qblk_ - 2 * (qblk_ & 1);
+            const uint32_t* w4 = reinterpret_cast<const uint32_t*>(src);
+#pragma unroll
+            for (int i = 0; i < kNW; ++i) qraw[i] = w4[i];
+        }
+    };
+    // dequantize the held block into the K or V tile of slot SL (fp16 rows
+    // in the swizzled layout of the load-to-LDS path)
+    auto store_q = [&](auto slot_c) __attribute__((always_inline)) {
+        if constexpr (SRC == SRC_Q8 || SRC == SRC_Q4) {
+            constexpr int SL = decltype(slot_c)::value;
+            const bool off2 = (qblk_ & 1) != 0;
+            constexpr int NC = SRC == SRC_Q8 ? 8 : 4;  // code dwords
+            uint32_t c[NC];
+#pragma unroll
+            for (int i = 0; i < NC; ++i)
+                c[i] = off2 ? qraw[i + 1] : __builtin_amdgcn_alignbyte(qraw[i + 1], qraw[i], 2);
+            const uint32_t d16 = off2 ? qraw[0] >> 16 : qraw[0] & 0xffffu;
+            const f16x2 d2 = __builtin_bit_cast(f16x2, d16 * 0x10001u);
+            uint8_t* dst = lds.tile[SL][lane >> 5] + qr * 256;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                u32x4 kw;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if constexpr (SRC == SRC_Q8) {
+                        const uint32_t wv = c[2 * j + (e >> 1)];  // values 8j + 2e, +1
+                        kw[e] = q8_pair_f16((e & 1) ? wv >> 16 : wv, d2);
+                    } else {
+                        const uint32_t wv = c[2 * (j & 1) + (e >> 1)];  // byte i: value i | value i+16 << 4
+                        kw[e] = q4_pair_f16((e & 1) ? wv >> 16 : wv, j >= 2 ? 4 : 0, d2);
+                    }
+                }
+                *reinterpret_cast<u32x4*>(dst + 16 * ((4 * qblk_ + j) ^ swz(qr))) = kw;
+            }
         }
     };
 
@@ -220,12 +340,21 @@ prefill_kernel(PrefillParams p) {
         constexpr int SL = decltype(slot_c)::value;
         constexpr bool EXACT = decltype(exact_c)::value;
         const int k0 = kv_lo + t * BN;
-        // skip: tile entirely after this wave's last row, or before its first window
-        const bool active = wave_ok && k0 <= wrow1 && k0 + BN - 1 >= wlo0;
+        // skip: tile entirely after this wave's last key, or before its first window
+        const bool active = k0 <= whi_max && k0 + BN - 1 >= wlo_min;
         if (!active) return;
         const uint8_t* kt = lds.tile[SL][0];
         const uint8_t* vtt = lds.vtr[SL];
-        const bool need_mask = (k0 + BN - 1 > wrow0) || (k0 < wlo1);
+        // pages: bit q set when page q of the tile is a hole (its keys masked)
+        uint32_t holes = 0;
+        if constexpr (kPaged) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int pi = (k0 >> 4) + q;
+                holes |= (pi <= last_page && bt_row[pi] < 0) ? 1u << q : 0u;
+            }
+        }
+        const bool need_mask = (k0 + BN - 1 > whi_min) || (k0 < wlo_max) || holes != 0;
         // ---- S^T = K Q^T, two 32-row kv blocks
         f32x16 sacc[2];
 #pragma unroll
@@ -260,7 +389,7 @@ prefill_kernel(PrefillParams p) {
 #pragma unroll
                 for (int j = 0; j < 16; ++j) {
                     const int kv = k0 + kb * 32 + 8 * (j >> 2) + 4 * h + (j & 3);
-                    const bool ok = kv <= row && kv >= lo && row_ok;
+                    const bool ok = kv <= hi && kv >= lo && !((holes >> (2 * kb + (j >> 3))) & 1u);
                     sacc[kb][j] = ok ? sacc[kb][j] : kNegInf;
                 }
         }
@@ -462,19 +591,30 @@ prefill_kernel(PrefillParams p) {
     // in the exact mode, which skips the V^T pass and multiplies the raw bf16
     // rows.  The pass runs to its end rather than leaving early: an early
     // exit costs the common case registers.
+    // q8_0 / q4_0 pages instead hold the next tile in registers while a
+    // tile runs and dequantize it into its slot before that tile's barrier.
     static_assert(NSLOT == 3, "wait counts below assume three slots");
+    constexpr bool kDma = SRC == SRC_LOCAL || SRC == SRC_PAGED;
     auto run = [&](auto exact_c) __attribute__((always_inline)) {
         constexpr bool EXACT = decltype(exact_c)::value;
         bool redo = false;
-        load_tile(0, std::integral_constant<int, 0>{});
-        if (1 < ntile) load_tile(1, std::integral_constant<int, 1>{});
+        if constexpr (kDma) {
+            load_tile(0, std::integral_constant<int, 0>{});
+            if (1 < ntile) load_tile(1, std::integral_constant<int, 1>{});
+        } else {
+            issue_q(0);
+        }
         for (int t0 = 0; t0 < ntile; t0 += NSLOT) {
             static_for<NSLOT>([&](auto sc) __attribute__((always_inline)) {
                 constexpr int S = decltype(sc)::value;
                 const int t = t0 + S;
                 if (t < ntile) {  // uniform over the workgroup
-                    if (t + 1 < ntile) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-                    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                    if constexpr (kDma) {
+                        if (t + 1 < ntile) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+                        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                    } else {
+                        store_q(sc);
+                    }
                     if constexpr (!EXACT) v_transpose(sc);
                     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
                     if constexpr (BF16 && !EXACT) {
@@ -482,25 +622,89 @@ prefill_kernel(PrefillParams p) {
                         redo |= (__builtin_amdgcn_readfirstlane((uint32_t)wf) |
                                  __builtin_amdgcn_readfirstlane((uint32_t)(wf >> 32))) != 0;
                     }
-                    if (t + 2 < ntile) load_tile(t + 2, std::integral_constant<int, (S + 2) % NSLOT>{});
+                    if constexpr (kDma) {
+                        if (t + 2 < ntile) load_tile(t + 2, std::integral_constant<int, (S + 2) % NSLOT>{});
+                    } else {
+                        if (t + 1 < ntile) issue_q(t + 1);
+                    }
                     process(t, sc, exact_c);
                 }
             });
         }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if constexpr (kDma) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         return redo;
     };
-    if (run(std::false_type{})) {
-        if constexpr (BF16) {
-            __syncthreads();  // every wave is past its last read of the ring
+    auto run_pass = [&]() __attribute__((always_inline)) {
+        if (run(std::false_type{})) {
+            if constexpr (BF16) {
+                __syncthreads();  // every wave is past its last read of the ring
+                // the pass's rows start over: O rows 8b + 4h + i, this lane's row
 #pragma unroll
-            for (int m = 0; m < 4; ++m)
+                for (int b = 0; b < 4; ++b)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) o[m][i] = 0.0f;
-            m_run = kNegInf;
-            m_thr = kNegInf;
-            l_part = 0.0f;
-            run(std::true_type{});
+                    for (int i = 0; i < 4; ++i) {
+                        const int r = wrow0 + 8 * b + 4 * h + i;
+                        if (r >= cur && r < rend) {
+#pragma unroll
+                            for (int m = 0; m < 4; ++m) o[m][4 * b + i] = 0.0f;
+                        }
+                    }
+                if (row >= cur && row < rend) {
+                    m_run = kNegInf;
+                    m_thr = kNegInf;
+                    l_part = 0.0f;
+                }
+                run(std::true_type{});
+            }
+        }
+    };
+
+    if constexpr (SRC == SRC_LOCAL) {
+        kv_lo = max(0, q0 - p.pos[q0]);
+        kv_end = q_end;
+        ntile = (kv_end - kv_lo + BN - 1) / BN;
+        lo = row_ok ? row - p.pos[row] : 0;
+        hi = row_ok ? row : -1;
+        if (wrow0 < T) {  // rows increase, and so do their window starts
+            const int wrow1 = min(wrow0 + 31, T - 1);
+            whi_min = wrow0;
+            whi_max = wrow1;
+            wlo_min = wrow0 - p.pos[wrow0];
+            wlo_max = wrow1 - p.pos[wrow1];
+        }
+        run_pass();
+    } else {
+        // runs of rows of one sequence: every wave scans the workgroup's rows
+        // and finds the same runs
+        while (cur < q_end) {
+            const int sq = p.tok_seq[cur];
+            rend = q_end;
+            int pmax = -1;
+            for (int r0 = cur; r0 < rend; r0 += 64) {
+                const int r = r0 + lane;
+                const int sr = r < rend ? p.tok_seq[r] : sq;
+                const uint64_t diff = __ballot(sr != sq);
+                if (diff) rend = r0 + (int)__builtin_ctzll(diff);
+                pmax = max(pmax, wave_max_int(r < rend ? p.pos[r] : -1));
+            }
+            pmax = __builtin_amdgcn_readfirstlane(pmax);
+            if (sq >= 0 && sq < p.num_seqs && pmax >= 0) {
+                kv_lo = 0;
+                kv_end = pmax + 1;
+                ntile = (kv_end + BN - 1) / BN;
+                bt_row = (cint*)(p.bt + (int64_t)sq * p.max_blocks);
+                last_page = min((kv_end - 1) >> 4, (int)p.max_blocks - 1);
+                const bool in = row_ok && row >= cur && row < rend;
+                hi = in ? p.pos[row] : -1;
+                lo = 0;
+                whi_max = __builtin_amdgcn_readfirstlane(wave_max_int(hi));
+                whi_min = __builtin_amdgcn_readfirstlane(-wave_max_int(-hi));
+                wlo_min = 0;
+                wlo_max = 0;
+                __syncthreads();  // the previous pass's last tiles are read before the ring refills
+                run_pass();
+            }
+            cur = rend;
         }
     }
 
@@ -522,7 +726,10 @@ prefill_kernel(PrefillParams p) {
                 const float inv = l4[i] > 0.0f ? 1.0f / l4[i] : 0.0f;
                 uint16_t* op = p.out + ((int64_t)r * p.Hq + hq) * kD + c32;
 #pragma unroll
-                for (int m = 0; m < 4; ++m) op[32 * m] = M::cvt(o[m][4 * b + i] * inv);
+                for (int m = 0; m < 4; ++m) {
+                    const float x = o[m][4 * b + i] * inv;
+                    op[32 * m] = qbf ? f32_to_bf16_bits(x) : f32_to_f16_bits(x);
+                }
             }
         }
     }
@@ -547,9 +754,9 @@ prefill_kernel(PrefillParams p) {
     }
 }
 
-template <bool BF16, int FMT>
+template <bool BF16, int FMT, int SRC = SRC_LOCAL>
 int launch_prefill(PrefillParams& prm, hipStream_t stream) {
-    auto kern = prefill_kernel<BF16, FMT>;
+    auto kern = prefill_kernel<BF16, FMT, SRC>;
     const int64_t grid = (int64_t)prm.ntiles * prm.Hkv * prm.hgroups;
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * NW), 0, stream, prm);
     VMC_LAUNCH_CHECK();
@@ -568,10 +775,72 @@ int dispatch_fmt(PrefillParams& prm, int fmt, hipStream_t s) {
     }
 }
 
+// workgroup shape shared by the local and paged entry points
+void set_tiling(PrefillParams& prm, int num_tokens, int num_heads, int num_kv_heads, float scale) {
+    prm.T = num_tokens;
+    prm.Hq = num_heads;
+    prm.Hkv = num_kv_heads;
+    prm.G = num_heads / num_kv_heads;
+    prm.scale_log2 = scale * kLog2e;
+    // heads per workgroup: 4, 2 or 1, dividing G; 32-row blocks per head fill 8 waves
+    prm.hw = prm.G % 4 == 0 ? 4 : (prm.G % 2 == 0 ? 2 : 1);
+    prm.rb = NW / prm.hw;
+    prm.qb = 32 * prm.rb;
+    prm.hgroups = prm.G / prm.hw;
+    prm.ntiles = (num_tokens + prm.qb - 1) / prm.qb;
+}
+
 }  // namespace
 }  // namespace vmc
 
 using namespace vmc;
+
+extern "C" int vmc_flash_attention_prefill_v2(void* output, const void* query, const void* key_cache,
+                                              const void* value_cache, int num_tokens, int num_heads,
+                                              int num_kv_heads, int head_dim, float scale, int block_size,
+                                              int max_num_blocks_per_req, const int32_t* block_tables,
+                                              const int32_t* seq_lens, const int32_t* token_to_seq,
+                                              const int32_t* token_positions, int num_reqs, int q_dtype,
+                                              int kv_format, int layout, vmc_stream_t stream) {
+    (void)seq_lens;  // a token's keys are positions 0 .. token_positions[t]
+    if (head_dim != kD || block_size != kBsP || num_tokens < 0 || num_heads <= 0 || num_kv_heads <= 0 ||
+        num_heads % num_kv_heads != 0 || max_num_blocks_per_req <= 0 || num_reqs < 0)
+        return VMC_EINVAL;
+    if (q_dtype != VMC_DTYPE_F16 && q_dtype != VMC_DTYPE_BF16) return VMC_EINVAL;
+    if (layout != VMC_LAYOUT_NHD && layout != VMC_LAYOUT_HND) return VMC_EINVAL;
+    if (kv_format != VMC_KV_F16 && kv_format != VMC_KV_BF16 && kv_format != VMC_KV_Q8_0 &&
+        kv_format != VMC_KV_Q4_0)
+        return VMC_EINVAL;
+    if (num_tokens == 0 || num_reqs == 0) return VMC_OK;
+    if (!output || !query || !key_cache || !value_cache || !block_tables || !token_to_seq ||
+        !token_positions)
+        return VMC_EINVAL;
+    // pages are read in 16-byte (f16 / bf16) and 4-byte (q8_0 / q4_0) units
+    if ((((uintptr_t)key_cache | (uintptr_t)value_cache) & 15) != 0) return VMC_EINVAL;
+    PrefillParams prm = {};
+    prm.out = reinterpret_cast<uint16_t*>(output);
+    prm.q = reinterpret_cast<const uint16_t*>(query);
+    prm.pos = token_positions;
+    set_tiling(prm, num_tokens, num_heads, num_kv_heads, scale);
+    prm.kp = reinterpret_cast<const uint8_t*>(key_cache);
+    prm.vp = reinterpret_cast<const uint8_t*>(value_cache);
+    prm.bt = block_tables;
+    prm.tok_seq = token_to_seq;
+    prm.max_blocks = max_num_blocks_per_req;
+    prm.num_seqs = num_reqs;
+    prm.E = vmc_kv_entry_bytes(kv_format, head_dim);
+    prm.page_bytes = (int64_t)kBsP * num_kv_heads * prm.E;
+    prm.hnd = layout == VMC_LAYOUT_HND;
+    prm.q_bf16 = q_dtype == VMC_DTYPE_BF16;
+    if ((int64_t)prm.ntiles * prm.Hkv * prm.hgroups > 0x7fffffffLL) return VMC_EINVAL;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    switch (kv_format) {
+        case VMC_KV_F16: return launch_prefill<false, -1, SRC_PAGED>(prm, s);
+        case VMC_KV_BF16: return launch_prefill<true, -1, SRC_PAGED>(prm, s);
+        case VMC_KV_Q8_0: return launch_prefill<false, -1, SRC_Q8>(prm, s);
+        default: return launch_prefill<false, -1, SRC_Q4>(prm, s);
+    }
+}
 
 extern "C" int vmc_flash_attention_prefill(void* output, const void* query, const void* key,
                                            const void* value, int num_tokens, int num_heads,
@@ -592,17 +861,7 @@ extern "C" int vmc_flash_attention_prefill(void* output, const void* query, cons
     prm.k = reinterpret_cast<const uint16_t*>(key);
     prm.v = reinterpret_cast<const uint16_t*>(value);
     prm.pos = token_positions;
-    prm.T = num_tokens;
-    prm.Hq = num_heads;
-    prm.Hkv = num_kv_heads;
-    prm.G = num_heads / num_kv_heads;
-    prm.scale_log2 = scale * kLog2e;
-    // heads per workgroup: 4, 2 or 1, dividing G; 32-row blocks per head fill 8 waves
-    prm.hw = prm.G % 4 == 0 ? 4 : (prm.G % 2 == 0 ? 2 : 1);
-    prm.rb = NW / prm.hw;
-    prm.qb = 32 * prm.rb;
-    prm.hgroups = prm.G / prm.hw;
-    prm.ntiles = (num_tokens + prm.qb - 1) / prm.qb;
+    set_tiling(prm, num_tokens, num_heads, num_kv_heads, scale);
     int fmt = -1;
     if (key_cache) {
         const int64_t E = vmc_kv_entry_bytes(kv_format, head_dim);

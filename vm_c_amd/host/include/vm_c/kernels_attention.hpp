@@ -61,6 +61,20 @@ void paged_attention_prefill(void* out, const void* query, const void* key_cache
                              const std::string& kv_cache_dtype, ScalarType dtype,
                              hipStream_t stream = nullptr, const std::string& layout = "nhd");
 
+// Tiled MFMA prefill over the paged cache (chunked prefill), the same
+// semantics as paged_attention_prefill with every K/V tile of a sequence
+// read once per block of query rows instead of once per token
+// (kernels_flash_attn.h:46-66).  kv_cache_dtype "auto", "fp16", "bf16",
+// "q8_0", "q4_0"; head_dim 128, block_size 16.  No workspace.
+void flash_attention_prefill_v2(void* output, const void* query, const void* key_cache,
+                                const void* value_cache, int num_tokens, int num_heads,
+                                int num_kv_heads, int head_dim, float scale, int64_t block_size,
+                                int64_t max_num_blocks_per_req, const int32_t* block_tables,
+                                const int32_t* seq_lens, const int32_t* token_to_seq,
+                                const int32_t* token_positions, int num_reqs,
+                                const std::string& kv_cache_dtype, ScalarType dtype,
+                                hipStream_t stream = nullptr, const std::string& layout = "nhd");
+
 // One pass per sequence (no split, no workspace): one workgroup per request.
 void paged_attention_v1(void* out, const void* query, const void* key_cache,
                         const void* value_cache, const AttentionParams& params,

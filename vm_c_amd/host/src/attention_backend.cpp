@@ -49,12 +49,13 @@ void PagedAttentionBackend::forward_prefill(void* output, const void* query, con
                                             hipStream_t stream) {
     if (meta.num_computed_tokens > 0 && meta.num_decode_tokens == 0) {
         // a cached prefix: attend through the pages (store_kv has appended
-        // this step's tokens), as the reference's paged prefill does
-        paged_attention_prefill(output, query, key_cache, value_cache, meta.num_tokens, num_heads,
-                                num_kv_heads, head_dim, scale, block_size, meta.max_num_blocks_per_req,
-                                meta.block_tables, meta.seq_lens, meta.token_to_seq,
-                                meta.token_positions, meta.num_reqs, kv_cache_dtype_, dtype, stream,
-                                kv_cache_layout_);
+        // this step's tokens) with the tiled kernel the reference's
+        // flash_attention_prefill_v2 call stands for
+        flash_attention_prefill_v2(output, query, key_cache, value_cache, meta.num_tokens, num_heads,
+                                   num_kv_heads, head_dim, scale, block_size, meta.max_num_blocks_per_req,
+                                   meta.block_tables, meta.seq_lens, meta.token_to_seq,
+                                   meta.token_positions, meta.num_reqs, kv_cache_dtype_, dtype, stream,
+                                   kv_cache_layout_);
         return;
     }
     require_no_cached_prefix(meta, "PagedAttentionBackend::forward_prefill");

@@ -250,6 +250,22 @@ void paged_attention_prefill(void* out, const void* query, const void* key_cache
                                          1, nullptr, 0, stream));
 }
 
+void flash_attention_prefill_v2(void* output, const void* query, const void* key_cache,
+                                const void* value_cache, int num_tokens, int num_heads,
+                                int num_kv_heads, int head_dim, float scale, int64_t block_size,
+                                int64_t max_num_blocks_per_req, const int32_t* block_tables,
+                                const int32_t* seq_lens, const int32_t* token_to_seq,
+                                const int32_t* token_positions, int num_reqs,
+                                const std::string& kv_cache_dtype, ScalarType dtype,
+                                hipStream_t stream, const std::string& layout) {
+    VMC_CALL(vmc_flash_attention_prefill_v2(output, query, key_cache, value_cache, num_tokens, num_heads,
+                                            num_kv_heads, head_dim, scale, (int)block_size,
+                                            (int)max_num_blocks_per_req, block_tables, seq_lens,
+                                            token_to_seq, token_positions, num_reqs, vmc_dtype_of(dtype),
+                                            vmc_kv_format_of(kv_cache_dtype, dtype), vmc_layout_of(layout),
+                                            stream));
+}
+
 namespace {
 void check_params(const AttentionParams& p, const float* alibi_slopes) {
     if (alibi_slopes) throw std::runtime_error("paged attention: ALiBi is not supported");
