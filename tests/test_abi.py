@@ -118,3 +118,25 @@ def test_null_and_stride_validation_without_gpu():
     assert fused(*args(17407, capi.KV_Q8_0)) == capi.VMC_EINVAL
     # f16 pages are written 16 bytes at a time
     assert fused(*args(16 * 8 * 256 + 8, capi.KV_F16)) == capi.VMC_EINVAL
+
+
+def test_tq_configs_other_head_dims():
+    """head_dim 64 and 256 (TQConfig::kMaxSupportedHeadDim = 256,
+    kernels_turboquant.h:11): slot sizes from compute_layout, the reference's
+    262-byte 4-bit slot at 256 (tp_runtime.cpp:257-261), fp8-key slots of
+    head_dim + head_dim / 2 + 4 bytes, and the host codebooks equal to the
+    oracle's."""
+    from vm_c_amd import capi
+    assert capi.tq_config(256, "turboquant_4bit_nc").slot_size_aligned == 262
+    for d in (64, 256):
+        for m in ("turboquant_4bit_nc", "turboquant_3bit_nc", "turboquant_k3v4_nc", "turboquant_k8v4"):
+            c = capi.tq_config(d, m)
+            L = O.tq_layout(m, d)
+            assert (c.mse_bytes, c.key_packed_size, c.val_data_bytes, c.slot_size_aligned) == \
+                   (L.mse_bytes, L.key_packed_size, L.val_data_bytes, L.slot_size_aligned)
+        assert capi.tq_config(d, "turboquant_k8v4").slot_size_aligned == d + d // 2 + 4
+        for bits in (3, 4):
+            c, m = capi.tq_host_tables(d, bits)
+            oc, om = O.tq_tables(d, bits)
+            assert np.array_equal(c.view(np.uint32), oc.view(np.uint32))
+            assert np.array_equal(m.view(np.uint32), om.view(np.uint32))

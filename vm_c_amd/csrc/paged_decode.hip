@@ -39,6 +39,7 @@
 // q_rot = H q is a Walsh-Hadamard transform done in registers (the order the
 // oracle and the store kernel share).
 #include "decode_plan.hpp"
+#include "generic_attn.hpp"
 #include "kv_quant.hpp"
 
 #include <mutex>
@@ -1362,6 +1363,41 @@ int paged_decode_rows(void* out, const void* query, const void* key_cache, const
                       int head_dim, int block_size, int max_num_blocks_per_req, float scale,
                       int q_dtype, int kv_format, int layout, int max_num_kv_splits, void* workspace,
                       size_t workspace_bytes, vmc_stream_t stream) {
+    if (generic_head_dim(head_dim)) {
+        // head_dim 64 / 256: one wave per (row, query head), no workspace
+        if (batch_size < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 ||
+            block_size <= 0 || max_num_blocks_per_req <= 0)
+            return VMC_EINVAL;
+        if (q_dtype != VMC_DTYPE_F16 && q_dtype != VMC_DTYPE_BF16) return VMC_EINVAL;
+        if (layout != VMC_LAYOUT_NHD && layout != VMC_LAYOUT_HND) return VMC_EINVAL;
+        const int64_t E = vmc_kv_entry_bytes(kv_format, head_dim);
+        if (E < 0) return VMC_EINVAL;
+        if (batch_size == 0) return VMC_OK;
+        if (!out || !query || !block_tables || !key_cache || !value_cache || !seq_lens) return VMC_EINVAL;
+        GenArgs a = {};
+        a.out = out;
+        a.q = query;
+        a.q_bf16 = q_dtype == VMC_DTYPE_BF16;
+        a.src = kv_format == VMC_KV_F16 ? GEN_F16 : kv_format == VMC_KV_BF16 ? GEN_BF16
+              : kv_format == VMC_KV_Q8_0 ? GEN_Q8 : GEN_Q4;
+        a.kp = reinterpret_cast<const uint8_t*>(key_cache);
+        a.vp = reinterpret_cast<const uint8_t*>(value_cache);
+        a.entry = E;
+        a.hnd = layout == VMC_LAYOUT_HND;
+        a.bs = block_size;
+        a.bt = block_tables;
+        a.max_blocks = max_num_blocks_per_req;
+        a.seq_lens = seq_lens;
+        a.tok_seq = row_seq;
+        a.pos = row_pos;
+        a.num_seqs = -1;
+        a.rows = batch_size;
+        a.Hq = num_heads;
+        a.Hkv = num_kv_heads;
+        a.D = head_dim;
+        a.scale = scale;
+        return gen_attention(a, reinterpret_cast<hipStream_t>(stream));
+    }
     DecodeParams prm = {};
     int rc = setup_common(prm, out, query, block_tables, seq_lens, batch_size, num_heads,
                           num_kv_heads, head_dim, block_size, max_num_blocks_per_req, scale,
@@ -1449,6 +1485,45 @@ int tq_decode_rows(void* output, const void* query, const void* kv_cache, const 
     if (!tq_config_valid(cfg) || cfg->head_dim != head_dim) return VMC_EINVAL;
     if (half_dtype != VMC_DTYPE_F16 && half_dtype != VMC_DTYPE_BF16) return VMC_EINVAL;
     if (max_num_blocks_per_req > 0x7fffffff) return VMC_EINVAL;
+    if (generic_head_dim(head_dim)) {
+        // head_dim 64 / 256: one wave per (row, query head), no workspace;
+        // q, out and the stored halves are half_dtype (fp8 keys included)
+        if (cfg->group_size != 0) return VMC_EINVAL;
+        if (batch_size < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 ||
+            block_size <= 0 || max_num_blocks_per_req <= 0)
+            return VMC_EINVAL;
+        if (batch_size == 0) return VMC_OK;
+        if (!output || !query || !kv_cache || !block_tables || !seq_lens) return VMC_EINVAL;
+        GenArgs a = {};
+        a.out = output;
+        a.q = query;
+        a.q_bf16 = half_dtype == VMC_DTYPE_BF16;
+        a.src = GEN_TQ;
+        a.kp = a.vp = reinterpret_cast<const uint8_t*>(kv_cache);
+        a.entry = cfg->slot_size_aligned;
+        a.hnd = 0;
+        a.bs = block_size;
+        a.bt = block_tables;
+        a.max_blocks = max_num_blocks_per_req;
+        a.seq_lens = seq_lens;
+        a.tok_seq = row_seq;
+        a.pos = row_pos;
+        a.num_seqs = -1;
+        a.rows = batch_size;
+        a.Hq = num_heads;
+        a.Hkv = num_kv_heads;
+        a.D = head_dim;
+        a.scale = scale;
+        a.kb = cfg->key_quant_bits;
+        a.vb = cfg->value_quant_bits;
+        a.key_fp8 = cfg->key_fp8;
+        a.fp8_e4b15 = cfg->fp8_e4b15;
+        a.mse_bytes = cfg->mse_bytes;
+        a.key_packed = cfg->key_packed_size;
+        a.val_data = cfg->val_data_bytes;
+        a.norm_correction = cfg->norm_correction;
+        return gen_attention(a, reinterpret_cast<hipStream_t>(stream));
+    }
     DecodeParams prm = {};
     if (cfg->group_size != 0) {
         // per-32-group variant: fp16 queries; d and m are fp16 whatever the

@@ -32,6 +32,7 @@
 // Fused append: head group 0 of each KV head writes the block's K/V rows into
 // the paged cache with the same block encoders as vmc_reshape_and_cache
 // (bit-identical pages).
+#include "generic_attn.hpp"
 #include "kv_quant.hpp"
 
 namespace vmc {
@@ -803,6 +804,43 @@ extern "C" int vmc_flash_attention_prefill_v2(void* output, const void* query, c
                                               const int32_t* token_positions, int num_reqs, int q_dtype,
                                               int kv_format, int layout, vmc_stream_t stream) {
     (void)seq_lens;  // a token's keys are positions 0 .. token_positions[t]
+    if (generic_head_dim(head_dim)) {
+        // head_dim 64 / 256: one wave per (token, query head), any block size
+        if (num_tokens < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 ||
+            block_size <= 0 || max_num_blocks_per_req <= 0 || num_reqs < 0)
+            return VMC_EINVAL;
+        if (q_dtype != VMC_DTYPE_F16 && q_dtype != VMC_DTYPE_BF16) return VMC_EINVAL;
+        if (layout != VMC_LAYOUT_NHD && layout != VMC_LAYOUT_HND) return VMC_EINVAL;
+        if (kv_format != VMC_KV_F16 && kv_format != VMC_KV_BF16 && kv_format != VMC_KV_Q8_0 &&
+            kv_format != VMC_KV_Q4_0)
+            return VMC_EINVAL;
+        if (num_tokens == 0 || num_reqs == 0) return VMC_OK;
+        if (!output || !query || !key_cache || !value_cache || !block_tables || !token_to_seq ||
+            !token_positions)
+            return VMC_EINVAL;
+        GenArgs a = {};
+        a.out = output;
+        a.q = query;
+        a.q_bf16 = q_dtype == VMC_DTYPE_BF16;
+        a.src = kv_format == VMC_KV_F16 ? GEN_F16 : kv_format == VMC_KV_BF16 ? GEN_BF16
+              : kv_format == VMC_KV_Q8_0 ? GEN_Q8 : GEN_Q4;
+        a.kp = reinterpret_cast<const uint8_t*>(key_cache);
+        a.vp = reinterpret_cast<const uint8_t*>(value_cache);
+        a.entry = vmc_kv_entry_bytes(kv_format, head_dim);
+        a.hnd = layout == VMC_LAYOUT_HND;
+        a.bs = block_size;
+        a.bt = block_tables;
+        a.max_blocks = max_num_blocks_per_req;
+        a.tok_seq = token_to_seq;
+        a.pos = token_positions;
+        a.num_seqs = num_reqs;
+        a.rows = num_tokens;
+        a.Hq = num_heads;
+        a.Hkv = num_kv_heads;
+        a.D = head_dim;
+        a.scale = scale;
+        return gen_attention(a, reinterpret_cast<hipStream_t>(stream));
+    }
     if (head_dim != kD || block_size != kBsP || num_tokens < 0 || num_heads <= 0 || num_kv_heads <= 0 ||
         num_heads % num_kv_heads != 0 || max_num_blocks_per_req <= 0 || num_reqs < 0)
         return VMC_EINVAL;
@@ -849,6 +887,39 @@ extern "C" int vmc_flash_attention_prefill(void* output, const void* query, cons
                                            void* key_cache, void* value_cache,
                                            const int64_t* slot_mapping, int64_t block_size,
                                            int kv_format, int layout, vmc_stream_t stream) {
+    if (generic_head_dim(head_dim)) {
+        // head_dim 64 / 256: the append by vmc_reshape_and_cache, then one
+        // wave per (token, query head) over this step's K/V
+        if (num_tokens < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
+            return VMC_EINVAL;
+        if (dtype != VMC_DTYPE_F16 && dtype != VMC_DTYPE_BF16) return VMC_EINVAL;
+        if (num_tokens == 0) return VMC_OK;
+        if (!output || !query || !key || !value || !token_positions) return VMC_EINVAL;
+        if (key_cache) {
+            const int64_t E = vmc_kv_entry_bytes(kv_format, head_dim);
+            if (E < 0 || block_size <= 0) return VMC_EINVAL;
+            const int rc = vmc_reshape_and_cache(key, value, key_cache, value_cache, slot_mapping, num_tokens,
+                                                 num_kv_heads, head_dim, block_size,
+                                                 block_size * num_kv_heads * E, kv_format, dtype, layout,
+                                                 stream);
+            if (rc != VMC_OK) return rc;
+        }
+        GenArgs a = {};
+        a.out = output;
+        a.q = query;
+        a.q_bf16 = dtype == VMC_DTYPE_BF16;
+        a.src = GEN_LOCAL;
+        a.k = reinterpret_cast<const uint16_t*>(key);
+        a.v = reinterpret_cast<const uint16_t*>(value);
+        a.pos = token_positions;
+        a.num_seqs = -1;
+        a.rows = num_tokens;
+        a.Hq = num_heads;
+        a.Hkv = num_kv_heads;
+        a.D = head_dim;
+        a.scale = scale;
+        return gen_attention(a, reinterpret_cast<hipStream_t>(stream));
+    }
     if (head_dim != kD || num_tokens < 0 || num_heads <= 0 || num_kv_heads <= 0 ||
         num_heads % num_kv_heads != 0)
         return VMC_EINVAL;

@@ -13,6 +13,7 @@
 // CPU oracle shares -- and the codebook index is the count of midpoints <= y,
 // which equals the reference's top-down scan (:283-304) for sorted midpoints.
 // Slot addressing: compute_slot_byte_offset (:39-45).
+#include "generic_attn.hpp"
 #include "vmc_store.hpp"
 
 namespace vmc {
@@ -149,11 +150,14 @@ extern "C" int vmc_turboquant_store(const void* key, const void* value, void* kv
                                     const vmc_tq_config* cfg, int half_dtype,
                                     vmc_stream_t stream) {
     if (!tq_config_valid(cfg) || cfg->head_dim != head_dim) return VMC_EINVAL;
-    if (head_dim != 128) return VMC_EINVAL;
+    if (head_dim != 128 && !generic_head_dim(head_dim)) return VMC_EINVAL;
     if (num_tokens < 0 || num_kv_heads <= 0 || block_size <= 0) return VMC_EINVAL;
     if (half_dtype != VMC_DTYPE_F16 && half_dtype != VMC_DTYPE_BF16) return VMC_EINVAL;
     if (num_tokens == 0) return VMC_OK;
     if (!key || !value || !kv_cache || !slot_mapping) return VMC_EINVAL;
+    if (head_dim != 128)
+        return gen_tq_store(key, value, kv_cache, slot_mapping, num_tokens, num_kv_heads, head_dim, block_size,
+                            cfg, half_dtype == VMC_DTYPE_BF16, reinterpret_cast<hipStream_t>(stream));
     if (cfg->key_fp8) {
         const int64_t grid = ((int64_t)num_tokens * num_kv_heads + 15) / 16;
         if (grid > 0x7fffffff) return VMC_EINVAL;

@@ -101,12 +101,15 @@ G32Signs g32_signs(unsigned long long seed) {
 bool tq_config_valid(const vmc_tq_config* c) {
     if (!c) return false;
     if (c->key_fp8) {
-        // turboquant_k8v4 (kernels_turboquant.h:29-55): 128 fp8 key bytes,
-        // 4-bit values, no norm, 196-byte slots
-        return c->head_dim == 128 && c->group_size == 0 && c->key_quant_bits == 8 &&
-               c->value_quant_bits == 4 && c->norm_correction == 0 && c->mse_bytes == 128 &&
-               c->key_packed_size == 128 && c->val_data_bytes == 64 && c->value_packed_size == 68 &&
-               c->slot_size == 196 && c->slot_size_aligned == 196;
+        // turboquant_k8v4 (kernels_turboquant.h:29-55): head_dim fp8 key
+        // bytes, 4-bit values, no norm (196-byte slots at head_dim 128)
+        const int d = c->head_dim;
+        if (d != 64 && d != 128 && d != 256) return false;
+        const int slot = d + d / 2 + 4;
+        return c->group_size == 0 && c->key_quant_bits == 8 && c->value_quant_bits == 4 &&
+               c->norm_correction == 0 && c->mse_bytes == d && c->key_packed_size == d &&
+               c->val_data_bytes == d / 2 && c->value_packed_size == d / 2 + 4 && c->slot_size == slot &&
+               c->slot_size_aligned == slot + (slot % 2);
     }
     if (c->group_size != 0) {
         // per-32-group variant: head_dim 128, equal K/V bits, the fixed part sizes
