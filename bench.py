@@ -424,24 +424,35 @@ def bench_fused_norm_rope(args, torch, capi, dev):
     return dict(ms=ms, med=med, gbs=gbs, bytes=nbytes)
 
 
-def bench_hbm_ceiling(torch, dev):
-    """Measured HBM ceilings next to the 8 TB/s datasheet figure: a 2 GiB
-    device-to-device copy (read + write bytes / time) and a read-only 4 GiB
-    reduction (torch's sum), median of 10 each."""
+def bench_hbm_ceiling(torch, capi, dev):
+    """Measured HBM ceilings next to the 8 TB/s datasheet figure, median of 10
+    each: a 2 GiB device-to-device copy (read + write bytes / time) and two
+    4 GiB streaming reads (vmc_hbm_read_probe: 16-byte non-temporal loads into
+    registers, and the decode's 16-byte non-temporal load-to-LDS transfers)."""
     stream = torch.cuda.current_stream()
     n = 2 << 30
     src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
     _, med_copy = time_loop(torch, lambda i: dst.copy_(src), 10, 3, stream)
     del src, dst
-    x = torch.ones((4 << 30) // 4, dtype=torch.float32, device=dev)
-    _, med_read = time_loop(torch, lambda i: x.sum(), 10, 3, stream)
-    del x
+    nr = 4 << 30
+    x = torch.ones(nr, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(256, dtype=torch.int32, device=dev)
+    meds = []
+    for mode in (0, 1, 2):
+        _, med = time_loop(torch, lambda i: capi.hbm_read_probe(x, mode, sink, stream), 10, 3, stream)
+        meds.append(med)
+    del x, sink
     torch.cuda.empty_cache()
     res = {"copy_gbs": round(2 * n / (med_copy * 1e-3) / 1e9, 1),
-           "read_gbs": round((4 << 30) / (med_read * 1e-3) / 1e9, 1),
-           "method": "2 GiB torch copy_ (read+write) and 4 GiB fp32 torch sum (read), median of 10"}
-    log(f"HBM ceiling: copy {res['copy_gbs']} GB/s, read {res['read_gbs']} GB/s")
+           "read_gbs": round(nr / (meds[0] * 1e-3) / 1e9, 1),
+           "read_lds_dma_nt_gbs": round(nr / (meds[1] * 1e-3) / 1e9, 1),
+           "read_lds_dma_gbs": round(nr / (meds[2] * 1e-3) / 1e9, 1),
+           "method": "2 GiB torch copy_ (read+write); 4 GiB vmc_hbm_read_probe reads: mode 0 nt loads to "
+                     "registers, mode 1 nt load-to-LDS, mode 2 load-to-LDS (the decode's transfers); "
+                     "medians of 10"}
+    log(f"HBM ceiling: copy {res['copy_gbs']} GB/s, read {res['read_gbs']} GB/s, load-to-LDS read "
+        f"{res['read_lds_dma_gbs']} GB/s (nt {res['read_lds_dma_nt_gbs']})")
     return res
 
 
@@ -599,6 +610,9 @@ def main():
     ap.add_argument("--only", choices=("decode", "prefill", "paged_prefill", "fused", "configs"),
                     help="profiling runs: only this part (decode: the headline operator; configs: "
                          "the other decode configurations), one JSON line of its numbers")
+    ap.add_argument("--read-calibration", action="store_true",
+                    help="only run a 1 GiB load-to-LDS read (vmc_hbm_read_probe mode 2, the decode's "
+                         "request type) 5 times (for scaling rocprofv3 FETCH_SIZE)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy 5 times (the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -612,6 +626,15 @@ def main():
     from vm_c_amd import capi
     capi.load()
     dev = torch.device("cuda:0")
+    if args.read_calibration:
+        n = 1 << 30
+        buf = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        torch.cuda.synchronize()
+        for _ in range(5):
+            capi.hbm_read_probe(buf, 2)
+        torch.cuda.synchronize()
+        print(json.dumps({"read_calibration_bytes": n, "launches": 5}), flush=True)
+        return
     if args.copy_calibration:
         n = 1 << 30
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
@@ -658,7 +681,7 @@ def main():
     pre = None if args.skip_prefill else bench_prefill(args, torch, capi, dev)
     paged = None if args.skip_prefill else bench_paged_prefill(args, torch, capi, dev)
     fused = None if args.skip_prefill else bench_fused_norm_rope(args, torch, capi, dev)
-    ceiling = bench_hbm_ceiling(torch, dev)
+    ceiling = bench_hbm_ceiling(torch, capi, dev)
     cpu = None
     if not args.no_cpu_baseline:
         nthreads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)

@@ -319,6 +319,18 @@ int vmc_flash_attention_prefill(void* output, const void* query, const void* key
                                 int64_t block_size, int kv_format, int layout,
                                 vmc_stream_t stream);
 
+/*
+ * Measurement only (no counterpart in the reference): one streaming read of
+ * bytes (a multiple of 16) at src (16-byte aligned).  mode 0: 16-byte
+ * non-temporal vector loads into registers (sink: 1 KB of device memory the
+ * kernel may write); mode 1: 16-byte non-temporal load-to-LDS transfers;
+ * mode 2: 16-byte load-to-LDS transfers, the request type of the TurboQuant
+ * decode (modes 1, 2: sink unused).  bench.py times them for the measured
+ * HBM read ceilings and runs mode 2 under rocprofv3 to scale FETCH_SIZE for
+ * the decode.
+ */
+int vmc_hbm_read_probe(const void* src, size_t bytes, int mode, void* sink, vmc_stream_t stream);
+
 /* Device self-check of the lane-level assumptions the kernels rely on (MFMA
  * operand/result layouts of the shapes used, cross-row reductions, the
  * wave-private LDS exchange).  No counterpart in the reference: a guard for

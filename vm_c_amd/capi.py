@@ -93,6 +93,8 @@ def load():
     L.vmc_flash_attention_prefill.restype = _I
     L.vmc_flash_attention_prefill.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P, _P,
                                               _P, _I64, _I, _I, _P]
+    L.vmc_hbm_read_probe.restype = _I
+    L.vmc_hbm_read_probe.argtypes = [_P, _SZ, _I, _P, _P]
     L.vmc_selftest.restype = _I
     L.vmc_selftest.argtypes = []
     L.vmc_version.restype = C.c_char_p
@@ -260,6 +262,15 @@ def flash_attention_prefill(out, query, key, value, token_positions, num_kv_head
         _ptr(slot_mapping), block_size, kv_format, layout, _stream(stream))
     _check(rc, "vmc_flash_attention_prefill")
     return out
+
+
+def hbm_read_probe(buf, mode, sink=None, stream=None):
+    """One streaming read of the whole buffer (measurement): mode 0 vector
+    loads into registers, mode 1 non-temporal load-to-LDS transfers, mode 2
+    the decode's load-to-LDS transfers."""
+    rc = load().vmc_hbm_read_probe(_ptr(buf), buf.numel() * buf.element_size(), mode, _ptr(sink),
+                                   _stream(stream))
+    _check(rc, "vmc_hbm_read_probe")
 
 
 def fused_qk_norm_rope_store(q, k, v, q_norm_weight, k_norm_weight, cos_sin_cache, position_ids,

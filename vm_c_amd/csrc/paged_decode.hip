@@ -554,7 +554,7 @@ paged_decode_kernel(DecodeParams p) {
             if (dma_on[c])
                 __builtin_amdgcn_global_load_lds(
                     (const void __attribute__((address_space(1)))*)(src + dma_off[c]),
-                    (void __attribute__((address_space(3)))*)dst, 16, 0, 2);  // non-temporal
+                    (void __attribute__((address_space(3)))*)dst, 16, 0, 0);  // cached: windows overlap
         }
     };
 
