@@ -580,7 +580,7 @@ def cpu_reference_ggml(nthreads):
 
 # ------------------------------------------------------------------ traffic
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "paged_decode_tq3_ragged32k_traffic.md")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "tq_decode_tq3_ragged32k_traffic.md")
 
 
 def measured_traffic():
@@ -716,7 +716,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(gbs_attn, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs_attn / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(),
-                     "kernel": "turboquant_decode_attention: paged_decode_kernel + "
+                     "kernel": "turboquant_decode_attention: tq_decode_kernel + "
                                "decode_merge_kernel (one operator, two launches)",
                      "ms": round(dec["ms_attn"], 4), "ms_median": round(dec["med_attn"], 4),
                      "launches_timed": dec["n_attn"], "bytes": dec["attn_bytes"],
