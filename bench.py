@@ -370,7 +370,37 @@ def bench_paged_prefill(args, torch, capi, dev):
         f"per-token path {ms_rows * 1e3:.1f} us")
     del sets
     torch.cuda.empty_cache()
-    return dict(ms=ms, med=med, tflops=tflops, flops=flops, n=n, ms_rows=ms_rows)
+
+    # the same chunk over 3-bit TurboQuant slots (vmc_turboquant_prefill_attention),
+    # the pages stored from random K/V by the TurboQuant store
+    cfg = capi.tq_config(D, "turboquant_3bit_nc")
+    pos = torch.arange(L, device=dev)
+    slots = (bt.view(-1).long()[pos // BS] * BS + pos % BS).contiguous()
+    tq_sets = []
+    for _ in range(nset):
+        cache = torch.zeros(nblk * BS * Hkv * cfg.slot_size_aligned, dtype=torch.uint8, device=dev)
+        k = torch.randn((L, Hkv, D), generator=gen, device=dev).half()
+        v = torch.randn((L, Hkv, D), generator=gen, device=dev).half()
+        capi.turboquant_store(k, v, cache, slots, BS, cfg)
+        del k, v
+        q = torch.randn((new, Hq, D), generator=gen, device=dev).half()
+        tq_sets.append((q, torch.empty_like(q), cache))
+
+    def run_tq(i):
+        q, out, cache = tq_sets[i % nset]
+        capi.turboquant_prefill_attention(out, q, cache, bt, tok_seq, tok_pos, Hkv, scale, cfg, block_size=BS,
+                                          stream=stream)
+
+    ms_tq, med_tq = time_loop(torch, run_tq, n, max(2, args.warmup // 2), stream)
+    assert all(torch.isfinite(st[1].float()).all().item() for st in tq_sets), \
+        "TurboQuant prefill produced non-finite values"
+    tflops_tq = flops / (ms_tq * 1e-3) / 1e12
+    log(f"TurboQuant 3-bit chunked prefill {ms_tq * 1e3:.1f} us (median {med_tq * 1e3:.1f}), "
+        f"{tflops_tq:.1f} TFLOP/s")
+    del tq_sets
+    torch.cuda.empty_cache()
+    return dict(ms=ms, med=med, tflops=tflops, flops=flops, n=n, ms_rows=ms_rows, tq3_ms=ms_tq, tq3_med=med_tq,
+                tq3_tflops=tflops_tq)
 
 
 # ------------------------------------------------------------------ fused norm + RoPE + append
@@ -741,7 +771,9 @@ def main():
             "ms": round(paged["ms"], 4), "ms_median": round(paged["med"], 4), "launches_timed": paged["n"],
             "tflops": round(paged["tflops"], 1),
             "pct_peak_mfma_fp16": round(100 * paged["tflops"] / MFMA_BF16_PEAK_TFLOPS, 2),
-            "ms_per_token_path": round(paged["ms_rows"], 3)}
+            "ms_per_token_path": round(paged["ms_rows"], 3),
+            "turboquant_3bit": {"ms": round(paged["tq3_ms"], 4), "ms_median": round(paged["tq3_med"], 4),
+                                "tflops": round(paged["tq3_tflops"], 1)}}
     if fused is not None:
         line["fused_norm_rope"] = {
             "workload": "q/k RMSNorm + neox RoPE + q8_0 K/V append, 16384 tokens, Hq=32 Hkv=8 bf16",

@@ -154,6 +154,54 @@ def test_tq_decode(dev, method, case):
     assert ok, f"vs reference restatement: max err {err}"
 
 
+@pytest.mark.parametrize("max_splits", [0, 1])
+def test_tq_4bit_without_norm_correction(dev, max_splits):
+    """4-bit keys and values with the norm correction off (the reference's
+    4/4 decode without it, turboquant_kernels.cu:901-912: keys are the
+    centroids times the stored norm, no division by ||C[codes]||).  The decode
+    and both prefill paths (15 tokens: one decode row per token; 40 tokens:
+    the tiled prefill) against fp64 attention over the same slots."""
+    import torch
+    from vm_c_amd import capi
+    w = make_workload(seq_lens=[300, 1024, 17, 0], Hq=16, Hkv=4, seed=90 + max_splits)
+    L = O.tq_layout("turboquant_4bit_nc")
+    L.norm_correction = 0
+    cfg = capi.tq_config(128, "turboquant_4bit_nc")
+    cfg.norm_correction = 0
+    cache = torch.zeros(w.num_blocks * BS * w.Hkv * cfg.slot_size_aligned, dtype=torch.uint8, device=dev)
+    capi.turboquant_store(torch.from_numpy(w.K).to(dev), torch.from_numpy(w.V).to(dev), cache,
+                          torch.from_numpy(w.slots).to(dev), BS, cfg)
+    bt = torch.from_numpy(w.bt).to(dev)
+    q = torch.from_numpy(w.Q).to(dev)
+    out = torch.full_like(q, float("nan"))
+    capi.turboquant_decode_attention(out, q, cache, bt, torch.from_numpy(w.seq_lens).to(dev), w.Hkv,
+                                     float(w.scale), cfg, block_size=BS, max_splits=max_splits)
+    rng = np.random.default_rng(max_splits)
+    outs = []
+    for T in (15, 40):
+        tok_seq = rng.integers(0, 3, T).astype(np.int32)
+        tok_pos = (rng.random(T) * w.seq_lens[tok_seq]).astype(np.int32)
+        qp = rng.standard_normal((T, 16, 128)).astype(np.float16)
+        o = torch.full((T, 16, 128), float("nan"), dtype=torch.float16, device=dev)
+        capi.turboquant_prefill_attention(o, torch.from_numpy(qp).to(dev), cache, bt,
+                                          torch.from_numpy(tok_seq).to(dev), torch.from_numpy(tok_pos).to(dev),
+                                          w.Hkv, float(w.scale), cfg, block_size=BS)
+        outs.append((qp, tok_seq, tok_pos, o))
+    torch.cuda.synchronize()
+    got_cache = cache.cpu().numpy()
+    c, _ = O.tq_tables(128, 4)
+    ex = O.tq_decode_exact(bits16(w.Q), got_cache, w.bt, w.seq_lens, w.Hkv, w.scale, BS, L, c)
+    ok, err = close_report(out.float().cpu().numpy(), ex, ATOL, RTOL)
+    assert ok, f"decode: max err {err}"
+    L1 = O.tq_layout("turboquant_4bit_nc")
+    ex1 = O.tq_decode_exact(bits16(w.Q), got_cache, w.bt, w.seq_lens, w.Hkv, w.scale, BS, L1, c)
+    assert not close_report(out.float().cpu().numpy(), ex1, ATOL, RTOL)[0], "the flag changed nothing"
+    for qp, tok_seq, tok_pos, o in outs:
+        ex = O.tq_decode_exact(bits16(qp), got_cache, w.bt[tok_seq], tok_pos + 1, w.Hkv, w.scale, BS, L, c)
+        ok, err = close_report(o.float().cpu().numpy(), ex, ATOL, RTOL)
+        assert ok, f"prefill of {len(tok_seq)} tokens: max err {err}"
+
+
 @pytest.mark.parametrize("method", ["turboquant_4bit_nc", "turboquant_3bit_nc", "turboquant_k3v4_nc"])
 @pytest.mark.parametrize("case", ["cfg5_small", "ragged", "gqa16"])
 @pytest.mark.parametrize("max_splits", [0, 1])

@@ -99,3 +99,38 @@ def test_k8v4_decode(dev, e4b15, case):
     for ms in (0, 1):
         ok, err = close_report(_decode(dev, w, cfg, cache, max_splits=ms), ex, ATOL, RTOL)
         assert ok, f"max_splits={ms}: max err {err}"
+
+
+@pytest.mark.parametrize("e4b15", [False, True])
+@pytest.mark.parametrize("case", ["ragged", "gqa16"])
+def test_k8v4_decode_bf16(dev, e4b15, case):
+    """bf16 q, out and V scale / zero (the reference's USE_BF16 stage 1 for
+    fp8 keys, turboquant_kernels.cu:876-881): the decode and a 20-token
+    prefill step against fp64 attention over the same slots."""
+    import torch
+    from vm_c_amd import capi
+    w = make_workload(seed=len(case) + 13, **CASES[case])
+    cfg, L, cache, _ = _store(dev, w, e4b15, bf16=True, kscale=0.3 if e4b15 else 1.0)
+    qb = f32_to_bf16_bits(w.Q.astype(np.float32))
+    as_bf16 = lambda b: torch.from_numpy(np.ascontiguousarray(b).view(np.int16)).to(dev).view(torch.bfloat16)
+    out = torch.full(w.Q.shape, float("nan"), dtype=torch.bfloat16, device=dev)
+    bt = torch.from_numpy(w.bt).to(dev)
+    capi.turboquant_decode_attention(out, as_bf16(qb), cache, bt, torch.from_numpy(w.seq_lens).to(dev), w.Hkv,
+                                     float(w.scale), cfg, block_size=BS)
+    rng = np.random.default_rng(len(case))
+    live = np.flatnonzero(w.seq_lens > 0)
+    tok_seq = live[rng.integers(0, live.size, 20)].astype(np.int32)
+    tok_pos = (rng.random(20) * w.seq_lens[tok_seq]).astype(np.int32)
+    qp = f32_to_bf16_bits(rng.standard_normal((20, w.Hq, D)).astype(np.float32))
+    outp = torch.full((20, w.Hq, D), float("nan"), dtype=torch.bfloat16, device=dev)
+    capi.turboquant_prefill_attention(outp, as_bf16(qp), cache, bt, torch.from_numpy(tok_seq).to(dev),
+                                      torch.from_numpy(tok_pos).to(dev), w.Hkv, float(w.scale), cfg, block_size=BS)
+    torch.cuda.synchronize()
+    got_cache = cache.cpu().numpy()
+    c, _ = O.tq_tables(D, 4)
+    ex = O.tq_decode_exact(qb, got_cache, w.bt, w.seq_lens, w.Hkv, w.scale, BS, L, c, bf16=True)
+    ok, err = close_report(out.float().cpu().numpy(), ex, ATOL, RTOL)
+    assert ok, f"decode: max err {err}"
+    ex = O.tq_decode_exact(qp, got_cache, w.bt[tok_seq], tok_pos + 1, w.Hkv, w.scale, BS, L, c, bf16=True)
+    ok, err = close_report(outp.float().cpu().numpy(), ex, ATOL, RTOL)
+    assert ok, f"prefill rows: max err {err}"

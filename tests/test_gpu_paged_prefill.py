@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as O
-from kvgen import BS, bits16, close_report, make_workload
+from kvgen import BS, bits16, close_report, f32_to_bf16_bits, make_workload
 
 pytestmark = pytest.mark.gpu
 
@@ -51,40 +51,107 @@ def test_paged_prefill_over_cached_prefix(dev, fmt, hnd, splits):
     assert ok, f"max err {err}"
 
 
-@pytest.mark.parametrize("method", ["turboquant_3bit_nc", "turboquant_4bit_g32", "turboquant_k8v4"])
-def test_turboquant_prefill_over_cached_prefix(dev, method):
-    """vmc_turboquant_prefill_attention (no reference counterpart: the
-    reference's TurboQuant prefill attends only the step's local K/V)."""
+def _tq_cache(dev, w, cfg, bf16):
     import torch
     from vm_c_amd import capi
+    cache = torch.zeros(w.num_blocks * BS * w.Hkv * cfg.slot_size_aligned, dtype=torch.uint8, device=dev)
+    dt = torch.bfloat16 if bf16 else torch.float16
+    k = torch.from_numpy(w.K).to(dev).to(dt)
+    v = torch.from_numpy(w.V).to(dev).to(dt)
+    capi.turboquant_store(k, v, cache, torch.from_numpy(w.slots).to(dev), BS, cfg)
+    return cache
+
+
+def _q_bits(q, bf16):
+    return f32_to_bf16_bits(q) if bf16 else q.astype(np.float16).view(np.uint16)
+
+
+def _q_dev(dev, qbits, bf16):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(qbits).view(np.int16)).to(dev).view(
+        torch.bfloat16 if bf16 else torch.float16)
+
+
+def _tq_exact(method, qbits, cache, bt_rows, len_rows, Hkv, scale, bf16):
+    if method.endswith("_g32"):
+        return O.g32_decode_exact(qbits, cache, bt_rows, len_rows, Hkv, scale, BS, 4 if "4bit" in method else 3,
+                                  0, bf16=bf16)
+    L = O.tq_layout(method)
+    c, _ = O.tq_tables(128, 4 if L.key_fp8 else L.key_quant_bits)
+    return O.tq_decode_exact(qbits, cache, bt_rows, len_rows, Hkv, scale, BS, L, c, bf16=bf16)
+
+
+@pytest.mark.parametrize("method", ["turboquant_3bit_nc", "turboquant_4bit_nc", "turboquant_k3v4_nc",
+                                    "turboquant_4bit_g32", "turboquant_k8v4"])
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("chunk", ["tiled", "per_token"])
+def test_turboquant_prefill_over_cached_prefix(dev, method, bf16, chunk):
+    """vmc_turboquant_prefill_attention (no reference counterpart: the
+    reference's TurboQuant prefill attends only the step's local K/V).  A
+    step of 121 tokens over codebook slots takes the tiled prefill; one of 15
+    tokens (and every step over fp8-key or per-32-group slots) one decode row
+    per token."""
+    import torch
+    from vm_c_amd import capi
+    if method.endswith("_g32") and bf16:
+        pytest.skip("the per-32-group variant takes fp16 queries")
     prefix = np.array([100, 0, 513])
-    new = np.array([37, 20, 64])
+    new = np.array([37, 20, 64]) if chunk == "tiled" else np.array([5, 3, 7])
     lens = prefix + new
     Hq, Hkv = 16, 4
     w = make_workload(lens, Hq=Hq, Hkv=Hkv, seed=41, pool_slack=2)
     cfg = capi.tq_config(128, method)
-    cache = torch.zeros(w.num_blocks * BS * Hkv * cfg.slot_size_aligned, dtype=torch.uint8, device=dev)
-    capi.turboquant_store(torch.from_numpy(w.K).to(dev), torch.from_numpy(w.V).to(dev), cache,
-                          torch.from_numpy(w.slots).to(dev), BS, cfg)
+    cache = _tq_cache(dev, w, cfg, bf16)
     tok_seq = np.concatenate([np.full(new[b], b) for b in range(len(lens))]).astype(np.int32)
     tok_pos = np.concatenate([np.arange(prefix[b], lens[b]) for b in range(len(lens))]).astype(np.int32)
     T = tok_seq.size
-    q = np.random.default_rng(6).standard_normal((T, Hq, 128)).astype(np.float16)
-    out = torch.full((T, Hq, 128), float("nan"), dtype=torch.float16, device=dev)
-    capi.turboquant_prefill_attention(out, torch.from_numpy(q).to(dev), cache, torch.from_numpy(w.bt).to(dev),
+    qbits = _q_bits(np.random.default_rng(6).standard_normal((T, Hq, 128)).astype(np.float32), bf16)
+    out = torch.full((T, Hq, 128), float("nan"), dtype=torch.bfloat16 if bf16 else torch.float16, device=dev)
+    capi.turboquant_prefill_attention(out, _q_dev(dev, qbits, bf16), cache, torch.from_numpy(w.bt).to(dev),
                                       torch.from_numpy(tok_seq).to(dev), torch.from_numpy(tok_pos).to(dev),
                                       Hkv, float(w.scale), cfg, block_size=BS)
     torch.cuda.synchronize()
-    got = cache.cpu().numpy()
-    bt_rows, len_rows = w.bt[tok_seq], (tok_pos + 1).astype(np.int32)
-    if method.endswith("_g32"):
-        ex = O.g32_decode_exact(bits16(q), got, bt_rows, len_rows, Hkv, float(w.scale), BS, 4, 0)
-    else:
-        L = O.tq_layout(method)
-        c, _ = O.tq_tables(128, 4 if L.key_fp8 else L.key_quant_bits)
-        ex = O.tq_decode_exact(bits16(q), got, bt_rows, len_rows, Hkv, float(w.scale), BS, L, c)
+    ex = _tq_exact(method, qbits, cache.cpu().numpy(), w.bt[tok_seq], (tok_pos + 1).astype(np.int32), Hkv,
+                   float(w.scale), bf16)
     ok, err = close_report(out.float().cpu().numpy(), ex, 2e-3, 1e-2)
     assert ok, f"max err {err}"
+
+
+@pytest.mark.parametrize("method", ["turboquant_3bit_nc", "turboquant_4bit_nc"])
+def test_turboquant_prefill_chunk_over_long_prefix(dev, method):
+    """A 2048-token chunk over a 30720-token prefix of codebook slots, 32/8
+    heads (the tiled prefill): every row against the per-token path (steps
+    of 15 tokens, which the test above pins to the oracle), 32 sampled tokens
+    x all heads against the oracle's fp64 attention."""
+    import torch
+    from vm_c_amd import capi
+    prefix, new = 30720, 2048
+    Hq, Hkv = 32, 8
+    w = make_workload([prefix + new], Hq=Hq, Hkv=Hkv, seed=62)
+    cfg = capi.tq_config(128, method)
+    cache = _tq_cache(dev, w, cfg, False)
+    tok_seq = np.zeros(new, np.int32)
+    tok_pos = np.arange(prefix, prefix + new, dtype=np.int32)
+    q = np.random.default_rng(10).standard_normal((new, Hq, 128)).astype(np.float16)
+    qt = torch.from_numpy(q).to(dev)
+    bt = torch.from_numpy(w.bt).to(dev)
+    ts, tp = torch.from_numpy(tok_seq).to(dev), torch.from_numpy(tok_pos).to(dev)
+    out = torch.full_like(qt, float("nan"))
+    capi.turboquant_prefill_attention(out, qt, cache, bt, ts, tp, Hkv, float(w.scale), cfg, block_size=BS)
+    rows = torch.full_like(qt, float("nan"))
+    for a in range(0, new, 15):
+        b = min(a + 15, new)
+        capi.turboquant_prefill_attention(rows[a:b], qt[a:b], cache, bt, ts[a:b], tp[a:b], Hkv, float(w.scale),
+                                          cfg, block_size=BS)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    ok, err = close_report(got, rows.float().cpu().numpy(), 2e-3, 1e-2)
+    assert ok, f"vs per-token path: max err {err}"
+    pick = np.concatenate([[0, 1, 63, 64, new - 1], np.random.default_rng(11).integers(0, new, 27)])
+    ex = _tq_exact(method, bits16(q[pick]), cache.cpu().numpy(), w.bt[tok_seq[pick]],
+                   (tok_pos[pick] + 1).astype(np.int32), Hkv, float(w.scale), False)
+    ok, err = close_report(got[pick], ex, 2e-3, 1e-2)
+    assert ok, f"vs exact: max err {err}"
 
 
 def _pages(dev, w, fmt, hnd):

@@ -327,7 +327,10 @@ def flash_attention_prefill_v2(out, query, key_cache, value_cache, block_tables,
 
 def turboquant_prefill_attention(out, query, kv_cache, block_tables, token_to_seq, token_positions,
                                  num_kv_heads, scale, cfg, block_size=16, stream=None):
-    """One row per token over the packed pages (cached prefix + appended step)."""
+    """Token t attends positions 0 .. token_positions[t] of its sequence over
+    the packed slots (cached prefix + appended step): steps of 16 tokens or
+    more over codebook slots (head_dim 128) take the tiled prefill, others
+    one decode row per token."""
     T, Hq, D = query.shape
     rc = load().vmc_turboquant_prefill_attention(
         _ptr(out), _ptr(query), _ptr(kv_cache), _ptr(block_tables), _ptr(token_to_seq),

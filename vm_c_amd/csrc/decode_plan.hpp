@@ -39,6 +39,7 @@ struct DecodeParams {
     int q_bf16;
     // TurboQuant
     int mse_bytes, key_packed, val_data;
+    int norm_corr;       // codebook keys: scaled by 1 / ||C[codes]|| (else by the stored norm alone)
     TQTables tab;
     uint32_t sgn[4];     // per-32-group variant: bit i set = rotation sign of dim i is -1
     int fp8_e4b15;       // turboquant_k8v4 keys: e4b15 (1) or e4m3 (0) codes

@@ -41,6 +41,7 @@
 #include "decode_plan.hpp"
 #include "generic_attn.hpp"
 #include "kv_quant.hpp"
+#include "prefill_api.hpp"
 
 #include <mutex>
 #include <utility>
@@ -667,7 +668,7 @@ paged_decode_kernel(DecodeParams p) {
             const float csq = sel_bits(sel_bits(gram[0], gram[1], odd_mask), sel_bits(gram[2], gram[3], odd_mask),
                                        hi_mask);
             const float nrm = half_to_f32<kTqBf16>((uint16_t)lds16(ke + GE::mse));
-            rowf[pp] = p.scale_log2 * nrm * __builtin_amdgcn_rsqf(csq + 1e-16f);
+            rowf[pp] = p.scale_log2 * nrm * (p.norm_corr ? __builtin_amdgcn_rsqf(csq + 1e-16f) : 1.0f);
             // V: the four bytes around token 4*grp + i's code run, its scale
             // and zero
             uint32_t cw[4];
@@ -1485,9 +1486,10 @@ int tq_decode_rows(void* output, const void* query, const void* kv_cache, const 
     if (!tq_config_valid(cfg) || cfg->head_dim != head_dim) return VMC_EINVAL;
     if (half_dtype != VMC_DTYPE_F16 && half_dtype != VMC_DTYPE_BF16) return VMC_EINVAL;
     if (max_num_blocks_per_req > 0x7fffffff) return VMC_EINVAL;
-    if (generic_head_dim(head_dim)) {
-        // head_dim 64 / 256: one wave per (row, query head), no workspace;
-        // q, out and the stored halves are half_dtype (fp8 keys included)
+    if (generic_head_dim(head_dim) || (cfg->key_fp8 && half_dtype == VMC_DTYPE_BF16)) {
+        // head_dim 64 / 256, and fp8 keys with bf16 halves: one wave per
+        // (row, query head), no workspace; q, out and the stored halves are
+        // half_dtype
         if (cfg->group_size != 0) return VMC_EINVAL;
         if (batch_size < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 ||
             block_size <= 0 || max_num_blocks_per_req <= 0)
@@ -1552,7 +1554,7 @@ int tq_decode_rows(void* output, const void* query, const void* kv_cache, const 
     }
     if (cfg->key_fp8) {
         // turboquant_k8v4: fp8 keys (q not rotated, no norm), 4-bit values;
-        // scale and zero stored as fp16
+        // fp16 q, out, scale and zero (bf16 takes the branch above)
         if (half_dtype != VMC_DTYPE_F16) return VMC_EINVAL;
         int rc = setup_common(prm, output, query, block_tables, seq_lens, batch_size, num_heads,
                               num_kv_heads, head_dim, (int)block_size, (int)max_num_blocks_per_req,
@@ -1590,6 +1592,7 @@ int tq_decode_rows(void* output, const void* query, const void* kv_cache, const 
     prm.mse_bytes = cfg->mse_bytes;
     prm.key_packed = cfg->key_packed_size;
     prm.val_data = cfg->val_data_bytes;
+    prm.norm_corr = cfg->norm_correction != 0;
     prm.tab = tq_tables(head_dim, cfg->key_quant_bits);
     if ((prm.page_bytes % 16) != 0) return VMC_EINVAL;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -1669,6 +1672,15 @@ extern "C" int vmc_turboquant_prefill_attention(void* output, const void* query,
                                                 int max_num_kv_splits, void* workspace,
                                                 size_t workspace_bytes, vmc_stream_t stream) {
     if (num_tokens > 0 && (!token_to_seq || !token_positions)) return VMC_EINVAL;
+    // chunks of 16 tokens or more over reference-layout slots: the tiled
+    // prefill (each 64-key tile of a sequence read once per block of query
+    // rows); fewer tokens, fp8 keys and the per-32-group variant: one decode
+    // row per token
+    if (head_dim == kD && block_size == kBs && num_tokens >= 16 && tq_config_valid(cfg) && cfg->head_dim == kD &&
+        cfg->group_size == 0 && !cfg->key_fp8 && ((uintptr_t)kv_cache & 3) == 0)
+        return tq_prefill_tiled(output, query, kv_cache, block_tables, token_to_seq, token_positions, num_tokens,
+                                num_heads, num_kv_heads, scale, max_num_blocks_per_req, cfg, half_dtype,
+                                reinterpret_cast<hipStream_t>(stream));
     // token_positions stands in for seq_lens (not read when rows are indirect)
     return tq_decode_rows(output, query, kv_cache, block_tables, token_positions, token_to_seq,
                           token_positions, num_tokens, num_heads, num_kv_heads, head_dim, scale, block_size,

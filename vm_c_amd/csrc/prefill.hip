@@ -34,6 +34,8 @@
 // (bit-identical pages).
 #include "generic_attn.hpp"
 #include "kv_quant.hpp"
+#include "prefill_api.hpp"
+#include "vmc_tq.hpp"
 
 namespace vmc {
 namespace {
@@ -47,9 +49,10 @@ constexpr float kNegInf = -__builtin_inff();
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 // K/V sources of the kernel: this step's contiguous rows, or the paged cache
-// (f16 / bf16 pages by load-to-LDS transfers; q8_0 / q4_0 pages dequantized
-// to fp16 through registers)
-constexpr int SRC_LOCAL = 0, SRC_PAGED = 1, SRC_Q8 = 2, SRC_Q4 = 3;
+// (f16 / bf16 pages by load-to-LDS transfers; q8_0 / q4_0 and TurboQuant
+// pages (key / value bits 3/3, 4/4, 3/4) dequantized to fp16 through
+// registers)
+constexpr int SRC_LOCAL = 0, SRC_PAGED = 1, SRC_Q8 = 2, SRC_Q4 = 3, SRC_TQ33 = 4, SRC_TQ44 = 5, SRC_TQ34 = 6;
 
 struct PrefillParams {
     uint16_t* out;
@@ -64,7 +67,12 @@ struct PrefillParams {
     const int32_t* tok_seq;
     int64_t max_blocks, page_bytes;
     int num_seqs;        // rows of a sequence outside [0, num_seqs) get no keys
-    int q_bf16;          // paged: q / out are bf16 (else fp16)
+    int q_bf16;          // paged: q / out (TurboQuant: and the stored halves) are bf16
+    // TurboQuant slots: Lloyd-Max centroids, 1 / sqrt(d), field offsets
+    float cent[16];
+    float rot_c;
+    int mse_bytes, key_packed, val_data;
+    int norm_corr;  // keys scaled by 1 / ||C[codes]|| (else by the stored norm alone)
     int T, Hq, Hkv, G;
     float scale_log2;
     int ntiles;          // query blocks of qb rows
@@ -126,6 +134,7 @@ struct PrefillLds {
     uint8_t vtr[NSLOT][kD * BN * 2];   // [slot][dim][kv position] fp16 V^T
     float scratch[2][NW][32];          // [alpha, l][wave][row]
     alignas(8) uint8_t wide[NSLOT][NW];  // bf16: wave w's V rows of the tile need the exact mode
+    float cent[16];                      // TurboQuant key centroids
 };
 
 __device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
@@ -213,6 +222,66 @@ prefill_kernel(PrefillParams p) {
             qb[s] = as_v8<V8>(u32x4{wv[0] ^ qflip, wv[1] ^ qflip, wv[2] ^ qflip, wv[3] ^ qflip});
         }
     }
+    if constexpr (SRC >= SRC_TQ33) {
+        // TurboQuant keys are stored rotated: q_rot = H q / sqrt(d), in fp32
+        // from the raw q.  Dim 16 s + 8 h + e: butterflies over e (half-widths
+        // 1, 2, 4) and s (16, 32, 64) in the lane, over h (8) with the lane
+        // 32 apart; then fp16.
+        const uint16_t* qp = p.q + ((int64_t)row * p.Hq + hq) * kD + 8 * h;
+        float y[8][8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            u32x4 wv = {0u, 0u, 0u, 0u};
+            if (row_ok) wv = *reinterpret_cast<const u32x4*>(qp + 16 * s);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                y[s][2 * e] = qbf ? __builtin_bit_cast(float, wv[e] << 16) : f16_bits_to_f32(wv[e] & 0xffff);
+                y[s][2 * e + 1] = qbf ? __builtin_bit_cast(float, wv[e] & 0xffff0000u) : f16_bits_to_f32(wv[e] >> 16);
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+#pragma unroll
+            for (int hw = 1; hw < 8; hw <<= 1)
+#pragma unroll
+                for (int i = 0; i < 8; i += 2 * hw)
+#pragma unroll
+                    for (int j = i; j < i + hw; ++j) {
+                        const float a = y[s][j], b = y[s][j + hw];
+                        y[s][j] = a + b;
+                        y[s][j + hw] = a - b;
+                    }
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float o = shfl_xor(y[s][e], 32);
+                y[s][e] = h ? o - y[s][e] : y[s][e] + o;
+            }
+#pragma unroll
+        for (int hw = 1; hw < 8; hw <<= 1)
+#pragma unroll
+            for (int i = 0; i < 8; i += 2 * hw)
+#pragma unroll
+                for (int j = i; j < i + hw; ++j)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float a = y[j][e], b = y[j + hw][e];
+                        y[j][e] = a + b;
+                        y[j + hw][e] = a - b;
+                    }
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            uint32_t wd[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                wd[e] = ((uint32_t)f32_to_f16_bits(y[s][2 * e] * p.rot_c) |
+                         ((uint32_t)f32_to_f16_bits(y[s][2 * e + 1] * p.rot_c) << 16)) ^ qflip;
+            qb[s] = as_v8<V8>(u32x4{wd[0], wd[1], wd[2], wd[3]});
+        }
+        if (tid < 16) lds.cent[tid] = p.cent[tid];
+        __syncthreads();
+    }
 
     f32x16 o[4];
 #pragma unroll
@@ -268,13 +337,39 @@ prefill_kernel(PrefillParams p) {
     // the rows whose V this wave transposes -- as the block's bytes read
     // from their 4-byte floor (a block is 2-byte aligned; the read stays in
     // the entry)
+    constexpr bool kTQ = SRC >= SRC_TQ33;
+    constexpr int TKB = SRC == SRC_TQ44 ? 4 : 3, TVB = SRC == SRC_TQ33 ? 3 : 4;
     constexpr int kBE = SRC == SRC_Q8 ? 34 : 18;        // block bytes
-    constexpr int kNW = SRC == SRC_Q8 ? 9 : 5;          // dwords read per block
+    // words read per lane: GGUF block from its 4-byte floor; TurboQuant:
+    // the 32 codes (12 / 16 bytes) from their floor (the read ends inside the
+    // slot), then the norm (K) or the scale and zero (V) as 16-bit reads
+    constexpr int kNC = kTQ ? (4 * (TKB > TVB ? TKB : TVB)) / 4 + 1 : 0;
+    constexpr int kNW = SRC == SRC_Q8 ? 9 : SRC == SRC_Q4 ? 5 : kTQ ? kNC + 1 : 1;
     const int qr = 32 * ((lane >> 4) & 1) + 4 * w + ((lane >> 2) & 3);
     const int qblk_ = lane & 3;
     uint32_t qraw[kPaged && SRC != SRC_PAGED ? kNW : 1];
+    uint32_t tq_sh = 0;  // TurboQuant: the code run's offset past its 4-byte floor (0 or 2)
     auto issue_q = [&](int t) __attribute__((always_inline)) {
-        if constexpr (SRC == SRC_Q8 || SRC == SRC_Q4) {
+        if constexpr (kTQ) {
+            const int k0 = kv_lo + t * BN;
+            const int kk = min(k0 + qr, kv_end - 1);
+            const int pg0 = page_at(min(k0 + 4 * wu, kv_end - 1));
+            const int pg1 = page_at(min(k0 + 32 + 4 * wu, kv_end - 1));
+            const int pg = (lane & 16) ? pg1 : pg0;
+            // slot fields: K codes at 0, the norm at mse_bytes, V codes at
+            // key_packed, scale and zero at key_packed + val_data; block b's
+            // codes at 4 bits b (the field offsets are multiples of 4 but for
+            // key_packed, and a slot is 2-byte aligned)
+            const uint8_t* slot = p.kp + (int64_t)pg * p.page_bytes + row_in_page(kk);
+            const uint8_t* codes = lane < 32 ? slot + 4 * TKB * qblk_ : slot + p.key_packed + 4 * TVB * qblk_;
+            const uint8_t* halves = lane < 32 ? slot + p.mse_bytes : slot + p.key_packed + p.val_data;
+            tq_sh = (uint32_t)((uintptr_t)codes & 2u);
+            const uint32_t* c4 = reinterpret_cast<const uint32_t*>((uintptr_t)codes & ~(uintptr_t)3);
+            const uint16_t* h2 = reinterpret_cast<const uint16_t*>(halves);
+#pragma unroll
+            for (int i = 0; i < kNC; ++i) qraw[i] = c4[i];
+            qraw[kNC] = (uint32_t)h2[0] | (lane < 32 ? 0u : (uint32_t)h2[1] << 16);
+        } else if constexpr (SRC == SRC_Q8 || SRC == SRC_Q4) {
             const int k0 = kv_lo + t * BN;
             const int kk = min(k0 + qr, kv_end - 1);
             const int pg0 = page_at(min(k0 + 4 * wu, kv_end - 1));
@@ -290,33 +385,110 @@ prefill_kernel(PrefillParams p) {
         }
     };
     // dequantize the held block into the K or V tile of slot SL (fp16 rows
-    // in the swizzled layout of the load-to-LDS path)
+    // in the swizzled layout of the load-to-LDS path).  The 16 lanes of a
+    // 16-byte write pass hold 4 rows x 4 blocks; written in order, lane
+    // (row e, block b) puts chunk j at position 4 (b ^ e) + (j ^ const): 4
+    // distinct positions, a 4-way bank conflict.  TurboQuant rows write chunk
+    // (j + e) & 3 at step j instead: 16 distinct positions, all 64 banks.
     auto store_q = [&](auto slot_c) __attribute__((always_inline)) {
-        if constexpr (SRC == SRC_Q8 || SRC == SRC_Q4) {
+        if constexpr (SRC == SRC_Q8 || SRC == SRC_Q4 || kTQ) {
             constexpr int SL = decltype(slot_c)::value;
-            const bool off2 = (qblk_ & 1) != 0;
-            constexpr int NC = SRC == SRC_Q8 ? 8 : 4;  // code dwords
-            uint32_t c[NC];
+            if constexpr (kTQ) {
+                u32x4 kw[4];
+                const bool kpart = lane < 32;
+                constexpr int NC = 4 * (TKB > TVB ? TKB : TVB) / 4;  // code dwords
+                uint32_t c[NC];
 #pragma unroll
-            for (int i = 0; i < NC; ++i)
-                c[i] = off2 ? qraw[i + 1] : __builtin_amdgcn_alignbyte(qraw[i + 1], qraw[i], 2);
-            const uint32_t d16 = off2 ? qraw[0] >> 16 : qraw[0] & 0xffffu;
-            const f16x2 d2 = __builtin_bit_cast(f16x2, d16 * 0x10001u);
-            uint8_t* dst = lds.tile[SL][lane >> 5] + qr * 256;
+                for (int i = 0; i < NC; ++i) c[i] = __builtin_amdgcn_alignbyte(qraw[i + 1], qraw[i], tq_sh);
+                const uint32_t hw2 = qraw[kNC];
+                auto half_f = [&](uint32_t b) {
+                    return qbf ? __builtin_bit_cast(float, b << 16) : f16_bits_to_f32(b & 0xffffu);
+                };
+                const int bits = kpart ? TKB : TVB;
+                uint32_t code[32];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                u32x4 kw;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    if constexpr (SRC == SRC_Q8) {
-                        const uint32_t wv = c[2 * j + (e >> 1)];  // values 8j + 2e, +1
-                        kw[e] = q8_pair_f16((e & 1) ? wv >> 16 : wv, d2);
-                    } else {
-                        const uint32_t wv = c[2 * (j & 1) + (e >> 1)];  // byte i: value i | value i+16 << 4
-                        kw[e] = q4_pair_f16((e & 1) ? wv >> 16 : wv, j >= 2 ? 4 : 0, d2);
-                    }
+                for (int j = 0; j < 32; ++j) {
+                    // 3-bit: code j at bits 3j of c[0..2]; 4-bit: at bits 4j
+                    const int b0 = 3 * j, wi = b0 >> 5, sh = b0 & 31;
+                    const uint32_t code3 =
+                        (sh <= 29 ? (c[wi] >> sh) : __builtin_amdgcn_alignbit(c[wi + 1], c[wi], sh)) & 7u;
+                    uint32_t code4 = 0;
+                    if constexpr (NC >= 4) code4 = (c[j >> 3] >> (4 * (j & 7))) & 15u;
+                    code[j] = bits == 3 ? code3 : code4;
                 }
-                *reinterpret_cast<u32x4*>(dst + 16 * ((4 * qblk_ + j) ^ swz(qr))) = kw;
+                float v[32];
+                if (kpart) {
+                    // K = C[code] * norm / ||C[codes]|| over the row's 128 dims
+                    // (C[code] * norm without the norm correction)
+                    // (the four lanes of a quad hold its four blocks)
+                    float ss = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < 32; ++j) {
+                        v[j] = lds.cent[code[j]];
+                        ss = __builtin_fmaf(v[j], v[j], ss);
+                    }
+                    ss += __shfl_xor(ss, 1, kWave);
+                    ss += __shfl_xor(ss, 2, kWave);
+                    const float f = half_f(hw2) * (p.norm_corr ? __builtin_amdgcn_rsqf(ss + 1e-16f) : 1.0f);
+#pragma unroll
+                    for (int j = 0; j < 32; ++j) v[j] *= f;
+                } else {
+                    // V = code * scale + zero
+                    const float vs = half_f(hw2), vz = half_f(hw2 >> 16);
+#pragma unroll
+                    for (int j = 0; j < 32; ++j) v[j] = __builtin_fmaf((float)code[j], vs, vz);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        kw[j][e] = (uint32_t)f32_to_f16_bits(v[8 * j + 2 * e]) |
+                                   ((uint32_t)f32_to_f16_bits(v[8 * j + 2 * e + 1]) << 16);
+                // chunk (j + rot) & 3 at step j, by two selects on the bits
+                // of rot (a select by the chunk index compiles to divergent
+                // branches)
+                uint8_t* dst = lds.tile[SL][lane >> 5] + qr * 256;
+                const int rot = qr & 3;
+                const bool b0 = (rot & 1) != 0, b1 = (rot & 2) != 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    u32x4 x;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t t0 = b0 ? kw[(j + 1) & 3][e] : kw[j][e];
+                        const uint32_t t1 = b0 ? kw[(j + 3) & 3][e] : kw[(j + 2) & 3][e];
+                        x[e] = b1 ? t1 : t0;
+                    }
+                    *reinterpret_cast<u32x4*>(dst + 16 * ((4 * qblk_ + ((j + rot) & 3)) ^ swz(qr))) = x;
+                }
+            } else {
+                // q8_0 / q4_0: each chunk written as soon as it is converted,
+                // in order (measured faster here than the conflict-free order,
+                // which needs all four chunks held)
+                const bool off2 = (qblk_ & 1) != 0;
+                constexpr int NC = SRC == SRC_Q8 ? 8 : 4;  // code dwords
+                uint32_t c[NC];
+#pragma unroll
+                for (int i = 0; i < NC; ++i)
+                    c[i] = off2 ? qraw[i + 1] : __builtin_amdgcn_alignbyte(qraw[i + 1], qraw[i], 2);
+                const uint32_t d16 = off2 ? qraw[0] >> 16 : qraw[0] & 0xffffu;
+                const f16x2 d2 = __builtin_bit_cast(f16x2, d16 * 0x10001u);
+                uint8_t* dst = lds.tile[SL][lane >> 5] + qr * 256;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    u32x4 kw;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if constexpr (SRC == SRC_Q8) {
+                            const uint32_t wv = c[2 * j + (e >> 1)];  // values 8j + 2e, +1
+                            kw[e] = q8_pair_f16((e & 1) ? wv >> 16 : wv, d2);
+                        } else {
+                            const uint32_t wv = c[2 * (j & 1) + (e >> 1)];  // byte i: value i | value i+16 << 4
+                            kw[e] = q4_pair_f16((e & 1) ? wv >> 16 : wv, j >= 2 ? 4 : 0, d2);
+                        }
+                    }
+                    *reinterpret_cast<u32x4*>(dst + 16 * ((4 * qblk_ + j) ^ swz(qr))) = kw;
+                }
             }
         }
     };
@@ -792,6 +964,48 @@ void set_tiling(PrefillParams& prm, int num_tokens, int num_heads, int num_kv_he
 }
 
 }  // namespace
+
+int tq_prefill_tiled(void* out, const void* query, const void* kv_cache, const int32_t* block_tables,
+                     const int32_t* token_to_seq, const int32_t* token_positions, int num_tokens, int num_heads,
+                     int num_kv_heads, float scale, int64_t max_blocks, const vmc_tq_config* cfg, int half_dtype,
+                     hipStream_t stream) {
+    if (!tq_config_valid(cfg) || cfg->head_dim != kD || cfg->group_size != 0 || cfg->key_fp8) return VMC_EINVAL;
+    if (half_dtype != VMC_DTYPE_F16 && half_dtype != VMC_DTYPE_BF16) return VMC_EINVAL;
+    if (num_tokens < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 || max_blocks <= 0 ||
+        max_blocks > 0x7fffffff)
+        return VMC_EINVAL;
+    if (num_tokens == 0) return VMC_OK;
+    if (!out || !query || !kv_cache || !block_tables || !token_to_seq || !token_positions) return VMC_EINVAL;
+    if (((uintptr_t)kv_cache & 3) != 0) return VMC_EINVAL;
+    PrefillParams prm = {};
+    prm.out = reinterpret_cast<uint16_t*>(out);
+    prm.q = reinterpret_cast<const uint16_t*>(query);
+    prm.pos = token_positions;
+    set_tiling(prm, num_tokens, num_heads, num_kv_heads, scale);
+    prm.kp = prm.vp = reinterpret_cast<const uint8_t*>(kv_cache);
+    prm.bt = block_tables;
+    prm.tok_seq = token_to_seq;
+    prm.max_blocks = max_blocks;
+    prm.num_seqs = 0x7fffffff;  // the rows' sequences are the caller's to keep in the table
+    prm.E = cfg->slot_size_aligned;
+    prm.page_bytes = (int64_t)kBsP * num_kv_heads * prm.E;
+    prm.hnd = 0;
+    prm.q_bf16 = half_dtype == VMC_DTYPE_BF16;
+    const TQTables& tab = tq_tables(kD, cfg->key_quant_bits);
+    for (int i = 0; i < 16; ++i) prm.cent[i] = i < tab.n_centroids ? tab.centroids[i] : 0.0f;
+    prm.rot_c = tab.rot_c;
+    prm.mse_bytes = cfg->mse_bytes;
+    prm.key_packed = cfg->key_packed_size;
+    prm.val_data = cfg->val_data_bytes;
+    prm.norm_corr = cfg->norm_correction != 0;
+    if ((int64_t)prm.ntiles * prm.Hkv * prm.hgroups > 0x7fffffffLL) return VMC_EINVAL;
+    const int kb = cfg->key_quant_bits, vb = cfg->value_quant_bits;
+    if (kb == 3 && vb == 3) return launch_prefill<false, -1, SRC_TQ33>(prm, stream);
+    if (kb == 4 && vb == 4) return launch_prefill<false, -1, SRC_TQ44>(prm, stream);
+    if (kb == 3 && vb == 4) return launch_prefill<false, -1, SRC_TQ34>(prm, stream);
+    return VMC_EINVAL;
+}
+
 }  // namespace vmc
 
 using namespace vmc;

@@ -419,7 +419,7 @@ __global__ void __launch_bounds__(512) tq_decode_kernel(DecodeParams p) {
                       __attribute__((always_inline)) {
         // ||C[codes]||^2 per token: the Gram diagonal (token r16's value in
         // the lanes with grp == r16 / 4, element r16 % 4); the row factor
-        // scale * norm / ||C||
+        // scale * norm / ||C|| (scale * norm without the norm correction)
         float rowf[2];
 #pragma unroll
         for (int pp = 0; pp < 2; ++pp) {
@@ -429,7 +429,7 @@ __global__ void __launch_bounds__(512) tq_decode_kernel(DecodeParams p) {
             const float csq = sel_bits(sel_bits(gram[0], gram[1], odd_mask), sel_bits(gram[2], gram[3], odd_mask),
                                        hi_mask);
             const uint16_t nb16 = (uint16_t)(pp ? H.nrm >> 16 : H.nrm & 0xffffu);
-            rowf[pp] = p.scale_log2 * half_to_f32<BF>(nb16) * __builtin_amdgcn_rsqf(csq + 1e-16f);
+            rowf[pp] = p.scale_log2 * half_to_f32<BF>(nb16) * (p.norm_corr ? __builtin_amdgcn_rsqf(csq + 1e-16f) : 1.0f);
         }
         // S^T per page against the same Q^T; S column c < 8 keeps the first
         // page's scores (head c), c >= 8 the second's (head c - 8)
