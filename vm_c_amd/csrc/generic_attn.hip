@@ -443,17 +443,12 @@ int store_dispatch(const void* key, const void* value, void* cache, const int64_
 }  // namespace
 
 int gen_attention(const GenArgs& a, hipStream_t s) {
-    const bool k8_bf16_128 = a.D == 128 && a.src == GEN_TQ && a.key_fp8 && a.q_bf16;
-    if (!(generic_head_dim(a.D) || k8_bf16_128) || a.rows < 0 || a.Hq <= 0 || a.Hkv <= 0 || a.Hq % a.Hkv != 0)
+    if ((a.D != 64 && a.D != 128 && a.D != 256) || a.rows < 0 || a.Hq <= 0 || a.Hkv <= 0 || a.Hq % a.Hkv != 0)
         return VMC_EINVAL;
     if (a.rows == 0) return VMC_OK;
     if (a.rows > 0x7fffffff) return VMC_EINVAL;
-    if (k8_bf16_128) {
-        // head_dim 128 has tuned kernels for every other source and dtype
-        if (a.vb != 4) return VMC_EINVAL;
-        return launch_gen<128, GEN_TQ, 8, 4, true>(a, TQTables{}, s);
-    }
     if (a.D == 64) return a.q_bf16 ? dispatch_src<64, true>(a, s) : dispatch_src<64, false>(a, s);
+    if (a.D == 128) return a.q_bf16 ? dispatch_src<128, true>(a, s) : dispatch_src<128, false>(a, s);
     return a.q_bf16 ? dispatch_src<256, true>(a, s) : dispatch_src<256, false>(a, s);
 }
 

@@ -13,8 +13,12 @@ namespace vmc {
 
 inline bool generic_head_dim(int d) { return d == 64 || d == 256; }
 
-// gen_attention also serves head_dim 128 for fp8-key TurboQuant slots with
-// bf16 q, out and halves (the tuned head_dim 128 decode reads fp16 halves)
+// gen_attention also serves head_dim 128 where the tuned decode kernels do
+// not: more than 8 KV heads or more than 16 query heads per KV head, and
+// fp8-key TurboQuant slots with bf16 q, out and halves
+inline bool beyond_tuned_decode(int d, int hq, int hkv) {
+    return d == 128 && hkv > 0 && (hkv > 8 || hq / hkv > 16);
+}
 
 // K/V source of one attention call
 enum GenSrc { GEN_F16 = 0, GEN_BF16 = 1, GEN_Q8 = 2, GEN_Q4 = 3, GEN_LOCAL = 4, GEN_TQ = 5 };

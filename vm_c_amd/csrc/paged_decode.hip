@@ -1364,8 +1364,9 @@ int paged_decode_rows(void* out, const void* query, const void* key_cache, const
                       int head_dim, int block_size, int max_num_blocks_per_req, float scale,
                       int q_dtype, int kv_format, int layout, int max_num_kv_splits, void* workspace,
                       size_t workspace_bytes, vmc_stream_t stream) {
-    if (generic_head_dim(head_dim)) {
-        // head_dim 64 / 256: one wave per (row, query head), no workspace
+    if (generic_head_dim(head_dim) || beyond_tuned_decode(head_dim, num_heads, num_kv_heads)) {
+        // head_dim 64 / 256, and head counts past the tuned kernels' (see
+        // beyond_tuned_decode): one wave per (row, query head), no workspace
         if (batch_size < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 ||
             block_size <= 0 || max_num_blocks_per_req <= 0)
             return VMC_EINVAL;
@@ -1486,10 +1487,12 @@ int tq_decode_rows(void* output, const void* query, const void* kv_cache, const 
     if (!tq_config_valid(cfg) || cfg->head_dim != head_dim) return VMC_EINVAL;
     if (half_dtype != VMC_DTYPE_F16 && half_dtype != VMC_DTYPE_BF16) return VMC_EINVAL;
     if (max_num_blocks_per_req > 0x7fffffff) return VMC_EINVAL;
-    if (generic_head_dim(head_dim) || (cfg->key_fp8 && half_dtype == VMC_DTYPE_BF16)) {
-        // head_dim 64 / 256, and fp8 keys with bf16 halves: one wave per
-        // (row, query head), no workspace; q, out and the stored halves are
-        // half_dtype
+    if (generic_head_dim(head_dim) || (cfg->key_fp8 && half_dtype == VMC_DTYPE_BF16) ||
+        beyond_tuned_decode(head_dim, num_heads, num_kv_heads)) {
+        // head_dim 64 / 256, fp8 keys with bf16 halves, and head counts past
+        // the tuned kernels': one wave per (row, query head), no workspace;
+        // q, out and the stored halves are half_dtype (the per-32-group
+        // variant has no such kernel)
         if (cfg->group_size != 0) return VMC_EINVAL;
         if (batch_size < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 ||
             block_size <= 0 || max_num_blocks_per_req <= 0)
