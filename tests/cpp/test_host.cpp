@@ -12,6 +12,7 @@
 #include "vm_c/attention_backend.hpp"
 #include "vm_c/attention_metadata.hpp"
 #include "vm_c/kv_cache_manager.hpp"
+#include "vm_c/turboquant_kv_bridge.hpp"
 
 using namespace vm_c;
 
@@ -315,6 +316,71 @@ static void test_errors() {
     CHECK(vmc_kv_format_of("q4_0", ScalarType::FLOAT16) == VMC_KV_Q4_0);
 }
 
+// the TurboQuant attention node: set-up, per-rank head split, op_params
+// decoding and every error the node raises before a launch
+static void test_tq_bridge() {
+    using official::TurboQuantKvBridge;
+    KVCacheManager tq(cache_cfg("auto", "turboquant_3bit_nc"), ModelConfig{}, 4, 4, 128, 0, false, hostmem());
+    tq.set_tq_boundary_layers({0});
+    tq.allocate_gpu_blocks_for_group(0, 4);
+    tq.allocate_gpu_blocks_for_group(1, 4);
+    TurboQuantKvBridge b;
+    b.initialize(cache_cfg("auto", "turboquant_3bit_nc"), 16, 4, 128, &tq, 0, 4, 1, ScalarType::FLOAT16);
+    CHECK(b.num_attention_heads() == 16 && b.num_kv_heads() == 4 && b.head_dim() == 128);
+    CHECK(b.tq_config().slot_size_aligned == 102 && b.tq_layer_enabled_count() == 3);
+    CHECK(!b.kv_cache_ptr(0) && b.kv_cache_ptr(1) == tq.key_cache_ptr(1) && !b.kv_cache_ptr(4));
+    CHECK(!vm_c_tq_bridge_layer_uses_turboquant(nullptr, 1));
+    CHECK(!vm_c_tq_bridge_layer_uses_turboquant(&b, 0) && vm_c_tq_bridge_layer_uses_turboquant(&b, 2));
+    TurboQuantKvBridge split;
+    split.initialize(cache_cfg("auto", "turboquant_3bit_nc"), 16, 4, 128, &tq, 0, 4, 8);
+    CHECK(split.num_attention_heads() == 2 && split.num_kv_heads() == 1);
+    auto throws = [](const std::function<void()>& f, const char* what) {
+        try {
+            f();
+        } catch (const std::runtime_error& e) {
+            return std::string(e.what()).find(what) != std::string::npos;
+        }
+        return false;
+    };
+    CHECK(throws([&] { split.initialize(cache_cfg("auto", "turboquant_3bit_nc"), 16, 4, 128, &tq, 0, 4, 0); },
+                 "tp_size must be positive"));
+    CHECK(throws([&] { split.initialize(cache_cfg("auto", "turboquant_3bit_nc"), 4, 4, 128, &tq, 0, 4, 8); },
+                 "num_attention_heads per rank is zero"));
+    KVCacheManager plain(cache_cfg("fp16"), ModelConfig{}, 1, 4, 128, 0, false, hostmem());
+    CHECK(throws([&] { split.initialize(cache_cfg("fp16"), 16, 4, 128, &plain, 0, 1); }, "is not TurboQuant"));
+    // op_params {layer, kq_scale, bridge}
+    auto params = [](int32_t layer, float scale, void* br) {
+        std::vector<unsigned char> p(official::kTqAttnOpBytes);
+        std::memcpy(p.data() + official::kTqAttnOpLayer, &layer, 4);
+        std::memcpy(p.data() + official::kTqAttnOpScale, &scale, 4);
+        std::memcpy(p.data() + official::kTqAttnOpBridge, &br, sizeof(br));
+        return p;
+    };
+    // q as the head-split view [128, 16, 3], as one token [2048, 1], and as
+    // [2048, 3] (third stride set, second extent > 1: read as head-split, so
+    // 6144 wide, as the reference reads it)
+    const int64_t ne3[4] = {128, 16, 3, 1}, ne2[4] = {2048, 1, 1, 1}, bad[4] = {128, 8, 3, 1};
+    const int64_t flat3[4] = {2048, 3, 1, 1};
+    const size_t nb3[4] = {2, 256, 4096, 12288}, nb2[4] = {2, 4096, 4096, 4096}, nbf[4] = {2, 4096, 12288, 12288};
+    int x = 0;
+    CHECK(throws([&] { official::turboquant_attn_op(params(1, 0.1f, nullptr).data(), &x, ne3, nb3, &x, &x, &x); },
+                 "null bridge"));
+    CHECK(throws([&] { official::turboquant_attn_op(params(1, 0.1f, &b).data(), &x, bad, nb3, &x, &x, &x); },
+                 "q embedding dim mismatch: ne0=1024 expected=2048"));
+    CHECK(throws([&] { official::turboquant_attn_op(params(0, 0.1f, &b).data(), &x, ne3, nb3, &x, &x, &x); },
+                 "null kv cache for layer 0"));
+    CHECK(throws([&] { official::turboquant_attn_op(params(1, 0.1f, &b).data(), &x, flat3, nbf, &x, &x, &x); },
+                 "ne0=6144 expected=2048"));
+    CHECK(throws([&] { official::turboquant_attn_op(params(1, 0.1f, &b).data(), &x, ne3, nb3, &x, &x, &x); },
+                 "slot_mapping not set"));
+    CHECK(throws([&] { official::turboquant_attn_op(params(2, 0.1f, &b).data(), &x, ne2, nb2, &x, &x, &x); },
+                 "slot_mapping not set"));
+    b.set_batch_metadata(nullptr, nullptr, nullptr, 3, 3, 4, 16, true, 3, 0, nullptr, nullptr, nullptr);
+    CHECK(b.is_prefill() && b.num_prefill_tokens() == 3);
+    b.mark_decode_mode(5);
+    CHECK(!b.is_prefill() && b.num_decode_tokens() == 5 && b.num_tokens() == 5 && b.num_prefill_tokens() == 0);
+}
+
 int main() {
     const std::vector<std::pair<const char*, std::function<void()>>> tests = {
         {"free_queue", test_free_queue},
@@ -326,6 +392,7 @@ int main() {
         {"swap", test_swap},
         {"metadata", test_metadata},
         {"errors", test_errors},
+        {"tq_bridge", test_tq_bridge},
     };
     for (auto& t : tests) {
         const int before = g_fail;

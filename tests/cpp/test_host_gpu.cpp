@@ -14,6 +14,7 @@
 #include "vm_c/attention_metadata.hpp"
 #include "vm_c/kernels_fused_attn.hpp"
 #include "vm_c/kv_cache_manager.hpp"
+#include "vm_c/turboquant_kv_bridge.hpp"
 #include "vmc_oracle.h"
 
 using namespace vm_c;
@@ -505,6 +506,89 @@ static void test_page_movement() {
     HIP_CHECK(hipHostFree(host));
 }
 
+// the ggml TurboQuant attention node (turboquant_attn_op) over layer 1 of a
+// two-layer pool: a prefill of three sequences with one query row per token
+// (its sequence's block-table row, length position + 1), then a decode step;
+// q in the head-split view [D, Hq, T]
+static void test_tq_bridge_node(const char* method) {
+    std::printf("case: TurboQuant attention node %s\n", method);
+    std::fflush(stdout);
+    using official::TurboQuantKvBridge;
+    CacheConfig cc;
+    cc.kv_cache_quant_method = method;
+    KVCacheManager mgr(cc, ModelConfig{}, 2, Hkv, D);
+    mgr.allocate_gpu_blocks_for_group(0, 64);
+    TurboQuantKvBridge br;
+    br.initialize(cc, Hq, Hkv, D, &mgr, 0, 2, 1, ScalarType::FLOAT16);
+    br.reserve_decode(512, 64);
+    void* pool = mgr.key_cache_ptr(1);
+    const size_t pool_n = (size_t)64 * mgr.group(0).bytes_per_block;
+    HIP_CHECK(hipMemset(pool, 0, pool_n));
+    HIP_CHECK(hipMemset(mgr.key_cache_ptr(0), 0, pool_n));
+    orc_tq_layout L;
+    CHECK(orc_tq_layout_from_method(D, method, &L) == 0);
+    std::vector<float> C(16), M(15);
+    orc_tq_lloyd_max(C.data(), D, L.key_quant_bits);
+    orc_tq_midpoints(C.data(), L.n_centroids, M.data());
+    std::vector<uint8_t> ref(pool_n, 0);
+    const float scale = 1.0f / std::sqrt((float)D);
+    std::vector<unsigned char> op(official::kTqAttnOpBytes);
+    const int32_t layer = 1;
+    void* bp = &br;
+    std::memcpy(op.data() + official::kTqAttnOpLayer, &layer, 4);
+    std::memcpy(op.data() + official::kTqAttnOpScale, &scale, 4);
+    std::memcpy(op.data() + official::kTqAttnOpBridge, &bp, sizeof(bp));
+    const std::vector<int> lens = {40, 17, 300};
+    for (int step = 0; step < 2; ++step) {
+        std::vector<ScheduledRequest> rq(lens.size());
+        for (size_t i = 0; i < lens.size(); ++i) {
+            rq[i].request_id = "r" + std::to_string(i);
+            if (step == 0) {
+                rq[i].num_scheduled_tokens = lens[i];
+                rq[i].is_prefill = true;
+            } else {
+                rq[i].num_computed_tokens = lens[i];
+            }
+        }
+        HostBatchMetadata hm = build_batch_metadata(mgr, rq);
+        CHECK(hm.ok);
+        const int T = hm.num_tokens, mb = hm.max_num_blocks_per_req;
+        std::vector<int32_t> bt_rows((size_t)T * mb), len_rows(T);
+        for (int t = 0; t < T; ++t) {
+            const int sq = hm.token_to_seq[t];
+            std::copy(hm.block_tables.begin() + (size_t)sq * mb, hm.block_tables.begin() + (size_t)(sq + 1) * mb,
+                      bt_rows.begin() + (size_t)t * mb);
+            len_rows[t] = hm.token_positions[t] + 1;
+        }
+        std::vector<uint16_t> K((size_t)T * Hkv * D), V(K.size()), Q((size_t)T * Hq * D);
+        orc_randn_f16(K.data(), (int64_t)K.size(), 20 + step, 1);
+        orc_randn_f16(V.data(), (int64_t)V.size(), 20 + step, 2);
+        orc_randn_f16(Q.data(), (int64_t)Q.size(), 20 + step, 3);
+        Dev<uint16_t> dK(K), dV(V), dQ(Q), dO(Q.size());
+        Dev<int64_t> dslots(hm.slot_mapping);
+        Dev<int32_t> dbt(bt_rows), dlen(len_rows);
+        br.set_batch_metadata(dslots.p, dbt.p, dlen.p, T, hm.num_reqs, mb, BS, step == 0, step == 0 ? T : 0,
+                              step == 0 ? 0 : T, nullptr, nullptr, nullptr);
+        if (step == 1) br.mark_decode_mode(T);
+        const int64_t ne[4] = {D, Hq, T, 1};
+        const size_t nb[4] = {2, (size_t)2 * D, (size_t)2 * D * Hq, (size_t)2 * D * Hq * T};
+        official::turboquant_attn_op(op.data(), dQ.p, ne, nb, dK.p, dV.p, dO.p);
+        HIP_CHECK(hipDeviceSynchronize());
+        std::vector<uint8_t> got = pool_bytes(pool, pool_n);
+        orc_tq_store(K.data(), V.data(), ref.data(), hm.slot_mapping.data(), T, Hkv, D, BS, &L, M.data(), 0);
+        CHECK(got == ref);
+        const std::vector<uint8_t> other = pool_bytes(mgr.key_cache_ptr(0), pool_n);
+        CHECK(std::all_of(other.begin(), other.end(), [](uint8_t b) { return b == 0; }));  // layer 0 untouched
+        std::vector<double> ex(Q.size());
+        orc_tq_decode_exact(ex.data(), Q.data(), got.data(), bt_rows.data(), len_rows.data(), T, Hq, Hkv, D, scale,
+                            BS, mb, &L, C.data(), 0, 0);
+        double err = 0;
+        CHECK(close(dO.get(), ex, &err));
+        std::printf("  %s: %d rows, max err %.3g\n", step == 0 ? "prefill" : "decode", T, err);
+    }
+    for (size_t i = 0; i < lens.size(); ++i) mgr.free_slots("r" + std::to_string(i));
+}
+
 int main() {
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || n < 1) {
@@ -522,6 +606,7 @@ int main() {
         test_fused_norm_rope("q4_0");
         test_fused_norm_rope("auto");
         test_page_movement();
+        for (const char* m : {"turboquant_3bit_nc", "turboquant_k3v4_nc"}) test_tq_bridge_node(m);
     } catch (const std::exception& e) {
         std::printf("FAIL exception: %s\n", e.what());
         return 1;
