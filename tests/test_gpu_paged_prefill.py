@@ -99,7 +99,7 @@ def test_turboquant_prefill_over_cached_prefix(dev, method, bf16, chunk):
     new = np.array([37, 20, 64]) if chunk == "tiled" else np.array([5, 3, 7])
     lens = prefix + new
     Hq, Hkv = 16, 4
-    w = make_workload(lens, Hq=Hq, Hkv=Hkv, seed=41, pool_slack=2)
+    w = make_workload(lens, Hq=Hq, Hkv=Hkv, seed=41, pool_slack=2, holes=3)
     cfg = capi.tq_config(128, method)
     cache = _tq_cache(dev, w, cfg, bf16)
     tok_seq = np.concatenate([np.full(new[b], b) for b in range(len(lens))]).astype(np.int32)
