@@ -88,9 +88,9 @@ def _tq_exact(method, qbits, cache, bt_rows, len_rows, Hkv, scale, bf16):
 def test_turboquant_prefill_over_cached_prefix(dev, method, bf16, chunk):
     """vmc_turboquant_prefill_attention (no reference counterpart: the
     reference's TurboQuant prefill attends only the step's local K/V).  A
-    step of 121 tokens over codebook slots takes the tiled prefill; one of 15
-    tokens (and every step over fp8-key or per-32-group slots) one decode row
-    per token."""
+    step of 121 tokens over reference-layout slots (codebook or fp8 keys)
+    takes the tiled prefill; one of 15 tokens (and every step over
+    per-32-group slots) one decode row per token."""
     import torch
     from vm_c_amd import capi
     if method.endswith("_g32") and bf16:
@@ -117,12 +117,13 @@ def test_turboquant_prefill_over_cached_prefix(dev, method, bf16, chunk):
     assert ok, f"max err {err}"
 
 
-@pytest.mark.parametrize("method", ["turboquant_3bit_nc", "turboquant_4bit_nc"])
+@pytest.mark.parametrize("method", ["turboquant_3bit_nc", "turboquant_4bit_nc", "turboquant_k8v4"])
 def test_turboquant_prefill_chunk_over_long_prefix(dev, method):
-    """A 2048-token chunk over a 30720-token prefix of codebook slots, 32/8
-    heads (the tiled prefill): every row against the per-token path (steps
-    of 15 tokens, which the test above pins to the oracle), 32 sampled tokens
-    x all heads against the oracle's fp64 attention."""
+    """A 2048-token chunk over a 30720-token prefix of reference-layout slots
+    (codebook or fp8 keys), 32/8 heads (the tiled prefill): every row against
+    the per-token path (steps of 15 tokens, which the test above pins to the
+    oracle), 32 sampled tokens x all heads against the oracle's fp64
+    attention."""
     import torch
     from vm_c_amd import capi
     prefix, new = 30720, 2048

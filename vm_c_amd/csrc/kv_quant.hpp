@@ -134,4 +134,15 @@ __device__ __forceinline__ uint32_t q4_pair_f16(uint32_t w16, int sh, f16x2 d2) 
     return __builtin_bit_cast(uint32_t, x * d2);
 }
 
+// fp16 bits of one of the reference's fp8 key codes (low byte of b):
+// e4m3 (1 + m/8) 2^(e-7) -> exponent field e + 8; e4b15 (1 + m/8) 2^(e-15)
+// -> exponent field e, or for e = 0 the fp16 subnormal (8 + m) 2^-18; the
+// zero code (either sign) -> signed zero.  Exact.
+__device__ __forceinline__ uint16_t fp8_f16_bits(uint32_t b, int e4b15) {
+    const uint32_t mag = b & 0x7fu, m = b & 7u;
+    const uint32_t h = !e4b15 ? (mag ? (mag << 7) + 0x2000u : 0u)
+                              : ((mag >> 3) ? (mag << 7) : (m ? 0x200u + (m << 6) : 0u));
+    return (uint16_t)(h | ((b & 0x80u) << 8));
+}
+
 }  // namespace vmc

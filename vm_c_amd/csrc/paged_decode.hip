@@ -95,16 +95,6 @@ struct Geo {
     static constexpr int nbuf = dma ? pf + 2 : pf;
 };
 
-// fp16 bits of one of the reference's fp8 key codes (low byte of b):
-// e4m3 (1 + m/8) 2^(e-7) -> exponent field e + 8; e4b15 (1 + m/8) 2^(e-15)
-// -> exponent field e, or for e = 0 the fp16 subnormal (8 + m) 2^-18; the
-// zero code (either sign) -> signed zero.  Exact.
-__device__ __forceinline__ uint16_t fp8_f16_bits(uint32_t b, int e4b15) {
-    const uint32_t mag = b & 0x7fu, m = b & 7u;
-    const uint32_t h = !e4b15 ? (mag ? (mag << 7) + 0x2000u : 0u)
-                              : ((mag >> 3) ? (mag << 7) : (m ? 0x200u + (m << 6) : 0u));
-    return (uint16_t)(h | ((b & 0x80u) << 8));
-}
 // Codes 2e and 2e+1 of an 8-code word of the per-32-group variant -> packed
 // fp16 code * d + m (4-bit, one fused rounding) or (code - 4) * d (3-bit,
 // exact operand times d, one rounding): the two fields go to the 16-bit
@@ -1677,10 +1667,10 @@ extern "C" int vmc_turboquant_prefill_attention(void* output, const void* query,
     if (num_tokens > 0 && (!token_to_seq || !token_positions)) return VMC_EINVAL;
     // chunks of 16 tokens or more over reference-layout slots: the tiled
     // prefill (each 64-key tile of a sequence read once per block of query
-    // rows); fewer tokens, fp8 keys and the per-32-group variant: one decode
-    // row per token
+    // rows); fewer tokens and the per-32-group variant: one decode row per
+    // token
     if (head_dim == kD && block_size == kBs && num_tokens >= 16 && tq_config_valid(cfg) && cfg->head_dim == kD &&
-        cfg->group_size == 0 && !cfg->key_fp8 && ((uintptr_t)kv_cache & 3) == 0)
+        cfg->group_size == 0 && ((uintptr_t)kv_cache & 3) == 0)
         return tq_prefill_tiled(output, query, kv_cache, block_tables, token_to_seq, token_positions, num_tokens,
                                 num_heads, num_kv_heads, scale, max_num_blocks_per_req, cfg, half_dtype,
                                 reinterpret_cast<hipStream_t>(stream));

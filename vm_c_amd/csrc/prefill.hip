@@ -50,9 +50,10 @@ typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 // K/V sources of the kernel: this step's contiguous rows, or the paged cache
 // (f16 / bf16 pages by load-to-LDS transfers; q8_0 / q4_0 and TurboQuant
-// pages (key / value bits 3/3, 4/4, 3/4) dequantized to fp16 through
-// registers)
-constexpr int SRC_LOCAL = 0, SRC_PAGED = 1, SRC_Q8 = 2, SRC_Q4 = 3, SRC_TQ33 = 4, SRC_TQ44 = 5, SRC_TQ34 = 6;
+// pages (key / value bits 3/3, 4/4, 3/4; fp8 keys with 4-bit values)
+// dequantized to fp16 through registers)
+constexpr int SRC_LOCAL = 0, SRC_PAGED = 1, SRC_Q8 = 2, SRC_Q4 = 3, SRC_TQ33 = 4, SRC_TQ44 = 5, SRC_TQ34 = 6,
+              SRC_K8 = 7;
 
 struct PrefillParams {
     uint16_t* out;
@@ -73,6 +74,7 @@ struct PrefillParams {
     float rot_c;
     int mse_bytes, key_packed, val_data;
     int norm_corr;  // keys scaled by 1 / ||C[codes]|| (else by the stored norm alone)
+    int fp8_e4b15;  // fp8 keys: e4b15 (1) or e4m3 (0) codes
     int T, Hq, Hkv, G;
     float scale_log2;
     int ntiles;          // query blocks of qb rows
@@ -222,7 +224,7 @@ prefill_kernel(PrefillParams p) {
             qb[s] = as_v8<V8>(u32x4{wv[0] ^ qflip, wv[1] ^ qflip, wv[2] ^ qflip, wv[3] ^ qflip});
         }
     }
-    if constexpr (SRC >= SRC_TQ33) {
+    if constexpr (SRC >= SRC_TQ33 && SRC != SRC_K8) {
         // TurboQuant keys are stored rotated: q_rot = H q / sqrt(d), in fp32
         // from the raw q.  Dim 16 s + 8 h + e: butterflies over e (half-widths
         // 1, 2, 4) and s (16, 32, 64) in the lane, over h (8) with the lane
@@ -338,11 +340,13 @@ prefill_kernel(PrefillParams p) {
     // from their 4-byte floor (a block is 2-byte aligned; the read stays in
     // the entry)
     constexpr bool kTQ = SRC >= SRC_TQ33;
-    constexpr int TKB = SRC == SRC_TQ44 ? 4 : 3, TVB = SRC == SRC_TQ33 ? 3 : 4;
+    constexpr bool kK8 = SRC == SRC_K8;  // fp8 keys: one byte per dim, 4-byte aligned
+    constexpr int TKB = SRC == SRC_TQ44 ? 4 : kK8 ? 8 : 3, TVB = SRC == SRC_TQ33 ? 3 : 4;
     constexpr int kBE = SRC == SRC_Q8 ? 34 : 18;        // block bytes
     // words read per lane: GGUF block from its 4-byte floor; TurboQuant:
-    // the 32 codes (12 / 16 bytes) from their floor (the read ends inside the
-    // slot), then the norm (K) or the scale and zero (V) as 16-bit reads
+    // the 32 codes (12 / 16 / 32 bytes) from their floor, TKB + 1 words for K
+    // lanes and TVB + 1 for V lanes (the reads end inside the slot), then the
+    // norm (K) or the scale and zero (V) as 16-bit reads
     constexpr int kNC = kTQ ? (4 * (TKB > TVB ? TKB : TVB)) / 4 + 1 : 0;
     constexpr int kNW = SRC == SRC_Q8 ? 9 : SRC == SRC_Q4 ? 5 : kTQ ? kNC + 1 : 1;
     const int qr = 32 * ((lane >> 4) & 1) + 4 * w + ((lane >> 2) & 3);
@@ -367,7 +371,7 @@ prefill_kernel(PrefillParams p) {
             const uint32_t* c4 = reinterpret_cast<const uint32_t*>((uintptr_t)codes & ~(uintptr_t)3);
             const uint16_t* h2 = reinterpret_cast<const uint16_t*>(halves);
 #pragma unroll
-            for (int i = 0; i < kNC; ++i) qraw[i] = c4[i];
+            for (int i = 0; i < kNC; ++i) qraw[i] = (lane < 32 ? i <= TKB : i <= TVB) ? c4[i] : 0u;
             qraw[kNC] = (uint32_t)h2[0] | (lane < 32 ? 0u : (uint32_t)h2[1] << 16);
         } else if constexpr (SRC == SRC_Q8 || SRC == SRC_Q4) {
             const int k0 = kv_lo + t * BN;
@@ -409,41 +413,59 @@ prefill_kernel(PrefillParams p) {
 #pragma unroll
                 for (int j = 0; j < 32; ++j) {
                     // 3-bit: code j at bits 3j of c[0..2]; 4-bit: at bits 4j
-                    const int b0 = 3 * j, wi = b0 >> 5, sh = b0 & 31;
-                    const uint32_t code3 =
-                        (sh <= 29 ? (c[wi] >> sh) : __builtin_amdgcn_alignbit(c[wi + 1], c[wi], sh)) & 7u;
-                    uint32_t code4 = 0;
+                    uint32_t code3 = 0, code4 = 0;
+                    if constexpr (TKB == 3 || TVB == 3) {
+                        const int b0 = 3 * j, wi = b0 >> 5, sh = b0 & 31;
+                        code3 = (sh <= 29 ? (c[wi] >> sh) : __builtin_amdgcn_alignbit(c[wi + 1], c[wi], sh)) & 7u;
+                    }
                     if constexpr (NC >= 4) code4 = (c[j >> 3] >> (4 * (j & 7))) & 15u;
                     code[j] = bits == 3 ? code3 : code4;
                 }
+                auto kw_from = [&](const float (&v)[32]) __attribute__((always_inline)) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            kw[j][e] = (uint32_t)f32_to_f16_bits(v[8 * j + 2 * e]) |
+                                       ((uint32_t)f32_to_f16_bits(v[8 * j + 2 * e + 1]) << 16);
+                };
                 float v[32];
                 if (kpart) {
-                    // K = C[code] * norm / ||C[codes]|| over the row's 128 dims
-                    // (C[code] * norm without the norm correction)
-                    // (the four lanes of a quad hold its four blocks)
-                    float ss = 0.0f;
+                    if constexpr (kK8) {
+                        // fp8 keys: each of the lane's 32 bytes is exact in fp16
 #pragma unroll
-                    for (int j = 0; j < 32; ++j) {
-                        v[j] = lds.cent[code[j]];
-                        ss = __builtin_fmaf(v[j], v[j], ss);
+                        for (int j = 0; j < 4; ++j)
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                const int b = 8 * j + 2 * e;  // bytes b and b + 1 share a word
+                                const uint32_t wv = c[b >> 2] >> (8 * (b & 3));
+                                kw[j][e] = (uint32_t)fp8_f16_bits(wv, p.fp8_e4b15) |
+                                           ((uint32_t)fp8_f16_bits(wv >> 8, p.fp8_e4b15) << 16);
+                            }
+                    } else {
+                        // K = C[code] * norm / ||C[codes]|| over the row's 128 dims
+                        // (C[code] * norm without the norm correction)
+                        // (the four lanes of a quad hold its four blocks)
+                        float ss = 0.0f;
+#pragma unroll
+                        for (int j = 0; j < 32; ++j) {
+                            v[j] = lds.cent[code[j]];
+                            ss = __builtin_fmaf(v[j], v[j], ss);
+                        }
+                        ss += __shfl_xor(ss, 1, kWave);
+                        ss += __shfl_xor(ss, 2, kWave);
+                        const float f = half_f(hw2) * (p.norm_corr ? __builtin_amdgcn_rsqf(ss + 1e-16f) : 1.0f);
+#pragma unroll
+                        for (int j = 0; j < 32; ++j) v[j] *= f;
+                        kw_from(v);
                     }
-                    ss += __shfl_xor(ss, 1, kWave);
-                    ss += __shfl_xor(ss, 2, kWave);
-                    const float f = half_f(hw2) * (p.norm_corr ? __builtin_amdgcn_rsqf(ss + 1e-16f) : 1.0f);
-#pragma unroll
-                    for (int j = 0; j < 32; ++j) v[j] *= f;
                 } else {
                     // V = code * scale + zero
                     const float vs = half_f(hw2), vz = half_f(hw2 >> 16);
 #pragma unroll
                     for (int j = 0; j < 32; ++j) v[j] = __builtin_fmaf((float)code[j], vs, vz);
+                    kw_from(v);
                 }
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        kw[j][e] = (uint32_t)f32_to_f16_bits(v[8 * j + 2 * e]) |
-                                   ((uint32_t)f32_to_f16_bits(v[8 * j + 2 * e + 1]) << 16);
                 // chunk (j + rot) & 3 at step j, by two selects on the bits
                 // of rot (a select by the chunk index compiles to divergent
                 // branches)
@@ -969,7 +991,7 @@ int tq_prefill_tiled(void* out, const void* query, const void* kv_cache, const i
                      const int32_t* token_to_seq, const int32_t* token_positions, int num_tokens, int num_heads,
                      int num_kv_heads, float scale, int64_t max_blocks, const vmc_tq_config* cfg, int half_dtype,
                      hipStream_t stream) {
-    if (!tq_config_valid(cfg) || cfg->head_dim != kD || cfg->group_size != 0 || cfg->key_fp8) return VMC_EINVAL;
+    if (!tq_config_valid(cfg) || cfg->head_dim != kD || cfg->group_size != 0) return VMC_EINVAL;
     if (half_dtype != VMC_DTYPE_F16 && half_dtype != VMC_DTYPE_BF16) return VMC_EINVAL;
     if (num_tokens < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 || max_blocks <= 0 ||
         max_blocks > 0x7fffffff)
@@ -991,15 +1013,19 @@ int tq_prefill_tiled(void* out, const void* query, const void* kv_cache, const i
     prm.page_bytes = (int64_t)kBsP * num_kv_heads * prm.E;
     prm.hnd = 0;
     prm.q_bf16 = half_dtype == VMC_DTYPE_BF16;
-    const TQTables& tab = tq_tables(kD, cfg->key_quant_bits);
-    for (int i = 0; i < 16; ++i) prm.cent[i] = i < tab.n_centroids ? tab.centroids[i] : 0.0f;
-    prm.rot_c = tab.rot_c;
+    if (!cfg->key_fp8) {
+        const TQTables& tab = tq_tables(kD, cfg->key_quant_bits);
+        for (int i = 0; i < 16; ++i) prm.cent[i] = i < tab.n_centroids ? tab.centroids[i] : 0.0f;
+        prm.rot_c = tab.rot_c;
+    }
+    prm.fp8_e4b15 = cfg->fp8_e4b15 ? 1 : 0;
     prm.mse_bytes = cfg->mse_bytes;
     prm.key_packed = cfg->key_packed_size;
     prm.val_data = cfg->val_data_bytes;
     prm.norm_corr = cfg->norm_correction != 0;
     if ((int64_t)prm.ntiles * prm.Hkv * prm.hgroups > 0x7fffffffLL) return VMC_EINVAL;
     const int kb = cfg->key_quant_bits, vb = cfg->value_quant_bits;
+    if (cfg->key_fp8) return vb == 4 ? launch_prefill<false, -1, SRC_K8>(prm, stream) : VMC_EINVAL;
     if (kb == 3 && vb == 3) return launch_prefill<false, -1, SRC_TQ33>(prm, stream);
     if (kb == 4 && vb == 4) return launch_prefill<false, -1, SRC_TQ44>(prm, stream);
     if (kb == 3 && vb == 4) return launch_prefill<false, -1, SRC_TQ34>(prm, stream);

@@ -11,7 +11,8 @@
 namespace vmc {
 
 // Chunked prefill over TurboQuant slots of the reference layout (codebook
-// keys, 3/3, 4/4 or 3/4 bits; head_dim 128, block size 16): token t attends
+// keys, 3/3, 4/4 or 3/4 bits, or fp8 keys with 4-bit values; head_dim 128,
+// block size 16): token t attends
 // positions 0 .. token_positions[t] of sequence token_to_seq[t] through its
 // block-table row.  q, out and the stored halves are half_dtype.
 int tq_prefill_tiled(void* out, const void* query, const void* kv_cache, const int32_t* block_tables,
