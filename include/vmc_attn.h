@@ -76,9 +76,12 @@ int vmc_reshape_and_cache(const void* key, const void* value, void* key_cache,
  *   max_num_kv_splits  1: one pass per sequence, no workspace (paged_attention_v1);
  *                 > 1: the batch's pages are split evenly over the GPU with at
  *                 most batch * max_num_kv_splits pieces; <= 0: no cap
- * Limits: head_dim == 128, num_heads / num_kv_heads <= 16, num_kv_heads <= 8.
- * Two launches on `stream` (split pass, merge of cut sequences); no host
- * synchronisation.  The workspace size depends on the current device's CU count.
+ * Limits: head_dim 64, 128 or 256; block_size 16 at head_dim 128.  At
+ * head_dim 128 with num_kv_heads <= 8 and num_heads / num_kv_heads <= 16 the
+ * tuned kernel runs: two launches on `stream` (split pass, merge of cut
+ * sequences).  Other head dims and head counts run a one-wave-per-row kernel
+ * (one launch, no workspace).  No host synchronisation.  The workspace size
+ * depends on the current device's CU count.
  */
 size_t vmc_paged_decode_workspace_size(int batch_size, int num_heads, int num_kv_heads,
                                        int head_dim, int max_num_blocks_per_req, int block_size,
@@ -181,7 +184,8 @@ int vmc_paged_attention_prefill(void* out, const void* query, const void* key_ca
  * (load-to-LDS rows), VMC_KV_Q8_0, VMC_KV_Q4_0 (dequantized to fp16 as
  * vmc_paged_attention_decode does); q_dtype VMC_DTYPE_F16 / VMC_DTYPE_BF16,
  * rounded to the page type when they differ (q8_0 / q4_0: fp16).  Limits:
- * head_dim 128, block_size 16, pools 16-byte aligned.  No workspace.
+ * head_dim 128 with block_size 16 and pools 16-byte aligned for the tiled
+ * kernel; head_dim 64 and 256 run a one-wave-per-row kernel.  No workspace.
  */
 int vmc_flash_attention_prefill_v2(void* out, const void* query, const void* key_cache,
                                    const void* value_cache, int num_tokens, int num_heads,
@@ -245,7 +249,11 @@ int vmc_fused_qk_norm_rope_store(void* q_buf, void* k_buf, const void* v_buf,
  * limits as for vmc_paged_attention_decode.  half_dtype (VMC_DTYPE_F16 or
  * VMC_DTYPE_BF16) is the dtype of query, output and the stored norms, scales
  * and zeros (the reference dispatches on its compute dtype,
- * turboquant_kernels.cu:966; the per-32-group and fp8-key layouts take fp16).
+ * turboquant_kernels.cu:966; the per-32-group layout takes fp16).
+ * norm_correction 0 scales keys by the stored norm alone (the reference's
+ * 4/4 decode without it, turboquant_kernels.cu:889-912).  At head_dim 128,
+ * shapes past 8 KV heads or 16 query heads per KV head, and fp8 keys with
+ * bf16 halves, run on a one-wave-per-row kernel.
  */
 size_t vmc_turboquant_decode_workspace_size(int batch_size, int num_heads, int num_kv_heads,
                                             int head_dim, int64_t max_num_blocks_per_req,
@@ -285,10 +293,14 @@ int vmc_turboquant_decode_attention_noalloc(void* output, const void* query, con
  * t is token_positions[t] of sequence token_to_seq[t] and attends positions
  * 0 .. token_positions[t] through its block_tables row (this step's tokens
  * already stored).  No counterpart in the reference, whose TurboQuant prefill
- * attends only the step's local K/V (attention_backend.cpp:153-196); the
- * arithmetic is that of vmc_turboquant_decode_attention with one row per
- * token (workspace: vmc_turboquant_decode_workspace_size(num_tokens, ...),
- * none when max_num_kv_splits == 1).
+ * attends only the step's local K/V (attention_backend.cpp:153-196).
+ * Steps of 16 tokens or more over reference-layout slots (codebook or fp8
+ * keys; head_dim 128, block_size 16, kv_cache 4-byte aligned) run the tiled
+ * MFMA prefill: each 64-key tile of a sequence is read once per block of
+ * query rows, no workspace.  Other steps run the arithmetic of
+ * vmc_turboquant_decode_attention with one row per token (workspace:
+ * vmc_turboquant_decode_workspace_size(num_tokens, ...), none when
+ * max_num_kv_splits == 1).
  */
 int vmc_turboquant_prefill_attention(void* output, const void* query, const void* kv_cache,
                                      const int32_t* block_tables, const int32_t* token_to_seq,
@@ -309,7 +321,8 @@ int vmc_turboquant_prefill_attention(void* output, const void* query, const void
  * Optional fused quantize-on-append: when key_cache != NULL the same launch
  * writes every K/V row into the paged cache (kv_format/layout as in
  * vmc_reshape_and_cache, slot_mapping int64 [num_tokens]).
- * Limits: head_dim == 128, num_heads % num_kv_heads == 0.
+ * Limits: head_dim 64, 128 or 256 (64 and 256: a one-wave-per-row kernel,
+ * then the append by vmc_reshape_and_cache), num_heads % num_kv_heads == 0.
  */
 int vmc_flash_attention_prefill(void* output, const void* query, const void* key,
                                 const void* value, int num_tokens, int num_heads,
