@@ -311,6 +311,25 @@ static void test_errors() {
         threw = true;
     }
     CHECK(threw);
+    threw = false;
+    try {
+        convert_fp8(nullptr, nullptr, 1.0, 16, "fp8_e4m3", ScalarType::FLOAT16);
+    } catch (const std::runtime_error& e) {
+        threw = std::string(e.what()).find("convert_fp8") != std::string::npos;
+    }
+    CHECK(threw);
+    convert_fp8(nullptr, nullptr, 1.0, 0, "fp8_e4m3", ScalarType::FLOAT16);  // nothing to convert
+    threw = false;
+    try {
+        reshape_and_cache_flash(nullptr, nullptr, nullptr, nullptr, nullptr, 0, 8, 128, 16, 0, "fp8_e5m2",
+                                nullptr, nullptr, ScalarType::FLOAT16);
+    } catch (const std::runtime_error& e) {
+        threw = std::string(e.what()).find("kv_cache_dtype") != std::string::npos;
+    }
+    CHECK(threw);
+    TQWorkspace tw;
+    tw.ensure_store(64, 128, 0);  // no scratch: allocates nothing
+    CHECK(tw.decode_workspace == nullptr);
     CHECK(vmc_layout_of("hnd") == VMC_LAYOUT_HND);
     CHECK(vmc_kv_format_of("auto", ScalarType::BFLOAT16) == VMC_KV_BF16);
     CHECK(vmc_kv_format_of("q4_0", ScalarType::FLOAT16) == VMC_KV_Q4_0);

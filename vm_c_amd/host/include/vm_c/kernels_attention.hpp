@@ -48,6 +48,21 @@ void reshape_and_cache(const void* key, const void* value, void* key_cache, void
                        const void* v_scale, ScalarType dtype, hipStream_t stream = nullptr,
                        const std::string& layout = "nhd");
 
+// kernels_cache.h:29-39: the reference's flash-layout entry is the same append
+// (cache_kernels.cu:146-157 forwards to reshape_and_cache); so is this one.
+void reshape_and_cache_flash(const void* key, const void* value, void* key_cache, void* value_cache,
+                             const int64_t* slot_mapping, int num_tokens, int num_kv_heads,
+                             int head_dim, int64_t block_size, int64_t cache_stride,
+                             const std::string& kv_cache_dtype, const void* k_scale,
+                             const void* v_scale, ScalarType dtype, hipStream_t stream = nullptr,
+                             const std::string& layout = "nhd");
+
+// kernels_cache.h:41-46 (cache_kernels.cu:160-200): fp8 KV caches are not
+// carried (reshape_and_cache rejects the fp8 dtype strings too); throws
+// std::runtime_error naming the call.
+void convert_fp8(void* dst_cache, const void* src_cache, double scale, int64_t num_elements,
+                 const std::string& kv_cache_dtype, ScalarType dtype, hipStream_t stream = nullptr);
+
 // Prefill over the paged cache (cached prefix + this step's appended tokens):
 // token t attends positions 0 .. token_positions[t] of sequence
 // token_to_seq[t] (attention_kernels.cu:416-436).  seq_lens and num_reqs are

@@ -87,6 +87,14 @@ struct TQWorkspace {
     void ensure_decode(int batch_size, int num_heads, int num_kv_heads, int head_dim,
                        int64_t max_num_blocks_per_req, int64_t block_size,
                        int max_num_kv_splits, int gpu_device);
+    // turboquant_kernels.cu:704-741 grows four fp32 scratch buffers for its
+    // multi-launch store; the fused HIP store needs none, so this only keeps
+    // the reference's call sites compiling
+    void ensure_store(int nh, int head_dim, int gpu_device) {
+        (void)nh;
+        (void)head_dim;
+        (void)gpu_device;
+    }
     void free_buf();
 };
 

@@ -232,6 +232,26 @@ void reshape_and_cache(const void* key, const void* value, void* key_cache, void
                                    vmc_layout_of(layout), stream));
 }
 
+void reshape_and_cache_flash(const void* key, const void* value, void* key_cache, void* value_cache,
+                             const int64_t* slot_mapping, int num_tokens, int num_kv_heads, int head_dim,
+                             int64_t block_size, int64_t cache_stride, const std::string& kv_cache_dtype,
+                             const void* k_scale, const void* v_scale, ScalarType dtype, hipStream_t stream,
+                             const std::string& layout) {
+    reshape_and_cache(key, value, key_cache, value_cache, slot_mapping, num_tokens, num_kv_heads, head_dim,
+                      block_size, cache_stride, kv_cache_dtype, k_scale, v_scale, dtype, stream, layout);
+}
+
+void convert_fp8(void* dst_cache, const void* src_cache, double scale, int64_t num_elements,
+                 const std::string& kv_cache_dtype, ScalarType dtype, hipStream_t stream) {
+    (void)dst_cache;
+    (void)src_cache;
+    (void)scale;
+    (void)dtype;
+    (void)stream;
+    if (num_elements <= 0) return;  // as the reference: nothing to convert
+    throw std::runtime_error("convert_fp8: fp8 KV caches (" + kv_cache_dtype + ") are not supported");
+}
+
 void paged_attention_prefill(void* out, const void* query, const void* key_cache,
                              const void* value_cache, int num_tokens, int num_heads,
                              int num_kv_heads, int head_dim, float scale, int64_t block_size,
