@@ -243,3 +243,48 @@ def test_tq_decode_bf16(dev, method, case, max_splits):
     ref = (ref.astype(np.uint32) << 16).view(np.float32)
     ok, err = close_report(got, ref, ATOL, RTOL)
     assert ok, f"vs reference restatement: max err {err}"
+
+
+@pytest.mark.parametrize("heads", [(8, 8), (16, 8), (32, 8), (64, 8), (12, 4)])
+def test_tq_decode_workspace_contents_do_not_matter(dev, heads):
+    """The split decode keeps no state in the workspace between calls: every
+    partial row the merge reads is written by the same call, so random bytes
+    in the workspace, or the leftovers of a call of another shape, give the
+    same output bit for bit as a zero-filled one.  G = 1, 2, 3, 4 and 8 query
+    heads per KV head; the lengths cut sequences into 2 to ~60 pieces and
+    include an empty one (whose rows must come out zero)."""
+    import torch
+    from vm_c_amd import capi
+    Hq, Hkv = heads
+    cfg = capi.tq_config(128, "turboquant_3bit_nc")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(Hq)
+    ws = None
+    for i, lens in enumerate(([32768, 1000, 0, 5000, 17], [3000, 64, 12000])):
+        w = make_workload(seq_lens=lens, Hq=Hq, Hkv=Hkv, seed=40 + i + Hq)
+        cache = torch.zeros(w.num_blocks * BS * Hkv * cfg.slot_size_aligned, dtype=torch.uint8, device=dev)
+        capi.turboquant_store(torch.from_numpy(w.K).to(dev), torch.from_numpy(w.V).to(dev), cache,
+                              torch.from_numpy(w.slots).to(dev), BS, cfg)
+        q = torch.from_numpy(w.Q).to(dev)
+        bt, sl = torch.from_numpy(w.bt).to(dev), torch.from_numpy(w.seq_lens).to(dev)
+        need = capi.turboquant_decode_workspace_size(len(lens), Hq, Hkv, 128, w.bt.shape[1], BS)
+        print(f"heads {Hq}/{Hkv} lens {lens} workspace {need} B", flush=True)
+        if ws is None:  # the second shape reuses the first call's workspace as it was left
+            ws = torch.randint(0, 256, (need,), dtype=torch.uint8, device=dev, generator=gen)
+        assert ws.numel() >= need
+        got = torch.full_like(q, float("nan"))
+        capi.turboquant_decode_attention(got, q, cache, bt, sl, Hkv, float(w.scale), cfg, BS, workspace=ws)
+        ref = torch.full_like(q, float("nan"))
+        capi.turboquant_decode_attention(ref, q, cache, bt, sl, Hkv, float(w.scale), cfg, BS,
+                                         workspace=torch.zeros(need, dtype=torch.uint8, device=dev))
+        again = torch.full_like(q, float("nan"))
+        capi.turboquant_decode_attention(again, q, cache, bt, sl, Hkv, float(w.scale), cfg, BS, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), f"call {i}: output depends on workspace bytes"
+        assert torch.equal(again.view(torch.int16), ref.view(torch.int16)), f"call {i}: second call differs"
+        c, _ = O.tq_tables(128, 3)
+        ex = O.tq_decode_exact(bits16(w.Q), cache.cpu().numpy(), w.bt, w.seq_lens, Hkv, w.scale, BS,
+                               O.tq_layout("turboquant_3bit_nc"), c)
+        ok, err = close_report(got.float().cpu().numpy(), ex, ATOL, RTOL)
+        assert ok, f"call {i}: max err {err}"
+        assert (got.float().cpu().numpy()[np.asarray(lens) == 0] == 0).all()
