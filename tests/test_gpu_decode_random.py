@@ -6,7 +6,8 @@ TurboQuant slots through vmc_turboquant_decode_attention.  Each case draws
 holes, a head shape from (8, 8), (12, 4), (16, 4), (24, 8), (64, 8), (32, 2)
 and (64, 2) (G = 1, 3, 4, 3, 8, 16, 32: the tuned kernels and the
 one-wave-per-row kernel past 16 query heads per KV head), and a split mode
-(one pass per sequence, at most 8 pieces per sequence, no cap).
+(one pass per sequence; pages split evenly with at most 8 x batch pieces;
+no cap).
 Tolerance |got - ref| <= 2e-3 + 1e-2 |ref|.
 """
 import numpy as np
