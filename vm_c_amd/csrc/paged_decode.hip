@@ -95,30 +95,6 @@ struct Geo {
     static constexpr int nbuf = dma ? pf + 2 : pf;
 };
 
-// Codes 2e and 2e+1 of an 8-code word of the per-32-group variant -> packed
-// fp16 code * d + m (4-bit, one fused rounding) or (code - 4) * d (3-bit,
-// exact operand times d, one rounding): the two fields go to the 16-bit
-// halves under 0x64 (fp16 1024 + code), then a packed subtract and a packed
-// FMA / multiply.
-template <int FMT>
-__device__ __forceinline__ uint32_t g32_pair_f16(uint32_t cw, int e, f16x2 d2, f16x2 m2) {
-    uint32_t z;
-    if constexpr (FMT == FMT_G4) {
-        const uint32_t b = (cw >> (8 * e)) & 0xffu;  // code 2e low nibble, 2e+1 high
-        z = ((b | (b << 12)) & 0x000f000fu) | 0x64006400u;
-    } else {
-        const uint32_t t = (cw >> (6 * e)) & 0x3fu;  // code 2e bits 0-2, 2e+1 bits 3-5
-        z = ((t | (t << 13)) & 0x00070007u) | 0x64006400u;
-    }
-    const f16x2 f = __builtin_bit_cast(f16x2, z);
-    if constexpr (FMT == FMT_G4) {
-        const f16x2 c = f - f16x2{(_Float16)1024.0f, (_Float16)1024.0f};
-        return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c, d2, m2));
-    } else {
-        const f16x2 c = f - f16x2{(_Float16)1028.0f, (_Float16)1028.0f};
-        return __builtin_bit_cast(uint32_t, c * d2);
-    }
-}
 // per-32-group variant: the codes of values 8j .. 8j+7 of the 32-value
 // block at blk (LDS, even address), value v of the 8 at bits 4v (4-bit:
 // byte i of the 16 holds values i and i + 16) or 3v (3-bit: 8 codes per 3
@@ -144,6 +120,10 @@ __device__ __forceinline__ uint32_t g32_codes8(const uint8_t* blk, int j) {
         return (w >> (8 * (o & 1))) & 0xffffffu;
     }
 }
+// two exact fp16 values times d, one rounding each (v_pk_mul_f16)
+__device__ __forceinline__ uint32_t g32_times(uint32_t c2, f16x2 d2) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, c2) * d2);
+}
 template <int FMT>
 __device__ __forceinline__ float g32_code(uint32_t cw, int v) {
     return FMT == FMT_G4 ? (float)((cw >> (4 * v)) & 0xfu) : (float)((cw >> (3 * v)) & 7u);
@@ -165,7 +145,9 @@ struct alignas(16) DecodeLds {
     // staged page pairs (PAIRS): two pairs of buffers, the one being read
     // and the one being filled
     uint8_t ring[GE::staged ? (PAIRS ? 4 : GE::nbuf) * GE::kBuf : 16];
-    u32x2 lut4[FMT == FMT_TQ && KB == 3 ? 4096 : 1];  // 3-bit keys: four fp16 centroids per 12 bits
+    // 3-bit codes, 12 bits -> four packed fp16 values: TurboQuant key
+    // centroids, or the per-32-group variant's exact code - 4
+    u32x2 lut4[(FMT == FMT_TQ && KB == 3) || FMT == FMT_G3 ? 4096 : 1];
     uint32_t lut[FMT == FMT_TQ ? 256 : 1];              // key code pair -> two fp16 centroids
     float wscr[GE::waves][80];                          // per-wave exchange
     int32_t bt[GE::chunk];                              // block of each page of the chunk
@@ -268,6 +250,17 @@ paged_decode_kernel(DecodeParams p) {
         if constexpr (KB == 3) {
             __syncthreads();
             for (int e = tid; e < 4096; e += blockDim.x) lut4[e] = u32x2{lut[e & 63], lut[e >> 6]};
+        }
+    }
+    if constexpr (FMT == FMT_G3) {
+        for (int e = tid; e < 4096; e += blockDim.x) {
+            uint32_t w[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float lo = (float)((int)((e >> (6 * h)) & 7) - 4), hi = (float)((int)((e >> (6 * h + 3)) & 7) - 4);
+                w[h] = (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
+            }
+            lut4[e] = u32x2{w[0], w[1]};
         }
     }
 
@@ -948,12 +941,13 @@ paged_decode_kernel(DecodeParams p) {
                 const uint32_t g24[4] = {c0 & 0xffffffu, (c0 >> 24) | ((c1 & 0xffffu) << 8),
                                          (c1 >> 16) | ((c2 & 0xffu) << 16), c2 >> 8};
                 const f16x2 d2 = __builtin_bit_cast(f16x2, d16 * 0x10001u);
-                const f16x2 m2 = {};
+                // four codes per table entry, exact (code - 4) in fp16, then
+                // one packed multiply by d: fp16((code - 4) * d)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    u32x4 kw;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) kw[e] = g32_pair_f16<FMT>(g24[j], e, d2, m2);
+                    const u32x2 lo = lut4[g24[j] & 0xfffu], hi = lut4[g24[j] >> 12];
+                    const u32x4 kw = {g32_times(lo[0], d2), g32_times(lo[1], d2), g32_times(hi[0], d2),
+                                      g32_times(hi[1], d2)};
                     a[j] = __builtin_bit_cast(AT, kw);
                 }
             }
@@ -981,10 +975,12 @@ paged_decode_kernel(DecodeParams p) {
                 } else {
                     const uint32_t dv16 = lds16(vb);
                     const f16x2 dv2 = __builtin_bit_cast(f16x2, dv16 | (dv16 << 16));
-                    const f16x2 mv2 = {};
                     const uint32_t cw = g32_codes8<FMT>(vb, r16 & 3);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) vw[i2][e] = ok ? g32_pair_f16<FMT>(cw, e, dv2, mv2) : 0u;
+                    const u32x2 lo = lut4[cw & 0xfffu], hi = lut4[cw >> 12];
+                    vw[i2][0] = ok ? g32_times(lo[0], dv2) : 0u;
+                    vw[i2][1] = ok ? g32_times(lo[1], dv2) : 0u;
+                    vw[i2][2] = ok ? g32_times(hi[0], dv2) : 0u;
+                    vw[i2][3] = ok ? g32_times(hi[1], dv2) : 0u;
                 }
             }
         } else {
