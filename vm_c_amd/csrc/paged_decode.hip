@@ -888,7 +888,6 @@ paged_decode_kernel(DecodeParams p) {
             // (even dim in the low nibble), code * scale + zero
 #pragma unroll
             for (int i2 = 0; i2 < 4; ++i2) {
-                const bool ok = 4 * grp + i2 < nv;
                 const uint8_t* vb = vpage + v_off[i2];
                 const float sc = f16_bits_to_f32((uint16_t)lds16(vb + 64));
                 const float zr = f16_bits_to_f32((uint16_t)lds16(vb + 66));
@@ -897,8 +896,7 @@ paged_decode_kernel(DecodeParams p) {
                 for (int e = 0; e < 4; ++e) {
                     const float x0 = __builtin_fmaf((float)((cw >> (8 * e)) & 0xfu), sc, zr);
                     const float x1 = __builtin_fmaf((float)((cw >> (8 * e + 4)) & 0xfu), sc, zr);
-                    vw[i2][e] = (uint32_t)f32_to_f16_bits(ok ? x0 : 0.0f) |
-                                ((uint32_t)f32_to_f16_bits(ok ? x1 : 0.0f) << 16);
+                    vw[i2][e] = (uint32_t)f32_to_f16_bits(x0) | ((uint32_t)f32_to_f16_bits(x1) << 16);
                 }
             }
         } else if constexpr (FMT == FMT_G4 || FMT == FMT_G3) {
@@ -954,7 +952,6 @@ paged_decode_kernel(DecodeParams p) {
             // V of tokens 4*grp + i, dims 8*r16 .. +7: block r16 / 4, values 8 (r16 % 4) ..
 #pragma unroll
             for (int i2 = 0; i2 < 4; ++i2) {
-                const bool ok = 4 * grp + i2 < nv;
                 const uint8_t* vb = vpage + v_off[i2] + BE * (r16 >> 2);
                 if constexpr (FMT == FMT_G4) {
                     // 20-byte block, 4-byte aligned: d | m, then the 8 code
@@ -970,17 +967,17 @@ paged_decode_kernel(DecodeParams p) {
                         const uint32_t sp = __builtin_amdgcn_perm(0u, w, (e & 1) ? 0x0c030c02u : 0x0c010c00u);
                         const uint32_t z = ((sp >> (l >= 2 ? 4 : 0)) & 0x000f000fu) | 0x64006400u;
                         const f16x2 c = __builtin_bit_cast(f16x2, z) - f16x2{(_Float16)1024.0f, (_Float16)1024.0f};
-                        vw[i2][e] = ok ? __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c, dv2, mv2)) : 0u;
+                        vw[i2][e] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c, dv2, mv2));
                     }
                 } else {
                     const uint32_t dv16 = lds16(vb);
                     const f16x2 dv2 = __builtin_bit_cast(f16x2, dv16 | (dv16 << 16));
                     const uint32_t cw = g32_codes8<FMT>(vb, r16 & 3);
                     const u32x2 lo = lut4[cw & 0xfffu], hi = lut4[cw >> 12];
-                    vw[i2][0] = ok ? g32_times(lo[0], dv2) : 0u;
-                    vw[i2][1] = ok ? g32_times(lo[1], dv2) : 0u;
-                    vw[i2][2] = ok ? g32_times(hi[0], dv2) : 0u;
-                    vw[i2][3] = ok ? g32_times(hi[1], dv2) : 0u;
+                    vw[i2][0] = g32_times(lo[0], dv2);
+                    vw[i2][1] = g32_times(lo[1], dv2);
+                    vw[i2][2] = g32_times(hi[0], dv2);
+                    vw[i2][3] = g32_times(hi[1], dv2);
                 }
             }
         } else {
@@ -1019,8 +1016,6 @@ paged_decode_kernel(DecodeParams p) {
             }
 #pragma unroll
             for (int i2 = 0; i2 < 4; ++i2) {
-                const int tok = 4 * grp + i2;
-                const bool ok = tok < nv;
                 const uint8_t* vb = vpage + v_off[i2] + BE * (r16 >> 2);
                 const uint32_t dv16 = lds16(vb);
                 const f16x2 dv2 = __builtin_bit_cast(f16x2, dv16 | (dv16 << 16));
@@ -1034,8 +1029,16 @@ paged_decode_kernel(DecodeParams p) {
                         const int jj = q0 + 2 * e;
                         x = q4_pair_f16(lds16(vb + 2 + (jj & 15)), jj < 16 ? 0 : 4, dv2);
                     }
-                    vw[i2][e] = ok ? x : 0u;
+                    vw[i2][e] = x;
                 }
+            }
+        }
+        if (nv < kBs) {  // rows past the page's valid tokens may hold anything
+#pragma unroll
+            for (int i2 = 0; i2 < 4; ++i2) {
+                const bool ok = 4 * grp + i2 < nv;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) vw[i2][e] = ok ? vw[i2][e] : 0u;
             }
         }
     };
