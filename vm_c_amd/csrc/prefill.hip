@@ -115,12 +115,10 @@ __device__ __forceinline__ V8 as_v8(u32x4 w) {
 }
 
 // One 16-byte-per-lane load-to-LDS transfer: lane L's 16 bytes from src land
-// at dst + 16 L.  Issued from asm so the compiler does not track it: it
+// at LDS address m0 + 16 L.  Issued from asm so the compiler does not track it: it
 // would otherwise make every later LDS read wait for all transfers in
 // flight (it cannot tell the slots apart); the kernel waits for them itself.
-__device__ __forceinline__ void dma16(const void* src, const void* dst) {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
-        (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)dst);
+__device__ __forceinline__ void dma16m(const void* src, uint32_t m0) {
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
 }
 
@@ -315,22 +313,42 @@ prefill_kernel(PrefillParams p) {
         const int r = k & (kBsP - 1);
         return p.hnd ? (int64_t)(g * kBsP + r) * p.E : (int64_t)(r * p.Hkv + g) * p.E;
     };
+    // local K/V: this lane's row of a tile starting at key k0 is k0 + ld_row
+    // (+ 32 in the second round); the LDS rows of this wave in slot 0 (the
+    // other slots and the V half at fixed offsets)
+    const uint8_t* const kg_row = kg + (int64_t)ld_row * row_stride;
+    const uint8_t* const vg_row = vg + (int64_t)ld_row * row_stride;
+    const uint32_t lds_w = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)&lds.tile[0][0][1024 * w]);
+    constexpr uint32_t kSlotB = 2 * BN * 256, kPartB = BN * 256;
     auto load_tile = [&](int t, auto slot_c) __attribute__((always_inline)) {
         constexpr int SL = decltype(slot_c)::value;
         const int k0 = kv_lo + t * BN;
+        if constexpr (SRC == SRC_LOCAL) {
+            if (k0 + BN <= kv_end) {  // uniform: every row of the tile in range
+                const int64_t toff = (int64_t)k0 * row_stride;
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const int64_t off = toff + (int64_t)(32 * i) * row_stride;
+                    dma16m(kg_row + off, lds_w + SL * kSlotB + 8192u * i);
+                    dma16m(vg_row + off, lds_w + SL * kSlotB + kPartB + 8192u * i);
+                }
+                return;
+            }
+        }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             // rows past the range re-read the last row (masked later)
             const int kk = min(k0 + 32 * i + ld_row, kv_end - 1);
             if constexpr (SRC == SRC_LOCAL) {
                 const int64_t off = (int64_t)kk * row_stride;
-                dma16(kg + off, &lds.tile[SL][0][1024 * (8 * i + w)]);
-                dma16(vg + off, &lds.tile[SL][1][1024 * (8 * i + w)]);
+                dma16m(kg + off, lds_w + SL * kSlotB + 8192u * i);
+                dma16m(vg + off, lds_w + SL * kSlotB + kPartB + 8192u * i);
             } else {
                 const int64_t off = (int64_t)page_at(min(k0 + 32 * i + 4 * wu, kv_end - 1)) * p.page_bytes +
                                     row_in_page(kk) + ld_col;
-                dma16(p.kp + off, &lds.tile[SL][0][1024 * (8 * i + w)]);
-                dma16(p.vp + off, &lds.tile[SL][1][1024 * (8 * i + w)]);
+                dma16m(p.kp + off, lds_w + SL * kSlotB + 8192u * i);
+                dma16m(p.vp + off, lds_w + SL * kSlotB + kPartB + 8192u * i);
             }
         }
     };
