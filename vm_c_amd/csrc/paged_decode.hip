@@ -157,14 +157,14 @@ struct alignas(16) DecodeLds {
     int n_seg;
 };
 
-// HALF (at most 8 query heads per KV head; TurboQuant and the staged
-// formats): the 16 columns of the S tile hold the heads for the step's first
-// page (columns 0-7) and for its second page (columns 8-15): K of both pages
-// runs against a block-diagonal Q^T, so every lane's scores are real and one
-// softmax covers two pages.  The PV product keeps the page of each row apart
-// (rows 0-7 first page, 8-15 second) and the halves are added when the piece
-// ends.  The per-32-group formats then stage and process two pages per
-// workgroup barrier.
+// HALF (the per-32-group formats with at most 8 query heads per KV head;
+// TurboQuant slots with G <= 8 run tq_decode.hip's kernel instead): the 16
+// columns of the S tile hold the heads for the step's first page (columns
+// 0-7) and for its second page (columns 8-15): K of both pages runs against a
+// block-diagonal Q^T, so every lane's scores are real and one softmax covers
+// two pages.  The PV product keeps the page of each row apart (rows 0-7 first
+// page, 8-15 second) and the halves are added when the piece ends.  Two pages
+// are staged and processed per workgroup barrier.
 template <int FMT, int KB, int VB, bool MBF16, bool HALF>
 __global__ void __launch_bounds__(512)
 paged_decode_kernel(DecodeParams p) {
@@ -175,7 +175,8 @@ paged_decode_kernel(DecodeParams p) {
     constexpr bool kTqBf16 = FMT == FMT_TQ && MBF16;
     using AT = typename std::conditional<MBF16 && FMT != FMT_TQ, bf16x8, f16x8>::type;
     using PT = typename std::conditional<MBF16 && FMT != FMT_TQ, s16x4, f16x4>::type;
-    constexpr bool kPairs = HALF && FMT >= FMT_Q8_0 && FMT != FMT_TQ;  // staged: two pages per step
+    static_assert(!HALF || FMT == FMT_G4 || FMT == FMT_G3, "page pairs: the per-32-group formats");
+    constexpr bool kPairs = HALF;  // staged: two pages per step
     __shared__ DecodeLds<FMT, KB, VB, kPairs> lds;
     uint8_t* const smem = lds.ring;
     WGPlan& plan = lds.plan;
@@ -664,13 +665,11 @@ paged_decode_kernel(DecodeParams p) {
             for (int i2 = 0; i2 < 4; ++i2) {
                 const uint8_t* cr = pg[pp] + vc_al[i2];
                 cw[i2] = lds16(cr) | (lds16(cr + 2) << 16);
-                if constexpr (!HALF) {
-                    const uint8_t* ve = pg[pp] + v_off[i2] + GE::key_packed + GE::val_data;
-                    vsc[pp][i2] = (uint16_t)lds16(ve);
-                    vzr[pp][i2] = (uint16_t)lds16(ve + 2);
-                }
+                const uint8_t* ve = pg[pp] + v_off[i2] + GE::key_packed + GE::val_data;
+                vsc[pp][i2] = (uint16_t)lds16(ve);
+                vzr[pp][i2] = (uint16_t)lds16(ve + 2);
             }
-            if constexpr (kMasked && !HALF) {  // tokens past the end may hold anything
+            if constexpr (kMasked) {  // tokens past the end may hold anything
 #pragma unroll
                 for (int i2 = 0; i2 < 4; ++i2) {
                     const bool ok = 4 * grp + i2 < nvp[pp];
@@ -709,85 +708,6 @@ paged_decode_kernel(DecodeParams p) {
                 }
             }
         }
-        if constexpr (HALF) {
-        // ---- S^T: column c < 8 is head c on the first page, c >= 8 head c - 8
-        // on the second (block-diagonal Q^T, one accumulator)
-        f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) sacc = mfma16x16x32(a[0][j], qb[j], sacc);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) sacc = mfma16x16x32(a[1][j], qb[4 + j], sacc);
-        // this lane's page: scale and zero of its tokens 4*grp + i, valid count
-        const uint8_t* vpg = smem + BUF0 * GE::kBuf + (r16 >= 8 ? GE::kBuf : 0);
-        uint16_t hs[4], hz[4];
-#pragma unroll
-        for (int i2 = 0; i2 < 4; ++i2) {
-            const uint8_t* ve = vpg + v_off[i2] + GE::key_packed + GE::val_data;
-            hs[i2] = (uint16_t)lds16(ve);
-            hz[i2] = (uint16_t)lds16(ve + 2);
-        }
-        wscr[diag_slot] = rowf[0];
-        wscr[32 + diag_slot] = rowf[1];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const f32x4 rf = *reinterpret_cast<const f32x4*>(wscr + (r16 >= 8 ? 32 : 0) + 4 * grp);
-        __builtin_amdgcn_wave_barrier();
-        float sv[4];
-#pragma unroll
-        for (int i2 = 0; i2 < 4; ++i2) sv[i2] = sacc[i2] * rf[i2];
-        if constexpr (kMasked) {
-            const int nvl = r16 >= 8 ? nv1 : nv0;
-#pragma unroll
-            for (int i2 = 0; i2 < 4; ++i2) {
-                const bool ok = 4 * grp + i2 < nvl;
-                sv[i2] = ok ? sv[i2] : kNegInf;
-                hs[i2] = ok ? hs[i2] : (uint16_t)0;
-                hz[i2] = ok ? hz[i2] : (uint16_t)0;
-            }
-        }
-        // Lazy reference max (see below); a head's max spans columns c, c ^ 8
-        const float mloc = vmax(vmax(sv[0], sv[1]), vmax(sv[2], sv[3]));
-        if (__ballot(mloc > m_thr)) {  // wave-uniform
-            float mx = vmax_over_groups(mloc);
-            mx = vmax(mx, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, mx), 0x128, 0xf, 0xf, false)));
-            const bool upd = mx > m_thr;  // the same in every lane of the head
-            const float m_new = upd ? mx : m_run;
-            const float alpha = upd ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;  // 0 when m_run = -inf
-            l_part *= alpha;
-            z_part *= alpha;
-            // O row m belongs to the head of column m
-            const f32x4 al = gather4_from_row0(alpha, wscr + 64, r16, grp);
-#pragma unroll
-            for (int i2 = 0; i2 < 4; ++i2)
-#pragma unroll
-                for (int c = 0; c < 8; ++c) oacc[c][i2] *= al[i2];
-            m_run = m_new;
-            m_thr = m_run + 8.0f;
-        }
-        const float m_use = m_run == kNegInf ? 0.0f : m_run;
-        float psum = 0.0f, zsum = 0.0f;
-        f16x4 pw;
-#pragma unroll
-        for (int i2 = 0; i2 < 4; ++i2) {
-            const float pv = __builtin_amdgcn_exp2f(sv[i2] - m_use);
-            psum += pv;
-            zsum = __builtin_fmaf(pv, half_to_f32<kTqBf16>(hz[i2]), zsum);
-            pw[i2] = (_Float16)__builtin_fmaf(pv, half_to_f32<kTqBf16>(hs[i2]), 0.0f);
-        }
-        l_part += psum;
-        z_part += zsum;
-        // ---- O += P . V: rows 0-7 take k = 8*grp + i (first page, token
-        // 4*grp + i), rows 8-15 k = 8*grp + 4 + i (second page)
-        const u32x2 pw2 = __builtin_bit_cast(u32x2, pw);
-        const uint32_t lo_m = r16 < 8 ? ~0u : 0u;
-        const AT pa = __builtin_bit_cast(AT, u32x4{pw2[0] & lo_m, pw2[1] & lo_m, pw2[0] & ~lo_m, pw2[1] & ~lo_m});
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const AT vb = __builtin_bit_cast(AT, u32x4{bop[0][c][0], bop[0][c][1], bop[1][c][0], bop[1][c][1]});
-            oacc[c] = mfma16x16x32(pa, vb, oacc[c]);
-        }
-        } else {
         // ---- S^T = K . Q^T per page, times the per-token factor
         f32x4 sacc[2];
 #pragma unroll
@@ -859,7 +779,6 @@ paged_decode_kernel(DecodeParams p) {
         for (int c = 0; c < 8; ++c) {
             const AT vb = __builtin_bit_cast(AT, u32x4{bop[0][c][0], bop[0][c][1], bop[1][c][0], bop[1][c][1]});
             oacc[c] = mfma16x16x32(pa, vb, oacc[c]);
-        }
         }
         }
     };
