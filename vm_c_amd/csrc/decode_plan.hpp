@@ -380,5 +380,8 @@ inline size_t workspace_bytes_for(int B, int Hq, int Hkv, int max_blocks, int ma
 // The pipelined TurboQuant decode (tq_decode.hip): reference slot layout,
 // at most 8 query heads per KV head; VMC_EINVAL for other shapes.
 int launch_tq_decode_any(DecodeParams& prm, int key_bits, int value_bits, bool bf16, hipStream_t stream);
+// The per-32-group variant (fp16, 3- or 4-bit codes) on the same kernel;
+// VMC_EINVAL for shapes it does not take.
+int launch_g32_decode(DecodeParams& prm, int bits, hipStream_t stream);
 
 }  // namespace vmc

@@ -1601,7 +1601,11 @@ int tq_decode_rows(void* output, const void* query, const void* kv_cache, const 
         const G32Signs sg = g32_signs(cfg->sign_seed);
         for (int i = 0; i < 4; ++i) prm.sgn[i] = sg.w[i];
         hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-        if (prm.G <= 8)  // page pairs
+        if (prm.G <= 8) {  // the pipelined kernel of tq_decode.hip, else page pairs
+            const int rc = launch_g32_decode(prm, cfg->key_quant_bits, s);
+            if (rc != VMC_EINVAL) return rc;
+        }
+        if (prm.G <= 8)
             return cfg->key_quant_bits == 4 ? launch_decode<FMT_G4, 0, 0, false, true>(prm, s)
                                             : launch_decode<FMT_G3, 0, 0, false, true>(prm, s);
         return cfg->key_quant_bits == 4 ? launch_decode<FMT_G4, 0, 0, false>(prm, s)

@@ -36,11 +36,16 @@
 namespace vmc {
 namespace {
 
-// Compile-time geometry of one slot layout (turboquant_kernels.cu:29-45).
-template <int KB, int VB>
+// Compile-time geometry of one slot layout: the reference's
+// (turboquant_kernels.cu:29-45), or the per-32-group variant (G32: K part
+// then V part, four blocks of be bytes each -- fp16 d and 12 code bytes at
+// 3 bits, fp16 d, m and 16 code bytes at 4 bits).
+template <int KB, int VB, bool G32 = false>
 struct TqGeo {
     static constexpr int mse = 16 * KB, kp = mse + 2, vd = 16 * VB;
-    static constexpr int slot = (kp + vd + 4 + 1) / 2 * 2;
+    static constexpr int be = KB == 3 ? 14 : 20;  // G32 block bytes
+    static constexpr int part = 4 * be;           // G32 K part bytes
+    static constexpr int slot = G32 ? 2 * part : (kp + vd + 4 + 1) / 2 * 2;
     // a head's run starts at most 14 bytes into its 16-byte window
     static constexpr int nch = (14 + slot + 15) / 16;
     static constexpr int nchp = nch | 1;  // odd: 16 rows -> 16 distinct bank groups
@@ -56,12 +61,13 @@ struct TqGeo {
     static_assert(nb * page < 60000, "a wave's ring offsets must fit the LDS instruction offset");
 };
 
-template <int KB, int VB>
+template <int KB, int VB, bool G32>
 struct alignas(16) TqLds {
-    using TG = TqGeo<KB, VB>;
+    using TG = TqGeo<KB, VB, G32>;
     // 3-bit keys: four fp16 centroids per 12 bits of codes (8-byte entries;
     // measured faster than the conflict-free 64-entry pair table, whose two
-    // lookups per 12 bits cost more index arithmetic than the conflicts cost)
+    // lookups per 12 bits cost more index arithmetic than the conflicts cost);
+    // G32: four exact fp16 (code - 4), keys and values
     u32x2 lut4[KB == 3 ? 4096 : 1];
     uint32_t lut[256];  // key code pair -> two fp16 centroids
     uint8_t ring[TG::waves][TG::nb][TG::page];
@@ -72,6 +78,22 @@ struct alignas(16) TqLds {
     WGPlan plan;
     int n_seg;
 };
+
+// per-32-group variant: two exact fp16 values times d (one packed multiply,
+// one rounding each)
+__device__ __forceinline__ uint32_t g32_mul(uint32_t c2, f16x2 d2) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, c2) * d2);
+}
+// 4-bit: two codes of the 16 code bytes (byte i = value i | value i + 16 << 4):
+// bytes 2 odd, 2 odd + 1 of w, low nibbles or high (hi), to packed fp16
+// code * d + m (fp16 1024 + code under 0x64, a packed subtract, one packed
+// FMA)
+__device__ __forceinline__ uint32_t g32_nib2(uint32_t w, int odd, bool hi, f16x2 d2, f16x2 m2) {
+    const uint32_t sp = __builtin_amdgcn_perm(0u, w, odd ? 0x0c030c02u : 0x0c010c00u);
+    const uint32_t z = ((sp >> (hi ? 4 : 0)) & 0x000f000fu) | 0x64006400u;
+    const f16x2 c = __builtin_bit_cast(f16x2, z) - f16x2{(_Float16)1024.0f, (_Float16)1024.0f};
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c, d2, m2));
+}
 
 // one 16-byte-per-lane load-to-LDS transfer, non-temporal: lane L's 16 bytes
 // from base + off land at LDS address m0 + 16 L.  Issued from asm, so the
@@ -106,12 +128,12 @@ struct TqHalves {
     uint32_t hsz[4][2];  // scale, zero of the lane's page's token 4*grp + i: two words from the 4-byte floor
 };
 
-template <int KB, int VB, bool BF>
+template <int KB, int VB, bool BF, bool G32>
 __global__ void __launch_bounds__(512) tq_decode_kernel(DecodeParams p) {
-    using TG = TqGeo<KB, VB>;
+    using TG = TqGeo<KB, VB, G32>;
     using AT = f16x8;
     using CODES = TqCodes<KB, VB>;
-    __shared__ TqLds<KB, VB> lds;
+    __shared__ TqLds<KB, VB, G32> lds;
     WGPlan& plan = lds.plan;
 
     const int tid = threadIdx.x;
@@ -163,11 +185,26 @@ __global__ void __launch_bounds__(512) tq_decode_kernel(DecodeParams p) {
         return;
     }
 
-    // ---- key centroid pair table
-    build_pair_lut<KB>(lds.lut, p.tab);
-    if constexpr (KB == 3) {
-        __syncthreads();
-        for (int e = tid; e < 4096; e += blockDim.x) lds.lut4[e] = u32x2{lds.lut[e & 63], lds.lut[e >> 6]};
+    // ---- key centroid pair table; G32 3-bit: the exact (code - 4) table
+    if constexpr (G32) {
+        if constexpr (KB == 3) {
+            for (int e = tid; e < 4096; e += blockDim.x) {
+                uint32_t w2[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const float lo = (float)((int)((e >> (6 * h)) & 7) - 4);
+                    const float hi = (float)((int)((e >> (6 * h + 3)) & 7) - 4);
+                    w2[h] = (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
+                }
+                lds.lut4[e] = u32x2{w2[0], w2[1]};
+            }
+        }
+    } else {
+        build_pair_lut<KB>(lds.lut, p.tab);
+        if constexpr (KB == 3) {
+            __syncthreads();
+            for (int e = tid; e < 4096; e += blockDim.x) lds.lut4[e] = u32x2{lds.lut[e & 63], lds.lut[e >> 6]};
+        }
     }
 
     // ---- Q operand: lane (r16, grp) holds dims 32 grp + 8 j + e of head qh
@@ -190,6 +227,11 @@ __global__ void __launch_bounds__(512) tq_decode_kernel(DecodeParams p) {
         } else {
 #pragma unroll
             for (int e = 0; e < 32; ++e) y[e] = 0.0f;
+        }
+        if constexpr (G32) {  // the variant's rotation: H (s q) / sqrt(d)
+            const uint32_t sb = p.sgn[grp];  // dims 32 grp .. + 31
+#pragma unroll
+            for (int e = 0; e < 32; ++e) y[e] = ((sb >> e) & 1u) ? -y[e] : y[e];
         }
         // Walsh-Hadamard: half-widths 1..16 inside the lane, 32 and 64 across
         // the lane groups (dim bit 32 = grp bit 0, dim bit 64 = grp bit 1)
@@ -234,6 +276,8 @@ __global__ void __launch_bounds__(512) tq_decode_kernel(DecodeParams p) {
     int cur_b = -1;
 
     // ---- finish a piece of sequence b: the rows, or the partial slot
+    // (TurboQuant: O chunk c in units of its code field's fp16 subnormal)
+    auto vscale = [](int c) { return G32 ? 1.0f : kVScale<FMT_TQ, VB>(c); };
     auto finalize = [&](int b) __attribute__((always_inline)) {
         const bool cut_before = b == __builtin_amdgcn_readfirstlane(plan.first_b) &&
                                 __builtin_amdgcn_readfirstlane(plan.first_cut);
@@ -251,6 +295,40 @@ __global__ void __launch_bounds__(512) tq_decode_kernel(DecodeParams p) {
         for (int c = 0; c < 8; ++c)
 #pragma unroll
             for (int i = 0; i < 4; ++i) oacc[c][i] += __shfl_xor(oacc[c][i], 32, 64);
+        if constexpr (G32) {
+            // O back from the rotated domain, s (H O_r) / sqrt(d) (linear: the
+            // partial rows of cut pieces too); oacc[c][i] = dim 8 r16 + c:
+            // half-widths 1..4 in the lane, 8..64 across r16
+#pragma unroll
+            for (int hw = 1; hw < 8; hw <<= 1)
+#pragma unroll
+                for (int c0 = 0; c0 < 8; c0 += 2 * hw)
+#pragma unroll
+                    for (int c = c0; c < c0 + hw; ++c)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const float x = oacc[c][i], y = oacc[c + hw][i];
+                            oacc[c][i] = x + y;
+                            oacc[c + hw][i] = x - y;
+                        }
+#pragma unroll
+            for (int m = 1; m < 16; m <<= 1)
+#pragma unroll
+                for (int c = 0; c < 8; ++c)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float o = __shfl_xor(oacc[c][i], m, 64);
+                        oacc[c][i] = (r16 & m) ? o - oacc[c][i] : oacc[c][i] + o;
+                    }
+            const uint32_t sb = (p.sgn[r16 >> 2] >> (8 * (r16 & 3))) & 0xffu;  // dims 8 r16 .. + 7
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float v = oacc[c][i] * p.tab.rot_c;
+                    oacc[c][i] = ((sb >> c) & 1u) ? -v : v;
+                }
+        }
         const f32x4 lh4 = gather4_from_row0(l_tot, wscr, r16, grp);
         const f32x4 zh4 = gather4_from_row0(z_tot, wscr + 16, r16, grp);
         const f32x4 mh4 = gather4_from_row0(m_run, wscr + 32, r16, grp);
@@ -265,8 +343,8 @@ __global__ void __launch_bounds__(512) tq_decode_kernel(DecodeParams p) {
                 uint32_t wd[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const float v0 = __builtin_fmaf(oacc[2 * e][i], kVScale<FMT_TQ, VB>(2 * e), zh) * inv;
-                    const float v1 = __builtin_fmaf(oacc[2 * e + 1][i], kVScale<FMT_TQ, VB>(2 * e + 1), zh) * inv;
+                    const float v0 = __builtin_fmaf(oacc[2 * e][i], vscale(2 * e), zh) * inv;
+                    const float v1 = __builtin_fmaf(oacc[2 * e + 1][i], vscale(2 * e + 1), zh) * inv;
                     wd[e] = (uint32_t)f32_to_half<BF>(v0) | ((uint32_t)f32_to_half<BF>(v1) << 16);
                 }
                 uint16_t* o = reinterpret_cast<uint16_t*>(p.out) + ((int64_t)b * p.Hq + hq) * kD + 8 * r16;
@@ -277,8 +355,8 @@ __global__ void __launch_bounds__(512) tq_decode_kernel(DecodeParams p) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
                     *reinterpret_cast<float2*>(od + 2 * e) =
-                        make_float2(__builtin_fmaf(oacc[2 * e][i], kVScale<FMT_TQ, VB>(2 * e), zh),
-                                    __builtin_fmaf(oacc[2 * e + 1][i], kVScale<FMT_TQ, VB>(2 * e + 1), zh));
+                        make_float2(__builtin_fmaf(oacc[2 * e][i], vscale(2 * e), zh),
+                                    __builtin_fmaf(oacc[2 * e + 1][i], vscale(2 * e + 1), zh));
                 if (r16 == 0) *reinterpret_cast<float2*>(o + kD) = make_float2(mh, lh);
             }
         }
@@ -339,12 +417,35 @@ __global__ void __launch_bounds__(512) tq_decode_kernel(DecodeParams p) {
     const uint32_t odd_mask = (r16 & 1) ? ~0u : 0u, hi_mask = (r16 & 2) ? ~0u : 0u;
     const int diag_slot = ((r16 >> 2) == grp ? 0 : 16) + r16;
 
+    // G32 (slots in whole 16-byte chunks, so mis = 0): the key block of token
+    // r16 (block grp; its 4-byte floor, the block starting gks = 0 or 2 bytes
+    // in), and the value block r16 / 4 of token 4 grp (+ i rows for token
+    // 4 grp + i): d (| m) at gvb, the codes of dims 8 r16 .. + 7 from the
+    // 4-byte floor of gvc, gvsh bytes in
+    const int gk = kq + TG::be * grp;
+    const int gkfl = gk & ~3;
+    const uint32_t gks = (uint32_t)(gk & 3);
+    const int gvb = 4 * grp * TG::row + TG::part + TG::be * (r16 >> 2);
+    const int gvc = gvb + (KB == 3 ? 2 + 3 * (r16 & 3) : 4 + 8 * (r16 & 1));
+    const uint32_t gvsh = (uint32_t)(gvc & 3);
+
     // raw bytes of the pair in page buffers 2 PS, 2 PS + 1
     auto read_codes = [&](auto ps_c, CODES& R) __attribute__((always_inline)) {
         constexpr int PS = decltype(ps_c)::value;
 #pragma unroll
         for (int pp = 0; pp < 2; ++pp) {
             const uint8_t* pg = ring + (2 * PS + pp) * TG::page;
+            if constexpr (G32) {
+#pragma unroll
+                for (int i = 0; i < (KB == 3 ? 4 : 5); ++i) R.kd[pp][i] = lds32(pg + gkfl + 4 * i);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint8_t* cr = pg + (gvc & ~3) + i * TG::row;
+                    R.cw[pp][i][0] = lds32(cr);
+                    R.cw[pp][i][1] = lds32(cr + 4);
+                }
+                continue;
+            }
 #pragma unroll
             for (int i = 0; i < (KB == 3 ? 4 : 5); ++i) R.kd[pp][i] = lds32(pg + kfl + 4 * i);
 #pragma unroll
@@ -355,9 +456,23 @@ __global__ void __launch_bounds__(512) tq_decode_kernel(DecodeParams p) {
             }
         }
     };
+    // TurboQuant: the norms of token r16 on both pages, the scales / zeros of
+    // tokens 4 grp + i of the lane's own page; G32: hsz[i][pp] = d (| m) of
+    // token 4 grp + i on page pp (value block r16 / 4)
     auto read_halves = [&](auto ps_c, TqHalves& H) __attribute__((always_inline)) {
         constexpr int PS = decltype(ps_c)::value;
         const uint8_t* pg = ring + 2 * PS * TG::page;
+        if constexpr (G32) {
+            H.nrm = 0u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int pp = 0; pp < 2; ++pp) {
+                    const uint8_t* vb = pg + pp * TG::page + gvb + i * TG::row;
+                    H.hsz[i][pp] = KB == 3 ? lds16(vb) : lds32(vb);
+                }
+            return;
+        }
         H.nrm = lds16(pg + kq + TG::mse) | (lds16(pg + TG::page + kq + TG::mse) << 16);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -372,6 +487,52 @@ __global__ void __launch_bounds__(512) tq_decode_kernel(DecodeParams p) {
     // run bytes r .. r + 1 of tokens 4 grp + 2 hh and + 1 in the two halves)
     constexpr int NW = VB == 4 ? 4 : 3;
     auto phase1 = [&](const CODES& R, AT (&a)[2][4], uint32_t (&wv)[2][2][NW]) __attribute__((always_inline)) {
+        if constexpr (G32) {
+            // keys: code * d + m (4-bit) or (code - 4) * d (3-bit, the exact
+            // table then one packed multiply), fp16, MFMA j values 8j .. 8j+7
+            // of block grp; values: the code words of tokens 4 grp + i
+            // (3-bit: wv[pp][i >> 1][i & 1] = 24 code bits; 4-bit:
+            // wv[pp][i >> 1][2 (i & 1) + k] = code dword k)
+#pragma unroll
+            for (int pp = 0; pp < 2; ++pp) {
+                u32x4 aw[4];
+                if constexpr (KB == 3) {
+                    const bool off2 = gks != 0u;
+                    const uint32_t d16 = off2 ? R.kd[pp][0] >> 16 : R.kd[pp][0] & 0xffffu;
+                    const uint32_t c0 = off2 ? R.kd[pp][1] : __builtin_amdgcn_alignbyte(R.kd[pp][1], R.kd[pp][0], 2);
+                    const uint32_t c1 = off2 ? R.kd[pp][2] : __builtin_amdgcn_alignbyte(R.kd[pp][2], R.kd[pp][1], 2);
+                    const uint32_t c2 = off2 ? R.kd[pp][3] : __builtin_amdgcn_alignbyte(R.kd[pp][3], R.kd[pp][2], 2);
+                    const uint32_t g24[4] = {c0 & 0xffffffu, (c0 >> 24) | ((c1 & 0xffffu) << 8),
+                                             (c1 >> 16) | ((c2 & 0xffu) << 16), c2 >> 8};
+                    const f16x2 d2 = __builtin_bit_cast(f16x2, d16 * 0x10001u);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const u32x2 lo = lds.lut4[g24[j] & 0xfffu], hi = lds.lut4[g24[j] >> 12];
+                        aw[j] = u32x4{g32_mul(lo[0], d2), g32_mul(lo[1], d2), g32_mul(hi[0], d2), g32_mul(hi[1], d2)};
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        wv[pp][i >> 1][i & 1] = __builtin_amdgcn_alignbyte(R.cw[pp][i][1], R.cw[pp][i][0], gvsh) & 0xffffffu;
+                } else {
+                    const uint32_t dm = R.kd[pp][0];
+                    const f16x2 d2 = __builtin_bit_cast(f16x2, (dm & 0xffffu) * 0x10001u);
+                    const f16x2 m2 = __builtin_bit_cast(f16x2, (dm >> 16) * 0x10001u);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            aw[j][e] = g32_nib2(R.kd[pp][1 + 2 * (j & 1) + (e >> 1)], e & 1, j >= 2, d2, m2);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        wv[pp][i >> 1][2 * (i & 1)] = R.cw[pp][i][0];
+                        wv[pp][i >> 1][2 * (i & 1) + 1] = R.cw[pp][i][1];
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) a[pp][j] = __builtin_bit_cast(AT, aw[j]);
+            }
+            return;
+        }
 #pragma unroll
         for (int pp = 0; pp < 2; ++pp) {
             u32x4 aw[4];
@@ -417,6 +578,109 @@ __global__ void __launch_bounds__(512) tq_decode_kernel(DecodeParams p) {
     // tokens of the first / second page (0: the page contributes nothing)
     auto phase2 = [&](const AT (&a)[2][4], uint32_t (&wv)[2][2][NW], const TqHalves& H, int nv0, int nv1)
                       __attribute__((always_inline)) {
+        if constexpr (G32) {
+            // values first: d (| m) of tokens 4 grp + i on both pages, zero past
+            // a page's end (so those rows are 0 whatever their bytes), and the
+            // 3-bit tables read early
+            uint32_t dv[2][4];
+#pragma unroll
+            for (int i2 = 0; i2 < 4; ++i2) {
+                dv[0][i2] = H.hsz[i2][0];
+                dv[1][i2] = H.hsz[i2][1];
+            }
+            u32x2 vlo[2][4], vhi[2][4];
+            if constexpr (KB == 3) {
+#pragma unroll
+                for (int pp = 0; pp < 2; ++pp)
+#pragma unroll
+                    for (int i2 = 0; i2 < 4; ++i2) {
+                        const uint32_t w = wv[pp][i2 >> 1][i2 & 1];
+                        vlo[pp][i2] = lds.lut4[w & 0xfffu];
+                        vhi[pp][i2] = lds.lut4[w >> 12];
+                    }
+            }
+            // S^T per page against the same Q^T (column r16 >= 8: the second
+            // page), times scale log2(e)
+            f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) s0 = mfma16x16x32(a[0][j], qb[j], s0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) s1 = mfma16x16x32(a[1][j], qb[j], s1);
+            const bool second = r16 >= 8;
+            float sv[4];
+#pragma unroll
+            for (int i2 = 0; i2 < 4; ++i2) sv[i2] = (second ? s1[i2] : s0[i2]) * p.scale_log2;
+            if (nv0 < kBs || nv1 < kBs) {  // tokens past a page's end may hold anything
+                const int nvl = second ? nv1 : nv0;
+#pragma unroll
+                for (int i2 = 0; i2 < 4; ++i2) {
+                    sv[i2] = 4 * grp + i2 < nvl ? sv[i2] : kNegInf;
+                    dv[0][i2] = 4 * grp + i2 < nv0 ? dv[0][i2] : 0u;
+                    dv[1][i2] = 4 * grp + i2 < nv1 ? dv[1][i2] : 0u;
+                }
+            }
+            // lazy reference max; a head's max spans columns c, c ^ 8
+            const float mloc = vmax(vmax(sv[0], sv[1]), vmax(sv[2], sv[3]));
+            if (__ballot(mloc > m_thr)) {
+                float mx = vmax_over_groups(mloc);
+                mx = vmax(mx, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, mx), 0x128, 0xf, 0xf, false)));
+                const bool upd = mx > m_thr;
+                const float m_new = upd ? mx : m_run;
+                const float alpha = upd ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+                l_part *= alpha;
+                const f32x4 al = gather4_from_row0(alpha, wscr + 64, r16, grp);
+#pragma unroll
+                for (int i2 = 0; i2 < 4; ++i2)
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) oacc[c][i2] *= al[i2];
+                m_run = m_new;
+                m_thr = m_run + 8.0f;
+            }
+            const float m_use = m_run == kNegInf ? 0.0f : m_run;
+            float psum = 0.0f;
+            f16x4 pw;
+#pragma unroll
+            for (int i2 = 0; i2 < 4; ++i2) {
+                const float pv = __builtin_amdgcn_exp2f(sv[i2] - m_use);
+                psum += pv;
+                pw[i2] = (_Float16)pv;
+            }
+            l_part += psum;
+            // P: rows 0-7 take k = 8 grp + i (first page, token 4 grp + i),
+            // rows 8-15 k = 8 grp + 4 + i (second page)
+            const u32x2 pw2 = __builtin_bit_cast(u32x2, pw);
+            const uint32_t lo_m = r16 < 8 ? ~0u : 0u;
+            const AT pa = __builtin_bit_cast(AT, u32x4{pw2[0] & lo_m, pw2[1] & lo_m, pw2[0] & ~lo_m, pw2[1] & ~lo_m});
+            // V values of tokens 4 grp + i, dims 8 r16 + 2e, + 1, one e at a
+            // time: B operands {token 0,1}, {token 2,3} of those dims, first
+            // page then second, for chunks 2e and 2e + 1; O += P . V
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                uint32_t ve[2][4];
+#pragma unroll
+                for (int pp = 0; pp < 2; ++pp)
+#pragma unroll
+                    for (int i2 = 0; i2 < 4; ++i2) {
+                        const f16x2 d2 = __builtin_bit_cast(f16x2, (dv[pp][i2] & 0xffffu) * 0x10001u);
+                        if constexpr (KB == 3) {
+                            ve[pp][i2] = g32_mul(e < 2 ? vlo[pp][i2][e] : vhi[pp][i2][e - 2], d2);
+                        } else {
+                            const f16x2 m2 = __builtin_bit_cast(f16x2, (dv[pp][i2] >> 16) * 0x10001u);
+                            const uint32_t w = wv[pp][i2 >> 1][2 * (i2 & 1) + (e >> 1)];
+                            ve[pp][i2] = g32_nib2(w, e & 1, (r16 & 3) >= 2, d2, m2);
+                        }
+                    }
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t sel = h ? 0x07060302u : 0x05040100u;
+                    const AT vb = __builtin_bit_cast(
+                        AT, u32x4{__builtin_amdgcn_perm(ve[0][1], ve[0][0], sel), __builtin_amdgcn_perm(ve[0][3], ve[0][2], sel),
+                                  __builtin_amdgcn_perm(ve[1][1], ve[1][0], sel), __builtin_amdgcn_perm(ve[1][3], ve[1][2], sel)});
+                    oacc[2 * e + h] = mfma16x16x32(pa, vb, oacc[2 * e + h]);
+                }
+            }
+            return;
+        }
         // ||C[codes]||^2 per token: the Gram diagonal (token r16's value in
         // the lanes with grp == r16 / 4, element r16 % 4); the row factor
         // scale * norm / ||C|| (scale * norm without the norm correction)
@@ -642,21 +906,28 @@ __global__ void __launch_bounds__(512) tq_decode_kernel(DecodeParams p) {
 
 // TurboQuant decode (reference layout, G <= 8) with the pipelined kernel;
 // returns VMC_EINVAL when the layout is not one it was built for.
-template <int KB, int VB, bool BF>
+template <int KB, int VB, bool BF, bool G32 = false>
 int launch_tq_decode(DecodeParams& prm, hipStream_t stream) {
-    using TG = TqGeo<KB, VB>;
-    if (prm.entry_bytes != TG::slot || prm.mse_bytes != TG::mse || prm.key_packed != TG::kp ||
-        prm.val_data != TG::vd || prm.G > 8 || prm.Hkv > TG::waves)
+    using TG = TqGeo<KB, VB, G32>;
+    if (G32 ? prm.entry_bytes != TG::slot
+            : (prm.entry_bytes != TG::slot || prm.mse_bytes != TG::mse || prm.key_packed != TG::kp ||
+               prm.val_data != TG::vd))
         return VMC_EINVAL;
+    if (prm.G > 8 || prm.Hkv > TG::waves) return VMC_EINVAL;
     prm.row_bytes = prm.Hkv * TG::slot;
     prm.grid = prm.per_seq ? prm.B : tq_ranges(prm.B, prm.Hkv, prm.max_blocks, prm.max_splits, num_cus());
-    hipLaunchKernelGGL((tq_decode_kernel<KB, VB, BF>), dim3(prm.grid), dim3(64 * prm.Hkv), 0, stream, prm);
+    hipLaunchKernelGGL((tq_decode_kernel<KB, VB, BF, G32>), dim3(prm.grid), dim3(64 * prm.Hkv), 0, stream, prm);
     VMC_LAUNCH_CHECK();
     if (!prm.per_seq) {
         hipLaunchKernelGGL(decode_merge_kernel, dim3(prm.B, prm.Hkv), dim3(64 * prm.G), 0, stream, prm);
         VMC_LAUNCH_CHECK();
     }
     return VMC_OK;
+}
+
+// the per-32-group variant (fp16 activations, 3- or 4-bit) on the same kernel
+int launch_g32_decode(DecodeParams& prm, int bits, hipStream_t s) {
+    return bits == 3 ? launch_tq_decode<3, 3, false, true>(prm, s) : launch_tq_decode<4, 4, false, true>(prm, s);
 }
 
 int launch_tq_decode_any(DecodeParams& prm, int kb, int vb, bool bf, hipStream_t s) {
