@@ -272,34 +272,50 @@ __global__ void __launch_bounds__(1024) decode_merge_kernel(DecodeParams p) {
         const int slot = s == 0 ? 2 * w0 + 1 : 2 * (w0 + s);
         return p.part + slot * rs + (int64_t)hq * (kD + 2);
     };
-    float M = kNegInf;
-    for (int s0 = 0; s0 < nseg; s0 += 64)
-        M = fmaxf(M, wave_max(s0 + lane < nseg ? row(s0 + lane)[kD] : kNegInf));
-    const float Mu = M == kNegInf ? 0.0f : M;
+    // one pass over the pieces, 64 at a time, with a running max: the m / l
+    // pair of each piece and the first 16 pieces' o rows are loaded together,
+    // so a sequence cut into at most 16 pieces costs one round of loads
     const int r16 = lane & 15, grp = lane >> 4;
-    float L = 0.0f;
+    float M = kNegInf, L = 0.0f;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int s0 = 0; s0 < nseg; s0 += 64) {
         const int cnt = min(64, nseg - s0);
+        float2 ml = make_float2(kNegInf, 0.0f);
+        if (lane < cnt) ml = *reinterpret_cast<const float2*>(row(s0 + lane) + kD);
+        // four 16-lane groups take pieces j = grp, grp + 4, ...; four in flight each
+        float2 o[4][4];
+        auto load_o = [&](int j0) __attribute__((always_inline)) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int jc = min(j0 + 4 * u + grp, cnt - 1);
+                const float2* r = reinterpret_cast<const float2*>(row(s0 + jc) + 8 * r16);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[u][e] = r[e];
+            }
+        };
+        load_o(0);
+        const float Mn = fmaxf(M, wave_max(ml.x));
+        if (Mn > M && M != kNegInf) {  // wave-uniform
+            const float f = __builtin_amdgcn_exp2f(M - Mn);
+            L *= f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] *= f;
+        }
+        M = Mn;
+        const float Mu = M == kNegInf ? 0.0f : M;
         float wt = 0.0f;
         if (lane < cnt) {
-            const float2 ml = *reinterpret_cast<const float2*>(row(s0 + lane) + kD);
             wt = __builtin_amdgcn_exp2f(ml.x - Mu);
             L = __builtin_fmaf(ml.y, wt, L);
         }
-        // four 16-lane groups take pieces j = grp, grp + 4, ...; four in flight each
         for (int j0 = 0; j0 < cnt; j0 += 16) {
-            float2 o[4][4];
+            if (j0 > 0) load_o(j0);
             float ws[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int j = j0 + 4 * u + grp;
-                const int jc = min(j, cnt - 1);
-                ws[u] = __shfl(wt, jc, 64);
+                ws[u] = __shfl(wt, min(j, cnt - 1), 64);
                 ws[u] = j < cnt ? ws[u] : 0.0f;
-                const float2* r = reinterpret_cast<const float2*>(row(s0 + jc) + 8 * r16);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) o[u][e] = r[e];
             }
 #pragma unroll
             for (int u = 0; u < 4; ++u)
@@ -329,7 +345,7 @@ __global__ void __launch_bounds__(1024) decode_merge_kernel(DecodeParams p) {
 
 // ------------------------------------------------------------------ host
 
-constexpr int kPpsMin = 4;
+constexpr int kPpsMin = 2;
 
 inline int num_cus() {
     static std::mutex mu;
