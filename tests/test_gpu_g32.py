@@ -81,6 +81,12 @@ CASES = {
     "ragged": dict(seq_lens=[1, 17, 0, 300], Hq=16, Hkv=4),
     "gqa16": dict(seq_lens=[300, 1024, 17, 33], Hq=32, Hkv=2),
     "gqa2": dict(seq_lens=[5, 129, 700], Hq=8, Hkv=4),
+    # head shapes of the pipelined kernel (at most 8 query heads per KV head):
+    # one query head per KV head, odd group sizes, one and three KV heads
+    "mha": dict(seq_lens=[40, 257, 2], Hq=4, Hkv=4),
+    "g3": dict(seq_lens=[700, 33], Hq=6, Hkv=2),
+    "g5_one_kv_head": dict(seq_lens=[95, 1500, 16], Hq=5, Hkv=1),
+    "g7_three_kv_heads": dict(seq_lens=[1, 600, 48, 31], Hq=21, Hkv=3),
 }
 
 
