@@ -435,15 +435,9 @@ __global__ void __launch_bounds__(512) tq_decode_kernel(DecodeParams p) {
 #pragma unroll
         for (int pp = 0; pp < 2; ++pp) {
             const uint8_t* pg = ring + (2 * PS + pp) * TG::page;
-            if constexpr (G32) {
+            if constexpr (G32) {  // the value codes: read_vcodes
 #pragma unroll
                 for (int i = 0; i < (KB == 3 ? 4 : 5); ++i) R.kd[pp][i] = lds32(pg + gkfl + 4 * i);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint8_t* cr = pg + (gvc & ~3) + i * TG::row;
-                    R.cw[pp][i][0] = lds32(cr);
-                    R.cw[pp][i][1] = lds32(cr + 4);
-                }
                 continue;
             }
 #pragma unroll
@@ -454,6 +448,21 @@ __global__ void __launch_bounds__(512) tq_decode_kernel(DecodeParams p) {
                 R.cw[pp][i][0] = lds32(cr);
                 R.cw[pp][i][1] = lds32(cr + 4);
             }
+        }
+    };
+    // G32: the value code words of the pair, read after the previous pair's
+    // phase 2 has consumed its own (so one pair's words are live at a time)
+    auto read_vcodes = [&](auto ps_c, CODES& R) __attribute__((always_inline)) {
+        constexpr int PS = decltype(ps_c)::value;
+        if constexpr (G32) {
+#pragma unroll
+            for (int pp = 0; pp < 2; ++pp)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint8_t* cr = ring + (2 * PS + pp) * TG::page + (gvc & ~3) + i * TG::row;
+                    R.cw[pp][i][0] = lds32(cr);
+                    R.cw[pp][i][1] = lds32(cr + 4);
+                }
         }
     };
     // TurboQuant: the norms of token r16 on both pages, the scales / zeros of
@@ -826,6 +835,7 @@ __global__ void __launch_bounds__(512) tq_decode_kernel(DecodeParams p) {
             nvb = (info1 >> 1) & 31;
             ends = info1;
         }
+        read_vcodes(next_c, R);
         read_halves(next_c, H);
     };
 
@@ -880,6 +890,7 @@ __global__ void __launch_bounds__(512) tq_decode_kernel(DecodeParams p) {
         CODES rc;
         TqHalves hz;
         read_codes(std::integral_constant<int, 0>{}, rc);
+        read_vcodes(std::integral_constant<int, 0>{}, rc);
         read_halves(std::integral_constant<int, 0>{}, hz);
         for (int k0 = 0; k0 < npairs; k0 += NPH) {
             static_for<NPH>([&](auto ph) __attribute__((always_inline)) {
