@@ -122,19 +122,22 @@ __device__ __forceinline__ void dma16m(const void* src, uint32_t m0) {
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
 }
 
-// All LDS of the kernel: the K / raw V tile ring (rows of 256 B, 16-byte
-// chunk ch of row r stored at chunk position ch ^ swz(r)), the fp16 V^T
-// tiles (128 rows of 64 keys, 16-byte chunk i of row d at position
-// i ^ ((d >> 1) & 7)), then the per-wave exchange.  swz(r) rotates the low
+// All LDS of the kernel: the per-wave exchange, the fp16 V^T tiles (128
+// rows of 64 keys, 16-byte chunk i of row d at position i ^ ((d >> 1) & 7)),
+// then the K / raw V tile ring (rows of 256 B, 16-byte chunk ch of row r
+// stored at chunk position ch ^ swz(r)).  In that order every V^T read and
+// the K reads of slot 0 sit below 64 KB, where their constant part fits the
+// 16-bit offset of the LDS instruction (above it, each address costs a
+// vector add: 704-710 vs 712-720 us on the 4 x 4096 prefill).  swz(r) rotates the low
 // 4 row bits by two: a bijection on 16 consecutive rows (the 32-row K
 // operand reads spread over all banks) whose bits 2-3 differ for 4
 // consecutive rows (the transpose reads of 4 rows x 16 dims spread too).
 struct PrefillLds {
-    uint8_t tile[NSLOT][2][BN * 256];  // [slot][K, V][row][position]
-    uint8_t vtr[NSLOT][kD * BN * 2];   // [slot][dim][kv position] fp16 V^T
-    float scratch[2][NW][32];          // [alpha, l][wave][row]
+    float scratch[2][NW][32];            // [alpha, l][wave][row]
     alignas(8) uint8_t wide[NSLOT][NW];  // bf16: wave w's V rows of the tile need the exact mode
     float cent[16];                      // TurboQuant key centroids
+    alignas(16) uint8_t vtr[NSLOT][kD * BN * 2];  // [slot][dim][kv position] fp16 V^T
+    uint8_t tile[NSLOT][2][BN * 256];             // [slot][K, V][row][position]
 };
 
 __device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
