@@ -121,6 +121,11 @@ __device__ __forceinline__ V8 as_v8(u32x4 w) {
 __device__ __forceinline__ void dma16m(const void* src, uint32_t m0) {
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
 }
+// The same transfer from a wave-uniform base (SGPRs) plus a 32-bit per-lane
+// offset: no per-lane 64-bit address arithmetic.
+__device__ __forceinline__ void dma16s(const void* base, uint32_t off, uint32_t m0) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(m0) : "memory");
+}
 
 // All LDS of the kernel: the per-wave exchange, the fp16 V^T tiles (128
 // rows of 64 keys, 16-byte chunk i of row d at position i ^ ((d >> 1) & 7)),
@@ -319,8 +324,11 @@ prefill_kernel(PrefillParams p) {
     // local K/V: this lane's row of a tile starting at key k0 is k0 + ld_row
     // (+ 32 in the second round); the LDS rows of this wave in slot 0 (the
     // other slots and the V half at fixed offsets)
-    const uint8_t* const kg_row = kg + (int64_t)ld_row * row_stride;
-    const uint8_t* const vg_row = vg + (int64_t)ld_row * row_stride;
+    // the fast path's transfers: uniform bases (this KV head's dims at the
+    // tile's rows) plus this lane's row and chunk as a 32-bit offset
+    const uint32_t ld_off = (uint32_t)ld_row * (uint32_t)row_stride + ld_col;
+    const uint8_t* const kgu = reinterpret_cast<const uint8_t*>(p.k) + (int64_t)g * kD * 2;
+    const uint8_t* const vgu = reinterpret_cast<const uint8_t*>(p.v) + (int64_t)g * kD * 2;
     const uint32_t lds_w = __builtin_amdgcn_readfirstlane(
         (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)&lds.tile[0][0][1024 * w]);
     constexpr uint32_t kSlotB = 2 * BN * 256, kPartB = BN * 256;
@@ -333,8 +341,8 @@ prefill_kernel(PrefillParams p) {
 #pragma unroll
                 for (int i = 0; i < 2; ++i) {
                     const int64_t off = toff + (int64_t)(32 * i) * row_stride;
-                    dma16m(kg_row + off, lds_w + SL * kSlotB + 8192u * i);
-                    dma16m(vg_row + off, lds_w + SL * kSlotB + kPartB + 8192u * i);
+                    dma16s(kgu + off, ld_off, lds_w + SL * kSlotB + 8192u * i);
+                    dma16s(vgu + off, ld_off, lds_w + SL * kSlotB + kPartB + 8192u * i);
                 }
                 return;
             }
@@ -876,7 +884,7 @@ prefill_kernel(PrefillParams p) {
     };
 
     if constexpr (SRC == SRC_LOCAL) {
-        kv_lo = max(0, q0 - p.pos[q0]);
+        kv_lo = __builtin_amdgcn_readfirstlane(max(0, q0 - p.pos[q0]));  // uniform: scalar tile addresses
         kv_end = q_end;
         ntile = (kv_end - kv_lo + BN - 1) / BN;
         lo = row_ok ? row - p.pos[row] : 0;
