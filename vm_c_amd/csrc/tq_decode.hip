@@ -1,6 +1,8 @@
 // tq_decode.hip -- split-KV paged decode over TurboQuant slots, gfx950:
 // the reference layout (turboquant_4bit_nc / 3bit_nc / k3v4_nc) with at most
-// 8 query heads per KV head.
+// 8 query heads per KV head, and (G32) the per-32-group variant of the same
+// slots (turboquant_4bit_g32 / 3bit_g32; its format is defined in
+// vmc_attn.h, the reference has no code for it).
 //
 // Replaces the decode of vm_c::turboquant_decode_attention
 // (src/cuda/turboquant_kernels.cu:939-1007: q rotation, stage 1 :353-506,
