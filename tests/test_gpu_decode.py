@@ -63,6 +63,18 @@ def test_paged_decode_vs_exact(dev, fmt, case):
     assert np.isfinite(got).all()
 
 
+@pytest.mark.parametrize("fmt", [O.KV_F16, O.KV_Q8_0])
+def test_paged_decode_more_than_64_pieces(dev, fmt):
+    """One 8192-token sequence over ~256 page ranges of 2 pages: the merge
+    combines ~254 pieces per head in rounds of 64, rescaling its running max
+    when a later round holds a larger one."""
+    w = make_workload([8192, 40], Hq=32, Hkv=8, seed=31)
+    got, kc, vc, qf = _run_paged(dev, w, fmt)
+    ex = O.paged_decode_exact(qf, kc, vc, fmt, w.bt, w.seq_lens, w.Hkv, w.scale, BS)
+    ok, err = close_report(got, ex, ATOL, RTOL)
+    assert ok, f"max err {err}"
+
+
 @pytest.mark.parametrize("fmt", [O.KV_F16, O.KV_Q8_0, O.KV_Q4_0])
 def test_paged_decode_vs_ggml_restatement(dev, fmt):
     w = make_workload(seq_lens=[2048, 777], Hq=32, Hkv=8, seed=3)
@@ -152,6 +164,18 @@ def test_tq_decode(dev, method, case):
                                    num_splits=32))
     ok, err = close_report(got, ref, ATOL, RTOL)
     assert ok, f"vs reference restatement: max err {err}"
+
+
+@pytest.mark.parametrize("method", ["turboquant_4bit_nc", "turboquant_3bit_nc"])
+def test_tq_decode_more_than_64_pieces(dev, method):
+    """The ring kernel and the merge on one 8192-token sequence cut into
+    ~254 pieces (rounds of 64 with a running max)."""
+    w = make_workload([8192, 40], Hq=32, Hkv=8, seed=32)
+    got, cache, L = _run_tq(dev, w, method)
+    c, _ = O.tq_tables(128, L.key_quant_bits)
+    ex = O.tq_decode_exact(bits16(w.Q), cache, w.bt, w.seq_lens, w.Hkv, w.scale, BS, L, c)
+    ok, err = close_report(got, ex, ATOL, RTOL)
+    assert ok, f"vs exact: max err {err}"
 
 
 @pytest.mark.parametrize("max_splits", [0, 1])
