@@ -108,7 +108,8 @@ __device__ __forceinline__ void dma16(const uint8_t* base, uint32_t off, uint32_
 // Raw bytes of a page pair in registers.  TqCodes is consumed by the first
 // phase of a pair (key table lookups issued, value bytes permuted), so the
 // next pair's codes are read into the same registers before the second phase
-// runs; TqHalves is used by the second phase, and the next pair's halves are
+// runs (G32: the value code words only after it, since its second phase
+// still reads this pair's from the copies the first phase made); TqHalves is used by the second phase, and the next pair's halves are
 // read into it after that phase (the next step's first phase covers their
 // latency).
 // wait until at most the transfers of N page pairs (6 each) are outstanding
@@ -805,7 +806,8 @@ __global__ void __launch_bounds__(512) tq_decode_kernel(DecodeParams p) {
 
     // ---- the pair of pages (i, i + 1) of the chunk from codes R and halves
     // H; between the phases, the codes of the next pair are read into R (from
-    // page buffers NEXT), after them its halves into H.  A pair that a piece
+    // page buffers NEXT; G32: its key words only), after them its halves
+    // into H (G32: and its value code words into R).  A pair that a piece
     // boundary splits runs phase 2 twice, each time with one page masked.
     auto process_pair = [&](CODES& R, TqHalves& H, auto next_c, int i, int npc) __attribute__((always_inline)) {
         AT a[2][4];
