@@ -311,6 +311,27 @@ int vmc_turboquant_prefill_attention(void* output, const void* query, const void
                                      size_t workspace_bytes, vmc_stream_t stream);
 
 /*
+ * One (sequence, position) row per token of an Engine step, for
+ * vmc_turboquant_prefill_attention.  The Engine uploads block_tables and
+ * seq_lens per request (src/core/engine.cpp:731-757) and token_to_seq /
+ * token_positions only for prefill requests' tokens (:686-691, :760-766; a
+ * decode request's token keeps 0 / 0).  The ggml TurboQuant node
+ * (src/official/turboquant_kv_bridge.cpp:99-107) decodes num_tokens rows over
+ * the per-request arrays, which is exact only for decode-only steps; this
+ * gives every token of a prefill or mixed step its row: a prefill token keeps
+ * (token_to_seq, token_positions), a decode token of request r (counted from
+ * the request boundaries in token order) gets (r, seq_lens[r] - 1).  Rows of
+ * a request outside [0, num_reqs) get (0, -1): no keys, a zero output row.
+ *   row_seq, row_pos   int32 [num_tokens] (written)
+ *   token_to_seq, token_positions int32 [num_tokens]; seq_lens int32 [num_reqs]
+ * No counterpart in the reference (it has no such mapping).  One workgroup;
+ * stream-ordered.
+ */
+int vmc_batch_token_rows(int32_t* row_seq, int32_t* row_pos, const int32_t* token_to_seq,
+                         const int32_t* token_positions, const int32_t* seq_lens, int num_tokens,
+                         int num_reqs, vmc_stream_t stream);
+
+/*
  * Causal flash-attention prefill over contiguous ("local") K/V, bf16 or fp16,
  * MFMA for QK^T and PV, fp32 softmax.  Each sequence's tokens are contiguous
  * with positions 0..n-1, so token t attends tokens [t - pos(t), t].

@@ -398,6 +398,23 @@ static void test_tq_bridge() {
     CHECK(b.is_prefill() && b.num_prefill_tokens() == 3);
     b.mark_decode_mode(5);
     CHECK(!b.is_prefill() && b.num_decode_tokens() == 5 && b.num_tokens() == 5 && b.num_prefill_tokens() == 0);
+    // batch metadata checked before any launch: a decode-only step must have
+    // one token per request; a step with prefill tokens needs token_to_seq /
+    // token_positions (the Engine's per-request block tables and lengths)
+    const int64_t fake_slots = 0;
+    b.set_batch_metadata(&fake_slots, nullptr, nullptr, 3, 2, 4, 16, false, 0, 3, nullptr, nullptr, nullptr);
+    CHECK(throws([&] { official::turboquant_attn_op(params(1, 0.1f, &b).data(), &x, ne3, nb3, &x, &x, &x); },
+                 "decode step of 3 tokens over 2 requests"));
+    b.set_batch_metadata(&fake_slots, nullptr, nullptr, 3, 2, 4, 16, true, 3, 0, nullptr, nullptr, nullptr);
+    CHECK(throws([&] { official::turboquant_attn_op(params(1, 0.1f, &b).data(), &x, ne3, nb3, &x, &x, &x); },
+                 "prefill step without token_to_seq"));
+    // the reference's workspace signature (kernels_turboquant.h:103): no
+    // device memory for head_dim other than 128, one split, or no rows
+    TQWorkspace ws;
+    ws.ensure_decode(16, 64, 32, 0);
+    ws.ensure_decode(16, 128, 1, 0);
+    ws.ensure_decode(0, 128, 32, 0);
+    CHECK(ws.decode_workspace == nullptr && ws.decode_bytes == 0);
 }
 
 int main() {

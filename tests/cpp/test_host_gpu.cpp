@@ -507,9 +507,12 @@ static void test_page_movement() {
 }
 
 // the ggml TurboQuant attention node (turboquant_attn_op) over layer 1 of a
-// two-layer pool: a prefill of three sequences with one query row per token
-// (its sequence's block-table row, length position + 1), then a decode step;
-// q in the head-split view [D, Hq, T]
+// two-layer pool, fed the batch metadata exactly as the Engine uploads it
+// (build_batch_metadata -> DeviceBatchMetadata::upload: block tables and
+// lengths per request, token_to_seq / positions only for prefill tokens):
+// a prefill of three sequences, a mixed step (a decode, a 20-token chunk over
+// a cached prefix, a new 5-token prompt, another decode), then a decode-only
+// step; q in the head-split view [D, Hq, T]
 static void test_tq_bridge_node(const char* method) {
     std::printf("case: TurboQuant attention node %s\n", method);
     std::fflush(stdout);
@@ -520,7 +523,7 @@ static void test_tq_bridge_node(const char* method) {
     mgr.allocate_gpu_blocks_for_group(0, 64);
     TurboQuantKvBridge br;
     br.initialize(cc, Hq, Hkv, D, &mgr, 0, 2, 1, ScalarType::FLOAT16);
-    br.reserve_decode(512, 64);
+    br.reserve_decode(64, 64);  // the 357-token prefill grows the rows and workspace itself
     void* pool = mgr.key_cache_ptr(1);
     const size_t pool_n = (size_t)64 * mgr.group(0).bytes_per_block;
     HIP_CHECK(hipMemset(pool, 0, pool_n));
@@ -538,38 +541,48 @@ static void test_tq_bridge_node(const char* method) {
     std::memcpy(op.data() + official::kTqAttnOpLayer, &layer, 4);
     std::memcpy(op.data() + official::kTqAttnOpScale, &scale, 4);
     std::memcpy(op.data() + official::kTqAttnOpBridge, &bp, sizeof(bp));
-    const std::vector<int> lens = {40, 17, 300};
-    for (int step = 0; step < 2; ++step) {
-        std::vector<ScheduledRequest> rq(lens.size());
-        for (size_t i = 0; i < lens.size(); ++i) {
-            rq[i].request_id = "r" + std::to_string(i);
-            if (step == 0) {
-                rq[i].num_scheduled_tokens = lens[i];
-                rq[i].is_prefill = true;
-            } else {
-                rq[i].num_computed_tokens = lens[i];
-            }
+    DeviceBatchMetadata dm(8, 512, 64);
+    struct Sched {
+        const char* id;
+        int computed, scheduled;
+        bool prefill;
+    };
+    const std::vector<std::vector<Sched>> steps = {
+        {{"r0", 0, 40, true}, {"r1", 0, 17, true}, {"r2", 0, 300, true}},
+        {{"r0", 40, 1, false}, {"r1", 17, 20, true}, {"r3", 0, 5, true}, {"r2", 300, 1, false}},
+        {{"r2", 301, 1, false}, {"r0", 41, 1, false}, {"r1", 37, 1, false}, {"r3", 5, 1, false}},
+    };
+    const char* names[3] = {"prefill", "mixed", "decode"};
+    for (size_t step = 0; step < steps.size(); ++step) {
+        std::vector<ScheduledRequest> rq(steps[step].size());
+        for (size_t i = 0; i < rq.size(); ++i) {
+            rq[i].request_id = steps[step][i].id;
+            rq[i].num_computed_tokens = steps[step][i].computed;
+            rq[i].num_scheduled_tokens = steps[step][i].scheduled;
+            rq[i].is_prefill = steps[step][i].prefill;
         }
         HostBatchMetadata hm = build_batch_metadata(mgr, rq);
         CHECK(hm.ok);
         const int T = hm.num_tokens, mb = hm.max_num_blocks_per_req;
+        AttentionMetadata am = dm.upload(hm, BS, nullptr);
+        // the rows the oracle attends: a prefill token its own position, a
+        // decode token its request's last position
         std::vector<int32_t> bt_rows((size_t)T * mb), len_rows(T);
-        for (int t = 0; t < T; ++t) {
-            const int sq = hm.token_to_seq[t];
-            std::copy(hm.block_tables.begin() + (size_t)sq * mb, hm.block_tables.begin() + (size_t)(sq + 1) * mb,
-                      bt_rows.begin() + (size_t)t * mb);
-            len_rows[t] = hm.token_positions[t] + 1;
-        }
+        for (size_t ri = 0, t = 0; ri < rq.size(); ++ri)
+            for (int i = 0; i < (rq[ri].is_prefill ? rq[ri].num_scheduled_tokens : 1); ++i, ++t) {
+                std::copy(hm.block_tables.begin() + ri * mb, hm.block_tables.begin() + (ri + 1) * mb,
+                          bt_rows.begin() + t * mb);
+                len_rows[t] = rq[ri].is_prefill ? rq[ri].num_computed_tokens + i + 1 : hm.seq_lens[ri];
+            }
         std::vector<uint16_t> K((size_t)T * Hkv * D), V(K.size()), Q((size_t)T * Hq * D);
         orc_randn_f16(K.data(), (int64_t)K.size(), 20 + step, 1);
         orc_randn_f16(V.data(), (int64_t)V.size(), 20 + step, 2);
         orc_randn_f16(Q.data(), (int64_t)Q.size(), 20 + step, 3);
         Dev<uint16_t> dK(K), dV(V), dQ(Q), dO(Q.size());
-        Dev<int64_t> dslots(hm.slot_mapping);
-        Dev<int32_t> dbt(bt_rows), dlen(len_rows);
-        br.set_batch_metadata(dslots.p, dbt.p, dlen.p, T, hm.num_reqs, mb, BS, step == 0, step == 0 ? T : 0,
-                              step == 0 ? 0 : T, nullptr, nullptr, nullptr);
-        if (step == 1) br.mark_decode_mode(T);
+        br.set_batch_metadata(am.slot_mapping, am.block_tables, am.seq_lens, T, am.num_reqs,
+                              am.max_num_blocks_per_req, BS, am.is_prefill, am.num_prefill_tokens,
+                              am.num_decode_tokens, am.token_to_seq, am.token_positions, nullptr);
+        if (!am.is_prefill) br.mark_decode_mode(T);
         const int64_t ne[4] = {D, Hq, T, 1};
         const size_t nb[4] = {2, (size_t)2 * D, (size_t)2 * D * Hq, (size_t)2 * D * Hq * T};
         official::turboquant_attn_op(op.data(), dQ.p, ne, nb, dK.p, dV.p, dO.p);
@@ -584,9 +597,9 @@ static void test_tq_bridge_node(const char* method) {
                             BS, mb, &L, C.data(), 0, 0);
         double err = 0;
         CHECK(close(dO.get(), ex, &err));
-        std::printf("  %s: %d rows, max err %.3g\n", step == 0 ? "prefill" : "decode", T, err);
+        std::printf("  %s: %d rows over %d requests, max err %.3g\n", names[step], T, hm.num_reqs, err);
     }
-    for (size_t i = 0; i < lens.size(); ++i) mgr.free_slots("r" + std::to_string(i));
+    for (const char* id : {"r0", "r1", "r2", "r3"}) mgr.free_slots(id);
 }
 
 int main() {

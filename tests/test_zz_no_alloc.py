@@ -46,16 +46,47 @@ def test_noalloc_decode_matches_workspace_decode(dev, bf16):
             f"noalloc decode differs from the workspace decode (B={w.B})"
 
 
+@pytest.mark.parametrize("D,Hq,Hkv", [(256, 16, 4), (128, 64, 2)])
+def test_noalloc_one_wave_per_row_shapes(dev, D, Hq, Hkv):
+    """head_dim 256 and 32 query heads per KV head run the one-wave-per-row
+    kernel, which needs no split partials: the allocation-free entry point
+    takes them at any size and matches the workspace entry point."""
+    import torch
+    from vm_c_amd import capi
+    cfg = capi.tq_config(D, "turboquant_4bit_nc")
+    w = make_workload([700, 33, 1500], Hq=Hq, Hkv=Hkv, D=D, seed=23)
+    cache, q = _pages(dev, w, cfg, False)
+    bt = torch.from_numpy(w.bt).to(dev)
+    sl = torch.from_numpy(w.seq_lens).to(dev)
+    ref = torch.full_like(q, float("nan"))
+    capi.turboquant_decode_attention(ref, q, cache, bt, sl, w.Hkv, float(w.scale), cfg, BS)
+    got = torch.full_like(q, float("nan"))
+    capi.turboquant_decode_attention_noalloc(got, q, cache, bt, sl, w.Hkv, float(w.scale), cfg, BS)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+
+
 def test_noalloc_rejects_oversized_partials(dev):
+    """A tuned-kernel shape whose split partials exceed the array is rejected
+    with VMC_ENOMEM.  Every argument is a real allocation of the call's full
+    size, with empty sequences and an all-hole block table, so the call could
+    not touch memory outside them even if it launched."""
     import ctypes as C
+    import torch
     from vm_c_amd import capi
     L = capi.load()
     cfg = capi.tq_config(128, "turboquant_3bit_nc")
     cap = L.vmc_noalloc_scratch_bytes()
-    # 1024 query heads per call: the partial rows of every range exceed the array
-    need = capi.turboquant_decode_workspace_size(64, 1024, 8, 128, 4096, BS)
+    B, Hq, Hkv, mb = 64, 128, 8, 4096  # 16 query heads per KV head: the tuned decode
+    need = capi.turboquant_decode_workspace_size(B, Hq, Hkv, 128, mb, BS)
     assert need > cap
-    p = C.c_void_p(256)
-    rc = L.vmc_turboquant_decode_attention_noalloc(p, p, p, p, p, 64, 1024, 8, 128, C.c_float(0.1), BS, 4096,
-                                                   C.byref(cfg), 0, 0, None)
+    q = torch.zeros(B, Hq, 128, dtype=torch.float16, device=dev)
+    out = torch.zeros_like(q)
+    bt = torch.full((B, mb), -1, dtype=torch.int32, device=dev)
+    sl = torch.zeros(B, dtype=torch.int32, device=dev)
+    cache = torch.zeros(BS * Hkv * cfg.slot_size_aligned, dtype=torch.uint8, device=dev)
+    p = lambda t: C.c_void_p(t.data_ptr())
+    rc = L.vmc_turboquant_decode_attention_noalloc(p(out), p(q), p(cache), p(bt), p(sl), B, Hq, Hkv, 128,
+                                                   C.c_float(0.1), BS, mb, C.byref(cfg), 0, 0, None)
+    torch.cuda.synchronize()
     assert rc == capi.VMC_ENOMEM

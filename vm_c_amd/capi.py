@@ -70,6 +70,8 @@ def load():
     L.vmc_turboquant_prefill_attention.restype = _I
     L.vmc_turboquant_prefill_attention.argtypes = [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I64,
                                                    _I64, C.POINTER(TQConfig), _I, _I, _P, _SZ, _P]
+    L.vmc_batch_token_rows.restype = _I
+    L.vmc_batch_token_rows.argtypes = [_P, _P, _P, _P, _P, _I, _I, _P]
     L.vmc_tq_config_from_method.restype = _I
     L.vmc_tq_config_from_method.argtypes = [_I, C.c_char_p, C.POINTER(TQConfig)]
     L.vmc_tq_host_tables.restype = _I
@@ -338,3 +340,12 @@ def turboquant_prefill_attention(out, query, kv_cache, block_tables, token_to_se
         C.byref(cfg), _dtype_code(query), 1, None, 0, _stream(stream))
     _check(rc, "vmc_turboquant_prefill_attention")
     return out
+
+
+def batch_token_rows(row_seq, row_pos, token_to_seq, token_positions, seq_lens, stream=None):
+    """Per-token (sequence, position) rows of an Engine step whose
+    token_to_seq / token_positions hold only the prefill tokens' entries
+    (decode tokens 0 / 0); seq_lens is per request."""
+    rc = load().vmc_batch_token_rows(_ptr(row_seq), _ptr(row_pos), _ptr(token_to_seq), _ptr(token_positions),
+                                     _ptr(seq_lens), token_to_seq.numel(), seq_lens.numel(), _stream(stream))
+    _check(rc, "vmc_batch_token_rows")

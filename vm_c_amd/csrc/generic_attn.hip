@@ -236,6 +236,8 @@ gen_attn_kernel(GenArgs a, TQTables tab) {
         n = a.pos[row] + 1;
         if (a.num_seqs >= 0 && (seq < 0 || seq >= a.num_seqs)) n = 0;
     }
+    // paged rows: no further than the block-table row reaches
+    if constexpr (SRC != GEN_LOCAL) n = (int)min((int64_t)n, a.max_blocks * a.bs);
     if (n <= 0) {
 #pragma unroll
         for (int i = 0; i < NPL; ++i) op[lane + 64 * i] = f32_to_half<BF>(0.0f);

@@ -1528,6 +1528,14 @@ int launch_tq(DecodeParams& prm, int kb, int vb, bool half, hipStream_t s) {
     return VMC_EINVAL;
 }
 
+// TurboQuant decode rows that the one-wave-per-(row, head) kernel takes:
+// head_dim 64 / 256, fp8 keys with bf16 halves, head counts past the tuned
+// kernels' (no workspace)
+bool tq_generic_route(const vmc_tq_config* cfg, int head_dim, int num_heads, int num_kv_heads, int half_dtype) {
+    return generic_head_dim(head_dim) || (cfg->key_fp8 && half_dtype == VMC_DTYPE_BF16) ||
+           beyond_tuned_decode(head_dim, num_heads, num_kv_heads);
+}
+
 int tq_decode_rows(void* output, const void* query, const void* kv_cache, const int32_t* block_tables,
                    const int32_t* seq_lens, const int32_t* row_seq, const int32_t* row_pos, int batch_size,
                    int num_heads, int num_kv_heads, int head_dim, float scale, int64_t block_size,
@@ -1536,8 +1544,7 @@ int tq_decode_rows(void* output, const void* query, const void* kv_cache, const 
     if (!tq_config_valid(cfg) || cfg->head_dim != head_dim) return VMC_EINVAL;
     if (half_dtype != VMC_DTYPE_F16 && half_dtype != VMC_DTYPE_BF16) return VMC_EINVAL;
     if (max_num_blocks_per_req > 0x7fffffff) return VMC_EINVAL;
-    if (generic_head_dim(head_dim) || (cfg->key_fp8 && half_dtype == VMC_DTYPE_BF16) ||
-        beyond_tuned_decode(head_dim, num_heads, num_kv_heads)) {
+    if (tq_generic_route(cfg, head_dim, num_heads, num_kv_heads, half_dtype)) {
         // head_dim 64 / 256, fp8 keys with bf16 halves, and head counts past
         // the tuned kernels': one wave per (row, query head), no workspace;
         // q, out and the stored halves are half_dtype (the per-32-group
@@ -1712,9 +1719,13 @@ extern "C" int vmc_turboquant_decode_attention_noalloc(
     int64_t block_size, int64_t max_num_blocks_per_req, const vmc_tq_config* cfg, int half_dtype,
     int max_num_kv_splits, vmc_stream_t stream) {
     if (num_heads <= 0 || num_kv_heads <= 0 || batch_size < 0) return VMC_EINVAL;
-    const size_t need = vmc_turboquant_decode_workspace_size(batch_size, num_heads, num_kv_heads, head_dim,
-                                                             max_num_blocks_per_req, block_size,
-                                                             max_num_kv_splits);
+    if (!tq_config_valid(cfg) || cfg->head_dim != head_dim) return VMC_EINVAL;
+    // the shapes of the one-wave-per-row kernel need no split partials
+    const size_t need = tq_generic_route(cfg, head_dim, num_heads, num_kv_heads, half_dtype)
+                            ? 0
+                            : vmc_turboquant_decode_workspace_size(batch_size, num_heads, num_kv_heads, head_dim,
+                                                                   max_num_blocks_per_req, block_size,
+                                                                   max_num_kv_splits);
     if (need > kNoAllocScratchBytes) return VMC_ENOMEM;
     void* ws = nullptr;
     if (need > 0 && !(ws = noalloc_scratch_ptr())) return VMC_EIO;

@@ -97,8 +97,8 @@ __device__ __forceinline__ uint32_t g32_nib2(uint32_t w, int odd, bool hi, f16x2
     return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c, d2, m2));
 }
 
-// one 16-byte-per-lane load-to-LDS transfer, non-temporal: lane L's 16 bytes
-// from base + off land at LDS address m0 + 16 L.  Issued from asm, so the
+// one 16-byte-per-lane load-to-LDS transfer, an ordinary cached load: lane
+// L's 16 bytes from base + off land at LDS address m0 + 16 L.  Issued from asm, so the
 // compiler does not track it (it would make every later LDS read wait for
 // all transfers); the kernel counts its own transfers.
 __device__ __forceinline__ void dma16(const uint8_t* base, uint32_t off, uint32_t m0) {

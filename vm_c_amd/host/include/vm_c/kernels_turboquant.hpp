@@ -87,6 +87,12 @@ struct TQWorkspace {
     void ensure_decode(int batch_size, int num_heads, int num_kv_heads, int head_dim,
                        int64_t max_num_blocks_per_req, int64_t block_size,
                        int max_num_kv_splits, int gpu_device);
+    // the reference's form (kernels_turboquant.h:103; its callers
+    // attention_backend.cpp:129-132 and turboquant_kv_bridge.cpp:162-163):
+    // enough for bhq = batch x num_heads query rows with num_kv_splits splits
+    // each, at any context length -- a decode of that many rows allocates
+    // nothing.  head_dim other than 128 and num_kv_splits <= 1 need none.
+    void ensure_decode(int bhq, int head_dim, int num_kv_splits, int gpu_device);
     // turboquant_kernels.cu:704-741 grows four fp32 scratch buffers for its
     // multi-launch store; the fused HIP store needs none, so this only keeps
     // the reference's call sites compiling

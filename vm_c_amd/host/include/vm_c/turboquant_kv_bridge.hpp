@@ -95,6 +95,12 @@ public:
     // the layer's slot pool, or null for a layer without TurboQuant slots
     void* kv_cache_ptr(int layer) const;
 
+    // Device rows [2][capacity] (sequence, then position) for num_tokens
+    // query tokens of a step with prefill tokens; grown when a step needs
+    // more than reserve_decode set aside.
+    int32_t* token_rows(int num_tokens);
+    int token_rows_capacity() const { return rows_cap_; }
+
 private:
     KVCacheManager* kv_cache_mgr_ = nullptr;
     int gpu_device_ = 0;
@@ -109,6 +115,8 @@ private:
     TQWorkspace tq_workspace_;
 
     std::vector<void*> kv_ptrs_;
+    int32_t* d_rows_ = nullptr;
+    int rows_cap_ = 0;
 
     const int64_t* d_slot_mapping_ = nullptr;
     const int32_t* d_block_tables_ = nullptr;
@@ -133,6 +141,18 @@ private:
 // dst n_tokens x n_embd.  Throws std::runtime_error (null bridge, q width
 // other than num_attention_heads x head_dim, a layer without slots, no slot
 // mapping) before any launch, as the reference does.
+//
+// The attention reads the batch metadata as vm_c's Engine uploads it
+// (engine.cpp:653-793): block tables and sequence lengths per request.  A
+// decode-only step (is_prefill false) has one token per request and runs the
+// paged decode over num_reqs rows.  A step with prefill tokens gets one
+// (sequence, position) row per token (vmc_batch_token_rows: the prefill
+// tokens' token_to_seq / token_positions, each decode token's request and
+// seq_lens - 1) and runs the paged prefill attention over those rows.  (The
+// reference decodes num_tokens rows over the per-request arrays in every
+// step, reading past both whenever a step holds prefill tokens.)  Also
+// throws for a decode-only step whose token count differs from its request
+// count, and for a prefill step without token_to_seq / token_positions.
 void turboquant_attn_op(const void* op_params, const void* q, const int64_t q_ne[4], const size_t q_nb[4],
                         const void* k, const void* v, void* dst);
 

@@ -29,6 +29,19 @@ void q_layout(const int64_t ne[4], const size_t nb[4], int* n_embd, int* num_tok
 TurboQuantKvBridge::~TurboQuantKvBridge() {
     tq_buffers_.free_buf();
     tq_workspace_.free_buf();
+    if (d_rows_) (void)hipFree(d_rows_);
+}
+
+int32_t* TurboQuantKvBridge::token_rows(int num_tokens) {
+    if (num_tokens > rows_cap_) {
+        HIP_CHECK(hipSetDevice(gpu_device_));
+        if (d_rows_) HIP_CHECK(hipFree(d_rows_));
+        d_rows_ = nullptr;
+        rows_cap_ = 0;
+        HIP_CHECK(hipMalloc(&d_rows_, sizeof(int32_t) * 2 * (size_t)num_tokens));
+        rows_cap_ = num_tokens;
+    }
+    return d_rows_;
 }
 
 void TurboQuantKvBridge::initialize(const CacheConfig& cache, int num_attention_heads, int num_key_value_heads,
@@ -56,6 +69,9 @@ void TurboQuantKvBridge::initialize(const CacheConfig& cache, int num_attention_
         throw std::runtime_error("TurboQuantKvBridge::initialize: num_attention_heads per rank is zero");
     }
     tq_config_ = TQConfig::from_method(head_dim_, cache.kv_cache_quant_method.c_str(), gpu_device_);
+    // the reference sizes its decode workspace here (turboquant_kv_bridge.cpp:
+    // 162-163); this one allocates nothing until reserve_decode or the first
+    // node, so set-up stays free of device calls
     kv_ptrs_.assign(static_cast<size_t>(std::max(num_layers, 0)), nullptr);
     for (int l = 0; l < num_layers; ++l)
         if (kv_cache_mgr_->is_layer_turboquant(l)) kv_ptrs_[static_cast<size_t>(l)] = kv_cache_mgr_->key_cache_ptr(l);
@@ -94,6 +110,7 @@ void TurboQuantKvBridge::reserve_decode(int max_num_tokens, int64_t max_num_bloc
     tq_workspace_.ensure_decode(max_num_tokens, num_attention_heads_, num_kv_heads_, head_dim_,
                                 max_num_blocks_per_req, kv_cache_mgr_->block_size(),
                                 tq_config_.max_num_kv_splits, gpu_device_);
+    if (max_num_tokens > 0) token_rows(max_num_tokens);
 }
 
 void* TurboQuantKvBridge::kv_cache_ptr(int layer) const {
@@ -139,16 +156,45 @@ void turboquant_attn_op(const void* op_params, const void* q, const int64_t q_ne
     if (!slot_mapping) {
         throw std::runtime_error("ggml_vm_c_turboquant_attn: slot_mapping not set");
     }
+    // the batch metadata is checked before any launch
+    const int num_reqs = bridge->num_reqs();
+    const bool decode_only = !bridge->is_prefill();
+    if (decode_only && num_tokens != num_reqs) {
+        throw std::runtime_error("ggml_vm_c_turboquant_attn: decode step of " + std::to_string(num_tokens) +
+                                 " tokens over " + std::to_string(num_reqs) +
+                                 " requests (token_to_seq / token_positions are set only with prefill tokens)");
+    }
+    if (!decode_only && num_tokens > 0 &&
+        (!bridge->token_to_seq() || !bridge->token_positions() || !bridge->seq_lens() || num_reqs <= 0)) {
+        throw std::runtime_error("ggml_vm_c_turboquant_attn: prefill step without token_to_seq / token_positions");
+    }
     hipStream_t stream = bridge->stream();
     const ScalarType dtype = bridge->compute_dtype();
     turboquant_store(k, v, kv_cache, slot_mapping, num_tokens, num_kv_heads, head_dim, bridge->block_size(),
                      bridge->tq_config(), bridge->tq_buffers(), bridge->tq_workspace(), stream, dtype);
-    // every token a query row over its block-table row and sequence length
-    // (prefill, decode and speculative verification alike)
-    turboquant_decode_attention(dst, q, kv_cache, bridge->block_tables(), bridge->seq_lens(), num_tokens, num_heads,
-                                num_kv_heads, head_dim, kq_scale, bridge->block_size(),
-                                bridge->max_num_blocks_per_req(), bridge->tq_config(), bridge->tq_buffers(),
-                                bridge->tq_workspace(), bridge->tq_config().max_num_kv_splits, stream, dtype);
+    const int splits = bridge->tq_config().max_num_kv_splits;
+    if (decode_only) {
+        // token t is request t's one query row
+        turboquant_decode_attention(dst, q, kv_cache, bridge->block_tables(), bridge->seq_lens(), num_reqs,
+                                    num_heads, num_kv_heads, head_dim, kq_scale, bridge->block_size(),
+                                    bridge->max_num_blocks_per_req(), bridge->tq_config(), bridge->tq_buffers(),
+                                    bridge->tq_workspace(), splits, stream, dtype);
+        return;
+    }
+    // prefill or mixed step: one (sequence, position) row per token
+    if (num_tokens == 0) return;
+    int32_t* rows = bridge->token_rows(num_tokens);
+    int32_t* row_pos = rows + bridge->token_rows_capacity();
+    VMC_CALL(vmc_batch_token_rows(rows, row_pos, bridge->token_to_seq(), bridge->token_positions(),
+                                  bridge->seq_lens(), num_tokens, num_reqs, stream));
+    TQWorkspace& ws = bridge->tq_workspace();
+    ws.ensure_decode(num_tokens, num_heads, num_kv_heads, head_dim, bridge->max_num_blocks_per_req(),
+                     bridge->block_size(), splits, bridge->gpu_device());
+    const vmc_tq_config c = bridge->tq_config().to_c();
+    VMC_CALL(vmc_turboquant_prefill_attention(dst, q, kv_cache, bridge->block_tables(), rows, row_pos, num_tokens,
+                                              num_heads, num_kv_heads, head_dim, kq_scale, bridge->block_size(),
+                                              bridge->max_num_blocks_per_req(), &c, vmc_dtype_of(dtype), splits,
+                                              ws.decode_workspace, ws.decode_bytes, stream));
 }
 
 }  // namespace vm_c::official
