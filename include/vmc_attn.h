@@ -269,7 +269,7 @@ int vmc_turboquant_decode_attention(void* output, const void* query, const void*
 /*
  * vmc_turboquant_decode_attention without a workspace argument: the split
  * partials go to a device array inside the library (one per GPU, held until
- * the process ends, vmc_noalloc_scratch_bytes() = 24 MiB), so the call
+ * the process ends, vmc_noalloc_scratch_bytes() = 64 MiB), so the call
  * allocates nothing -- no hipMalloc, hipFree or allocating library routine --
  * and records no memset.  No counterpart in the reference: for callers that
  * cannot allocate (code under HIP graph capture, serving loops, harnesses that

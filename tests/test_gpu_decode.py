@@ -269,6 +269,51 @@ def test_tq_decode_bf16(dev, method, case, max_splits):
     assert ok, f"vs reference restatement: max err {err}"
 
 
+@pytest.mark.parametrize("method", ["turboquant_4bit_nc", "turboquant_3bit_nc"])
+@pytest.mark.parametrize("heads", [(64, 8), (16, 4), (32, 2)])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_tq_decode_large_value_scales(dev, method, heads, bf16):
+    """V of magnitude ~2000 (value scales of ~300-2000 per token) with peaked
+    scores (q x 3): P enters the PV product as fp16(P * scale), and with the
+    lazy running max P reaches 2^8, so these pages must take the exact max
+    (P <= 1) or the product overflows to inf.  Output against fp64 attention
+    over the stored pages, with the absolute tolerance scaled to the values:
+    the fp16 P * scale operand carries 11 bits relative to the value range
+    (up to ~9 sigma), so a dominant token contributes up to 2^-11 * 9 sigma
+    ~ 0.0044 sigma of error; atol = 5e-3 * 2000.  Heads (64, 8) run the 3-bit
+    streaming kernel, (16, 4) the pipelined kernel, (32, 2) the
+    16-heads-per-page kernel."""
+    import torch
+    from kvgen import f32_to_bf16_bits
+    from vm_c_amd import capi
+    Hq, Hkv = heads
+    w = make_workload([1500, 37, 4000], Hq=Hq, Hkv=Hkv, seed=Hq + Hkv + (5 if bf16 else 0))
+    V = w.V.astype(np.float32) * 2000.0
+    Q = w.Q.astype(np.float32) * 3.0
+    L = O.tq_layout(method)
+    cfg = capi.tq_config(w.D, method)
+    cache = torch.zeros(w.num_blocks * BS * w.Hkv * cfg.slot_size_aligned, dtype=torch.uint8, device=dev)
+    if bf16:
+        kb, vb, qb = (f32_to_bf16_bits(x.astype(np.float32)) for x in (w.K, V, Q))
+        conv = lambda b: torch.from_numpy(b.view(np.int16)).to(dev).view(torch.bfloat16)
+    else:
+        kb, vb, qb = (x.astype(np.float16).view(np.uint16) for x in (w.K, V, Q))
+        conv = lambda b: torch.from_numpy(b.view(np.float16)).to(dev)
+    capi.turboquant_store(conv(kb), conv(vb), cache, torch.from_numpy(w.slots).to(dev), BS, cfg)
+    q = conv(qb)
+    out = torch.full_like(q, float("nan"))
+    capi.turboquant_decode_attention(out, q, cache, torch.from_numpy(w.bt).to(dev),
+                                     torch.from_numpy(w.seq_lens).to(dev), w.Hkv, float(w.scale), cfg,
+                                     block_size=BS)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all(), "non-finite decode rows with large value scales"
+    c, _ = O.tq_tables(128, L.key_quant_bits)
+    ex = O.tq_decode_exact(qb, cache.cpu().numpy(), w.bt, w.seq_lens, w.Hkv, w.scale, BS, L, c, bf16=bf16)
+    ok, err = close_report(got, ex, 5e-3 * 2000.0, RTOL)
+    assert ok, f"vs exact: max err {err}"
+
+
 @pytest.mark.parametrize("heads", [(8, 8), (16, 8), (32, 8), (64, 8), (12, 4)])
 def test_tq_decode_workspace_contents_do_not_matter(dev, heads):
     """The split decode keeps no state in the workspace between calls: every

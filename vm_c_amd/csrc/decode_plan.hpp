@@ -388,9 +388,24 @@ inline int tq_ranges(int B, int Hkv, int max_blocks, int max_splits, int cus) {
     return (int)std::max<int64_t>(1, n);
 }
 
+// Page ranges of the streaming TurboQuant decode (tq_stream.hip): two
+// resident workgroups per CU, one per range (every KV head of its pages);
+// fewer for small batches
+inline int tq_stream_ranges(int B, int Hkv, int max_blocks, int max_splits, int cus) {
+    (void)Hkv;
+    int64_t n = std::max<int64_t>(1, (int64_t)cus * 2);
+    n = std::min<int64_t>(n, ((int64_t)B * max_blocks + kPpsMin - 1) / kPpsMin);
+    if (max_splits > 1) n = std::min<int64_t>(n, (int64_t)B * max_splits);
+    return (int)std::max<int64_t>(1, n);
+}
+
+// split partials: two rows per page range of the largest grid any decode
+// kernel launches for the shape
 inline size_t workspace_bytes_for(int B, int Hq, int Hkv, int max_blocks, int max_splits, int cus) {
     if (max_splits == 1) return 0;
-    return (size_t)2 * flat_grid(B, Hkv, max_blocks, max_splits, cus) * Hq * (kD + 2) * sizeof(float);
+    const int n = std::max(flat_grid(B, Hkv, max_blocks, max_splits, cus),
+                           tq_stream_ranges(B, Hkv, max_blocks, max_splits, cus));
+    return (size_t)2 * n * Hq * (kD + 2) * sizeof(float);
 }
 
 // The pipelined TurboQuant decode (tq_decode.hip): reference slot layout,
@@ -399,5 +414,8 @@ int launch_tq_decode_any(DecodeParams& prm, int key_bits, int value_bits, bool b
 // The per-32-group variant (fp16, 3- or 4-bit codes) on the same kernel;
 // VMC_EINVAL for shapes it does not take.
 int launch_g32_decode(DecodeParams& prm, int bits, hipStream_t stream);
+// The streaming TurboQuant decode (tq_stream.hip): reference slot layout,
+// 8 KV heads, at most 8 query heads per KV head; VMC_EINVAL for other shapes.
+int launch_tq_stream_any(DecodeParams& prm, int key_bits, int value_bits, bool bf16, hipStream_t stream);
 
 }  // namespace vmc

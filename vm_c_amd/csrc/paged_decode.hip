@@ -741,13 +741,26 @@ paged_decode_kernel(DecodeParams p) {
         // rescale.  Every term of l, z and O uses the same reference: exact.
         // The cross-group max is taken only when some lane's own max passes
         // the threshold.
+        // P enters the PV product as fp16(p * scale), so p <= 256 needs every
+        // value scale <= 65504 / 256: a step whose largest scale is above that
+        // takes the exact running max instead (p <= 1; in range for any fp16
+        // scale)
+        float scf[2][4];
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp)
+#pragma unroll
+            for (int i2 = 0; i2 < 4; ++i2) scf[pp][i2] = half_to_f32<kTqBf16>(vsc[pp][i2]);
+        const float smax = vmax(vmax(vmax(scf[0][0], scf[0][1]), vmax(scf[0][2], scf[0][3])),
+                                vmax(vmax(scf[1][0], scf[1][1]), vmax(scf[1][2], scf[1][3])));
+        const bool exact = __ballot(smax > 255.875f) != 0;  // wave-uniform, rare
+        const float thr = exact ? m_run : m_thr;
         const float mloc = vmax(vmax(vmax(sv[0][0], sv[0][1]), vmax(sv[0][2], sv[0][3])),
                                 vmax(vmax(sv[1][0], sv[1][1]), vmax(sv[1][2], sv[1][3])));
-        if (__ballot(mloc > m_thr)) {  // wave-uniform
+        if (__ballot(mloc > thr)) {  // wave-uniform
             const float mx = vmax_over_groups(mloc);
-            const bool upd = mx > m_thr;  // the same in every lane of head r16
-            const float m_new = upd ? mx : m_run;
-            const float alpha = upd ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;  // 0 when m_run = -inf
+            const bool upd = mx > thr;  // the same in every lane of head r16
+            const float m_new = upd ? vmax(mx, m_run) : m_run;
+            const float alpha = m_new > m_run ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;  // 0 when m_run = -inf
             l_part *= alpha;
             z_part *= alpha;
             const f32x4 al = gather4_from_row0(alpha, wscr + 64, r16, grp);
@@ -766,11 +779,10 @@ paged_decode_kernel(DecodeParams p) {
 #pragma unroll
             for (int i2 = 0; i2 < 4; ++i2) {
                 const float pv = __builtin_amdgcn_exp2f(sv[pp][i2] - m_use);
-                const float sc = half_to_f32<kTqBf16>(vsc[pp][i2]);
                 const float zr = half_to_f32<kTqBf16>(vzr[pp][i2]);
                 psum += pv;
                 zsum = __builtin_fmaf(pv, zr, zsum);
-                pa[4 * pp + i2] = (_Float16)__builtin_fmaf(pv, sc, 0.0f);
+                pa[4 * pp + i2] = (_Float16)__builtin_fmaf(pv, scf[pp][i2], 0.0f);
             }
         l_part += psum;
         z_part += zsum;
@@ -1521,7 +1533,11 @@ namespace {
 // per S tile
 template <bool BF>
 int launch_tq(DecodeParams& prm, int kb, int vb, bool half, hipStream_t s) {
-    if (half) return launch_tq_decode_any(prm, kb, vb, BF, s);
+    if (half) {
+        const int rc = launch_tq_stream_any(prm, kb, vb, BF, s);
+        if (rc != VMC_EINVAL) return rc;
+        return launch_tq_decode_any(prm, kb, vb, BF, s);
+    }
     if (kb == 4 && vb == 4) return launch_decode<FMT_TQ, 4, 4, BF>(prm, s);
     if (kb == 3 && vb == 3) return launch_decode<FMT_TQ, 3, 3, BF>(prm, s);
     if (kb == 3 && vb == 4) return launch_decode<FMT_TQ, 3, 4, BF>(prm, s);
@@ -1693,7 +1709,7 @@ extern "C" int vmc_turboquant_decode_attention(void* output, const void* query, 
 // same call's split pass wrote.  Calls that overlap on one device share the
 // array and race.
 namespace {
-constexpr size_t kNoAllocScratchBytes = size_t{24} << 20;  // 24 MiB per device
+constexpr size_t kNoAllocScratchBytes = size_t{64} << 20;  // 64 MiB per device
 __device__ __align__(256) unsigned char noalloc_scratch[kNoAllocScratchBytes];
 
 void* noalloc_scratch_ptr() {

@@ -1,6 +1,7 @@
 // tq_decode.hip -- split-KV paged decode over TurboQuant slots, gfx950:
-// the reference layout (turboquant_4bit_nc / 3bit_nc / k3v4_nc) with at most
-// 8 query heads per KV head, and (G32) the per-32-group variant of the same
+// the reference layout (turboquant_4bit_nc / k3v4_nc, and 3bit_nc with other
+// than 8 KV heads -- tq_stream.hip takes 3-bit slots with 8) with at most 8
+// query heads per KV head, and (G32) the per-32-group variant of the same
 // slots (turboquant_4bit_g32 / 3bit_g32; its format is defined in
 // vmc_attn.h, the reference has no code for it).
 //
@@ -739,14 +740,22 @@ __global__ void __launch_bounds__(512) tq_decode_kernel(DecodeParams p) {
             }
         }
         // lazy reference max: m_run moves only when a head's max passes it by
-        // more than 8 (log2 units); a head's max spans columns c, c ^ 8
+        // more than 8 (log2 units), so P <= 2^8; when a value scale of the pair
+        // exceeds 65504 / 2^8 the max is taken exactly (P <= 1), so that
+        // fp16(P * scale) cannot overflow.  A head's max spans columns c, c ^ 8
+        float scf[4];
+#pragma unroll
+        for (int i2 = 0; i2 < 4; ++i2) scf[i2] = half_to_f32<BF>((uint16_t)(hsz[i2] & 0xffffu));
+        const float smax = vmax(vmax(scf[0], scf[1]), vmax(scf[2], scf[3]));
+        const bool exact = __ballot(smax > 255.875f) != 0;  // wave-uniform, rare
+        const float thr = exact ? m_run : m_thr;
         const float mloc = vmax(vmax(sv[0], sv[1]), vmax(sv[2], sv[3]));
-        if (__ballot(mloc > m_thr)) {
+        if (__ballot(mloc > thr)) {
             float mx = vmax_over_groups(mloc);
             mx = vmax(mx, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, mx), 0x128, 0xf, 0xf, false)));
-            const bool upd = mx > m_thr;
-            const float m_new = upd ? mx : m_run;
-            const float alpha = upd ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+            const bool upd = mx > thr;
+            const float m_new = upd ? vmax(mx, m_run) : m_run;
+            const float alpha = m_new > m_run ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
             l_part *= alpha;
             z_part *= alpha;
             const f32x4 al = gather4_from_row0(alpha, wscr + 64, r16, grp);
@@ -765,7 +774,7 @@ __global__ void __launch_bounds__(512) tq_decode_kernel(DecodeParams p) {
             const float pv = __builtin_amdgcn_exp2f(sv[i2] - m_use);
             psum += pv;
             zsum = __builtin_fmaf(pv, half_to_f32<BF>((uint16_t)(hsz[i2] >> 16)), zsum);
-            pw[i2] = (_Float16)__builtin_fmaf(pv, half_to_f32<BF>((uint16_t)(hsz[i2] & 0xffffu)), 0.0f);
+            pw[i2] = (_Float16)__builtin_fmaf(pv, scf[i2], 0.0f);
         }
         l_part += psum;
         z_part += zsum;
