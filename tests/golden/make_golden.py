@@ -22,12 +22,14 @@ Fixtures
   fa_decode_q8_0.npz, fa_decode_q4_0.npz
       same operator over q8_0 / q4_0 K/V rows encoded by the reference's own
       quantizer: batch 16, 32/8 heads, lengths uniform in [512, 4096]
-      (seed 1); outputs of the first 4 sequences.
+      (seed 1); outputs of all 16 sequences.
   fa_prefill_bf16.npz
       causal prefill rows of the bf16 batch-4 x 4096-token workload (32/8
-      heads, seed 3), sampled (token, head) pairs; each row is the operator
-      on that token's causal prefix (the bf16 K/V path evaluates every query
-      row independently, ops.cpp:8895-8934 -> one_chunk).
+      heads, seed 3): every head of the first and last 4 rows of each
+      sequence, rows at 64-key tile and page edges, random (token, head)
+      pairs (1,280 rows); each row is the operator on that token's causal
+      prefix (the bf16 K/V path evaluates every query row independently,
+      ops.cpp:8895-8934 -> one_chunk).
   tq_tables_d128.json
       TurboQuant codebooks of the restated Lloyd-Max solver (not a reference
       run: the reference computes them in its CUDA host code).
@@ -120,7 +122,7 @@ def gen_decode_single(fmt, name):
     print(f"{name}: |nth1 - nth4| max {np.abs(o1 - o4).max():.3e}")
 
 
-def gen_decode_batched(fmt, name, nseq=4):
+def gen_decode_batched(fmt, name, nseq=16):
     w = kvgen.batched_q8_0_workload()
     o = _ref_decode(w, fmt, list(range(nseq)), 8)
     np.savez(os.path.join(HERE, name), out=o, seqs=np.arange(nseq), seq_lens=w.seq_lens,
@@ -132,14 +134,23 @@ PREFILL = dict(seq_lens=[4096] * 4, Hq=32, Hkv=8, seed=3)
 
 
 def prefill_rows():
-    """(token, head) pairs sampled from the batch-4 x 4096 prefill."""
+    """(token, head) pairs of the batch-4 x 4096 prefill: every head of the
+    first and last 4 rows of each sequence, rows on both sides of 64-key tile
+    edges and page edges (4 heads each), and 64 random pairs."""
     rng = np.random.default_rng(5)
-    T = 4 * 4096
-    toks = np.concatenate([[0, 1, 15, 16, 17, 4095, 4096, 4097, 8191, T - 1],
-                           rng.integers(0, T, 30)]).astype(np.int64)
-    heads = np.concatenate([[0, 31, 5, 8, 9, 30, 0, 7, 16, 31],
-                            rng.integers(0, 32, 30)]).astype(np.int32)
-    return toks, heads
+    S, Hq = 4096, 32
+    toks, heads = [], []
+    for b in range(4):
+        for p in list(range(4)) + list(range(S - 4, S)):
+            toks += [b * S + p] * Hq
+            heads += list(range(Hq))
+        for p in (15, 16, 63, 64, 65, 127, 128, 1023, 1024, 2047, 2048, 3071):
+            hs = rng.choice(Hq, 4, replace=False)
+            toks += [b * S + p] * 4
+            heads += hs.tolist()
+    toks += rng.integers(0, 4 * S, 64).tolist()
+    heads += rng.integers(0, Hq, 64).tolist()
+    return np.array(toks, np.int64), np.array(heads, np.int32)
 
 
 def gen_prefill(name):

@@ -81,8 +81,9 @@ def test_prefill_fused_append_bitexact(dev, fmt):
 
 def test_prefill_config4_full_size(dev):
     """B=4, S=4096, Hq=32, Hkv=8, bf16, causal, fused q8_0 append (seed 3):
-    sampled rows vs the reference's output (golden fixture) and exact fp64,
-    every page byte vs the oracle's append."""
+    1,280 rows vs the reference's output (golden fixture: every head of the
+    first and last 4 rows of each sequence, tile and page edges), 8,256 rows
+    vs exact fp64, every page byte vs the oracle's append."""
     seq_lens, Hq, Hkv = [4096] * 4, 32, 8
     qb, kb, vb, pos, cu = _inputs(seq_lens, Hq, Hkv, seed=3)
     T = qb.shape[0]
@@ -91,9 +92,12 @@ def test_prefill_config4_full_size(dev):
     nbytes = nblk * BS * Hkv * E
     scale = 1.0 / np.sqrt(128)
     got, kc, vc = _run(dev, qb, kb, vb, pos, Hkv, scale, append=(O.KV_Q8_0, slots, nbytes))
+    # 8,256 rows against fp64 attention: every head of 256 random tokens and
+    # of the first and last token of each sequence
     rng = np.random.default_rng(0)
-    toks = np.concatenate([rng.integers(0, T, 96), [0, 4095, 4096, T - 1, 127, 128]])
-    heads = rng.integers(0, Hq, toks.size)
+    pick = np.concatenate([rng.integers(0, T, 256), [0, 4095, 4096, 8191, 8192, 12287, 12288, T - 1]])
+    toks = np.repeat(pick, Hq)
+    heads = np.tile(np.arange(Hq), pick.size)
     ex = O.prefill_exact_rows(qb, kb, vb, cu, Hkv, scale, toks, heads)
     ok, err = close_report(got[toks, heads], ex, ATOL, RTOL)
     assert ok, f"max err {err}"
