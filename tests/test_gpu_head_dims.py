@@ -165,3 +165,80 @@ def test_local_prefill_with_append(dev, d, bf16):
     vr = np.zeros(n, np.uint8)
     O.kv_append(kb, vb, slots, kr, vr, BS, O.KV_Q8_0, src_bf16=bf16)
     assert np.array_equal(kc.cpu().numpy(), kr) and np.array_equal(vc.cpu().numpy(), vr)
+
+
+# head_dim 256 over 3- and 4-bit slots runs the MFMA decode of
+# tq_decode_d256.hip (1, 2 or 4 KV heads, at most 8 query heads per KV head):
+# the reference's deployment shape (16 query / 2 KV heads, 262-byte slots),
+# the other head groupings, split counts that exercise the merge (0 = as
+# many ranges as the GPU holds, 3) and the per-sequence mode (1), ragged
+# lengths with an empty sequence, a one-token one, page-edge lengths and a
+# block-table hole
+@pytest.mark.parametrize("method", ["turboquant_4bit_nc", "turboquant_3bit_nc"])
+@pytest.mark.parametrize("heads", [(16, 2), (8, 1), (32, 4), (4, 4), (3, 1)])
+@pytest.mark.parametrize("splits", [0, 1, 3])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_tq_d256_decode(dev, method, heads, splits, bf16):
+    import torch
+    from vm_c_amd import capi
+    d = 256
+    Hq, Hkv = heads
+    lens = np.array([1, 700, 0, 16, 33, 1024, 5, 257], np.int32)
+    w = make_workload(lens, Hq=Hq, Hkv=Hkv, D=d, seed=300 + Hq + Hkv + splits, holes=1)
+    cfg = capi.tq_config(d, method)
+    L = O.tq_layout(method, d)
+    c, m = O.tq_tables(d, L.key_quant_bits)
+    kb, vb, qb = _bits(w.K, bf16), _bits(w.V, bf16), _bits(w.Q, bf16)
+    n = w.num_blocks * BS * Hkv * cfg.slot_size_aligned
+    cache = torch.zeros(n, dtype=torch.uint8, device=dev)
+    capi.turboquant_store(_dev(dev, kb, bf16), _dev(dev, vb, bf16), cache, torch.from_numpy(w.slots).to(dev),
+                          BS, cfg)
+    out = torch.full((len(lens), Hq, d), float("nan"), dtype=torch.bfloat16 if bf16 else torch.float16,
+                     device=dev)
+    print(f"d256 decode {method} Hq={Hq} Hkv={Hkv} splits={splits} bf16={bf16}", flush=True)
+    capi.turboquant_decode_attention(out, _dev(dev, qb, bf16), cache, torch.from_numpy(w.bt).to(dev),
+                                     torch.from_numpy(lens).to(dev), Hkv, float(w.scale), cfg, max_splits=splits)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    pool = cache.cpu().numpy()
+    two = _f32(O.tq_decode(qb, pool, w.bt, lens, Hkv, np.float32(w.scale), BS, L, c, bf16=bf16), bf16)
+    ok, err = close_report(got, two, ATOL, RTOL)
+    assert ok, f"decode vs two-stage: {err}"
+    ex = O.tq_decode_exact(qb, pool, w.bt, lens, Hkv, w.scale, BS, L, c, bf16=bf16)
+    ok, err = close_report(got, ex, ATOL, RTOL)
+    assert ok, f"decode vs exact: {err}"
+    assert (got[2] == 0).all()  # the empty sequence
+
+
+@pytest.mark.parametrize("method", ["turboquant_4bit_nc", "turboquant_3bit_nc"])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_tq_d256_large_value_scales(dev, method, bf16):
+    """V of magnitude ~2000 with peaked scores (q x 3): pages whose value
+    scale exceeds 65504 / 2^8 take the exact running max, so fp16(P * scale)
+    stays finite; against fp64 attention with atol 5e-3 * 2000 (the fp16
+    P * scale operand's 11 bits against values of up to ~9 sigma)."""
+    import torch
+    from vm_c_amd import capi
+    d, Hq, Hkv = 256, 16, 2
+    lens = np.array([900, 37, 1600], np.int32)
+    w = make_workload(lens, Hq=Hq, Hkv=Hkv, D=d, seed=17 + bf16)
+    V = w.V.astype(np.float32) * 2000.0
+    Q = w.Q.astype(np.float32) * 3.0
+    cfg = capi.tq_config(d, method)
+    L = O.tq_layout(method, d)
+    c, _ = O.tq_tables(d, L.key_quant_bits)
+    kb, vb, qb = _bits(w.K, bf16), _bits(V, bf16), _bits(Q, bf16)
+    cache = torch.zeros(w.num_blocks * BS * Hkv * cfg.slot_size_aligned, dtype=torch.uint8, device=dev)
+    capi.turboquant_store(_dev(dev, kb, bf16), _dev(dev, vb, bf16), cache, torch.from_numpy(w.slots).to(dev),
+                          BS, cfg)
+    out = torch.full((len(lens), Hq, d), float("nan"), dtype=torch.bfloat16 if bf16 else torch.float16,
+                     device=dev)
+    print(f"d256 large value scales {method} bf16={bf16}", flush=True)
+    capi.turboquant_decode_attention(out, _dev(dev, qb, bf16), cache, torch.from_numpy(w.bt).to(dev),
+                                     torch.from_numpy(lens).to(dev), Hkv, float(w.scale), cfg)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all(), "non-finite decode rows with large value scales"
+    ex = O.tq_decode_exact(qb, cache.cpu().numpy(), w.bt, lens, Hkv, w.scale, BS, L, c, bf16=bf16)
+    ok, err = close_report(got, ex, 5e-3 * 2000.0, RTOL)
+    assert ok, f"vs exact: {err}"

@@ -399,6 +399,24 @@ inline int tq_stream_ranges(int B, int Hkv, int max_blocks, int max_splits, int 
     return (int)std::max<int64_t>(1, n);
 }
 
+// Page ranges of the head_dim-256 TurboQuant decode (tq_decode_d256.hip):
+// workgroups of 4 / Hkv ranges (one per group of Hkv waves), two resident
+// per CU; fewer for small batches (the last workgroup's surplus streams idle)
+inline int d256_ranges(int B, int Hkv, int max_blocks, int max_splits, int cus) {
+    const int ns = std::max(1, 4 / Hkv);
+    int64_t n = (int64_t)cus * 2 * ns;
+    n = std::min<int64_t>(n, ((int64_t)B * max_blocks + kPpsMin - 1) / kPpsMin);
+    if (max_splits > 1) n = std::min<int64_t>(n, (int64_t)B * max_splits);
+    return (int)std::max<int64_t>(1, n);
+}
+
+// split partials of the head_dim-256 TurboQuant decode: two rows of 256 + 2
+// floats per page range
+inline size_t workspace_bytes_d256(int B, int Hq, int Hkv, int max_blocks, int max_splits, int cus) {
+    if (max_splits == 1) return 0;
+    return (size_t)2 * d256_ranges(B, Hkv, max_blocks, max_splits, cus) * Hq * (256 + 2) * sizeof(float);
+}
+
 // split partials: two rows per page range of the largest grid any decode
 // kernel launches for the shape
 inline size_t workspace_bytes_for(int B, int Hq, int Hkv, int max_blocks, int max_splits, int cus) {
@@ -417,5 +435,9 @@ int launch_g32_decode(DecodeParams& prm, int bits, hipStream_t stream);
 // The streaming TurboQuant decode (tq_stream.hip): reference slot layout,
 // 8 KV heads, at most 8 query heads per KV head; VMC_EINVAL for other shapes.
 int launch_tq_stream_any(DecodeParams& prm, int key_bits, int value_bits, bool bf16, hipStream_t stream);
+// The head_dim-256 TurboQuant decode (tq_decode_d256.hip): reference slot
+// layout, equal key and value bits (3 or 4), 1, 2 or 4 KV heads, at most 8
+// query heads per KV head; VMC_EINVAL for other shapes.
+int launch_tq_decode_d256(DecodeParams& prm, int bits, bool bf16, hipStream_t stream);
 
 }  // namespace vmc

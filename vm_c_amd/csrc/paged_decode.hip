@@ -1411,9 +1411,14 @@ extern "C" size_t vmc_paged_decode_workspace_size(int batch_size, int num_heads,
 extern "C" size_t vmc_turboquant_decode_workspace_size(int batch_size, int num_heads, int num_kv_heads,
                                                        int head_dim, int64_t max_num_blocks_per_req,
                                                        int64_t block_size, int max_num_kv_splits) {
-    return vmc_paged_decode_workspace_size(batch_size, num_heads, num_kv_heads, head_dim,
-                                           (int)std::min<int64_t>(max_num_blocks_per_req, 0x7fffffff),
-                                           (int)block_size, max_num_kv_splits);
+    const int mb = (int)std::min<int64_t>(max_num_blocks_per_req, 0x7fffffff);
+    const size_t n = vmc_paged_decode_workspace_size(batch_size, num_heads, num_kv_heads, head_dim, mb,
+                                                     (int)block_size, max_num_kv_splits);
+    // head_dim 256 (tq_decode_d256.hip): rows of 256 + 2 floats
+    if (head_dim == 256 && batch_size >= 0 && num_heads > 0 && num_kv_heads > 0 && mb > 0)
+        return std::max(n, workspace_bytes_d256(batch_size, num_heads, num_kv_heads, mb, max_num_kv_splits,
+                                                num_cus()));
+    return n;
 }
 
 namespace {
@@ -1552,6 +1557,62 @@ bool tq_generic_route(const vmc_tq_config* cfg, int head_dim, int num_heads, int
            beyond_tuned_decode(head_dim, num_heads, num_kv_heads);
 }
 
+// head_dim 256 over reference-layout slots with equal key and value bits (3
+// or 4), 1, 2 or 4 KV heads and at most 8 query heads per KV head -- the
+// reference's deployment of this size, 262-byte slots with 16 query / 2 KV
+// heads (src/distributed/tp_runtime.cpp:257-261) -- with q, out and the pool
+// 16-byte aligned: the MFMA decode of tq_decode_d256.hip
+bool tq_d256_route(const vmc_tq_config* cfg, int head_dim, int num_heads, int num_kv_heads, int64_t block_size,
+                   const void* q, const void* out, const void* pool) {
+    return head_dim == 256 && cfg->group_size == 0 && !cfg->key_fp8 &&
+           cfg->key_quant_bits == cfg->value_quant_bits &&
+           (cfg->key_quant_bits == 3 || cfg->key_quant_bits == 4) && block_size == kBs &&
+           (num_kv_heads == 1 || num_kv_heads == 2 || num_kv_heads == 4) && num_heads > 0 &&
+           num_heads % num_kv_heads == 0 && num_heads / num_kv_heads <= 8 &&
+           (((uintptr_t)q | (uintptr_t)out | (uintptr_t)pool) & 15) == 0;
+}
+
+int tq_d256_rows(void* output, const void* query, const void* kv_cache, const int32_t* block_tables,
+                 const int32_t* seq_lens, const int32_t* row_seq, const int32_t* row_pos, int batch_size,
+                 int num_heads, int num_kv_heads, float scale, int64_t max_num_blocks_per_req,
+                 const vmc_tq_config* cfg, int half_dtype, int max_num_kv_splits, void* workspace,
+                 size_t workspace_bytes, vmc_stream_t stream) {
+    if (batch_size < 0 || max_num_blocks_per_req <= 0 || batch_size > (1 << 24)) return VMC_EINVAL;
+    if (batch_size == 0) return VMC_OK;
+    if (!output || !query || !kv_cache || !block_tables || !seq_lens) return VMC_EINVAL;
+    const int mb = (int)max_num_blocks_per_req;
+    const size_t need = workspace_bytes_d256(batch_size, num_heads, num_kv_heads, mb, max_num_kv_splits, num_cus());
+    if (need > 0 && (!workspace || workspace_bytes < need)) return workspace ? VMC_ENOMEM : VMC_EINVAL;
+    DecodeParams prm = {};
+    prm.out = output;
+    prm.q = reinterpret_cast<const uint16_t*>(query);
+    prm.bt = block_tables;
+    prm.seq_lens = seq_lens;
+    prm.row_seq = row_seq;
+    prm.row_pos = row_pos;
+    prm.B = batch_size;
+    prm.Hq = num_heads;
+    prm.Hkv = num_kv_heads;
+    prm.G = num_heads / num_kv_heads;
+    prm.max_blocks = mb;
+    prm.scale_log2 = scale * kLog2e;
+    prm.part = reinterpret_cast<float*>(workspace);
+    prm.per_seq = max_num_kv_splits == 1;
+    prm.pps_min = kPpsMin;
+    prm.max_splits = max_num_kv_splits;
+    prm.kc = reinterpret_cast<const uint8_t*>(kv_cache);
+    prm.vc = prm.kc;
+    prm.q_bf16 = half_dtype == VMC_DTYPE_BF16 ? 1 : 0;
+    prm.entry_bytes = cfg->slot_size_aligned;
+    prm.page_bytes = (int64_t)kBs * num_kv_heads * cfg->slot_size_aligned;
+    prm.mse_bytes = cfg->mse_bytes;
+    prm.key_packed = cfg->key_packed_size;
+    prm.val_data = cfg->val_data_bytes;
+    prm.norm_corr = cfg->norm_correction != 0;
+    prm.tab = tq_tables(256, cfg->key_quant_bits);
+    return launch_tq_decode_d256(prm, cfg->key_quant_bits, prm.q_bf16 != 0, reinterpret_cast<hipStream_t>(stream));
+}
+
 int tq_decode_rows(void* output, const void* query, const void* kv_cache, const int32_t* block_tables,
                    const int32_t* seq_lens, const int32_t* row_seq, const int32_t* row_pos, int batch_size,
                    int num_heads, int num_kv_heads, int head_dim, float scale, int64_t block_size,
@@ -1560,6 +1621,10 @@ int tq_decode_rows(void* output, const void* query, const void* kv_cache, const 
     if (!tq_config_valid(cfg) || cfg->head_dim != head_dim) return VMC_EINVAL;
     if (half_dtype != VMC_DTYPE_F16 && half_dtype != VMC_DTYPE_BF16) return VMC_EINVAL;
     if (max_num_blocks_per_req > 0x7fffffff) return VMC_EINVAL;
+    if (tq_d256_route(cfg, head_dim, num_heads, num_kv_heads, block_size, query, output, kv_cache))
+        return tq_d256_rows(output, query, kv_cache, block_tables, seq_lens, row_seq, row_pos, batch_size, num_heads,
+                            num_kv_heads, scale, max_num_blocks_per_req, cfg, half_dtype, max_num_kv_splits, workspace,
+                            workspace_bytes, stream);
     if (tq_generic_route(cfg, head_dim, num_heads, num_kv_heads, half_dtype)) {
         // head_dim 64 / 256, fp8 keys with bf16 halves, and head counts past
         // the tuned kernels': one wave per (row, query head), no workspace;
@@ -1737,7 +1802,8 @@ extern "C" int vmc_turboquant_decode_attention_noalloc(
     if (num_heads <= 0 || num_kv_heads <= 0 || batch_size < 0) return VMC_EINVAL;
     if (!tq_config_valid(cfg) || cfg->head_dim != head_dim) return VMC_EINVAL;
     // the shapes of the one-wave-per-row kernel need no split partials
-    const size_t need = tq_generic_route(cfg, head_dim, num_heads, num_kv_heads, half_dtype)
+    const bool d256 = tq_d256_route(cfg, head_dim, num_heads, num_kv_heads, block_size, query, output, kv_cache);
+    const size_t need = !d256 && tq_generic_route(cfg, head_dim, num_heads, num_kv_heads, half_dtype)
                             ? 0
                             : vmc_turboquant_decode_workspace_size(batch_size, num_heads, num_kv_heads, head_dim,
                                                                    max_num_blocks_per_req, block_size,

@@ -173,7 +173,7 @@ void TQWorkspace::ensure_decode(int bhq, int head_dim, int num_kv_splits, int de
     // the decode's split partials are fp32 rows of head_dim + 2 floats, at
     // most two per launched workgroup and query head, with at most
     // batch x num_kv_splits workgroups (vmc_turboquant_decode_workspace_size)
-    if (bhq <= 0 || num_kv_splits <= 1 || head_dim != 128) return;
+    if (bhq <= 0 || num_kv_splits <= 1 || (head_dim != 128 && head_dim != 256)) return;
     const size_t need = (size_t)2 * (size_t)num_kv_splits * (size_t)bhq * (size_t)(head_dim + 2) * sizeof(float);
     if (need <= decode_bytes) return;
     HIP_CHECK(hipSetDevice(device));
