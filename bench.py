@@ -52,6 +52,7 @@ HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 BS = 16
 D = 128
+HEAD_DIM = D
 
 
 def log(*a):
@@ -79,20 +80,30 @@ def decode_workload():
 
 
 def time_loop(torch, fn, n, warm, stream):
-    """`warm` untimed calls, then `n` timed ones with a HIP event after each
-    on `stream` (the stream the kernels run on); returns (mean ms over the
-    timed region, median ms of the individual calls)."""
+    """`warm` untimed calls, then `n` back-to-back timed calls between two HIP
+    events on `stream` (the stream the kernels run on): the mean ms per call
+    over that region; then `n` more calls with an event after each, for the
+    median ms of one call.  (An event between calls is a full release on this
+    runtime: it adds several microseconds to every call it follows, so it
+    stays out of the mean.)  Returns (mean, median)."""
     for i in range(warm):
         fn(i)
     torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(n):
+        fn(warm + i)
+    e1.record(stream)
+    e1.synchronize()
+    mean = e0.elapsed_time(e1) / n
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
     ev[0].record(stream)
     for i in range(n):
-        fn(warm + i)
+        fn(warm + n + i)
         ev[i + 1].record(stream)
     ev[n].synchronize()
     per = [ev[i].elapsed_time(ev[i + 1]) for i in range(n)]
-    return ev[0].elapsed_time(ev[n]) / n, float(np.median(per))
+    return mean, float(np.median(per))
 
 
 def slots_for(bt, lens, positions_of):
@@ -177,6 +188,8 @@ DECODE_CFGS = {
     "tq4_32x8192": (2, 32, 32, 8, "8192", "turboquant_4bit_nc"),
     "g32_4bit_32x8192": (2, 32, 32, 8, "8192", "turboquant_4bit_g32"),
     "q8_0_batch16": (1, 16, 32, 8, "u512_4096", "q8_0"),
+    # (head_dim 256: the 16 / 2-head, 262-byte-slot deployment shape)
+    "tq4_d256_32x32768": (3, 32, 16, 2, "32768", "turboquant_4bit_nc", 256),
 }
 
 
@@ -188,9 +201,12 @@ def bench_decode_cfg(args, torch, capi, dev, kind):
     (134 B slots), seed 2; "g32_4bit_32x8192": the same batch with the
     configuration text's 4-bit per-32-group variant (160 B slots, signs
     seed 2); "q8_0_batch16": batch 16, lengths uniform in [512, 4096]
-    (seed 1), 32/8 heads, q8_0 K and V pages (136 B per token-head each).
-    Pools replicated to >= 2 GiB and rotated."""
-    seed, B, Hq, Hkv, lspec, fmt = DECODE_CFGS[kind]
+    (seed 1), 32/8 heads, q8_0 K and V pages (136 B per token-head each);
+    "tq4_d256_32x32768": batch 32 x 32768 tokens, head_dim 256, 16/2 heads,
+    turboquant_4bit_nc (262 B slots), seed 3.  Pools replicated to >= 2 GiB
+    and rotated."""
+    seed, B, Hq, Hkv, lspec, fmt, *hd = DECODE_CFGS[kind]
+    D = hd[0] if hd else HEAD_DIM
     if lspec == "u512_4096":
         lens = np.random.default_rng(seed).integers(512, 4097, B).astype(np.int32)
     else:
@@ -262,7 +278,7 @@ def bench_decode_cfg(args, torch, capi, dev, kind):
     log(f"decode {kind}: {ms * 1e3:.1f} us (median {med * 1e3:.1f}), {gbs:.0f} GB/s")
     del pools
     torch.cuda.empty_cache()
-    return {"workload": kind, "kv": fmt, "batch": B, "num_heads": Hq, "num_kv_heads": Hkv,
+    return {"workload": kind, "kv": fmt, "batch": B, "num_heads": Hq, "num_kv_heads": Hkv, "head_dim": D,
             "sum_ctx": T, "ms": round(ms, 4), "ms_median": round(med, 4), "gbs": round(gbs, 1),
             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes,
             "tokens_per_s": round(B / (ms * 1e-3), 1)}
@@ -640,6 +656,8 @@ def main():
     ap.add_argument("--only", choices=("decode", "prefill", "paged_prefill", "fused", "configs"),
                     help="profiling runs: only this part (decode: the headline operator; configs: "
                          "the other decode configurations), one JSON line of its numbers")
+    ap.add_argument("--config", choices=tuple(DECODE_CFGS),
+                    help="with --only configs: just this decode configuration")
     ap.add_argument("--read-calibration", action="store_true",
                     help="only run a 1 GiB load-to-LDS read (vmc_hbm_read_probe mode 2, the decode's "
                          "request type) 5 times (for scaling rocprofv3 FETCH_SIZE)")
@@ -687,7 +705,8 @@ def main():
         elif args.only == "fused":
             r = bench_fused_norm_rope(args, torch, capi, dev)
         else:
-            r = {"configs": [bench_decode_cfg(args, torch, capi, dev, k) for k in DECODE_CFGS]}
+            r = {"configs": [bench_decode_cfg(args, torch, capi, dev, k) for k in DECODE_CFGS
+                             if args.config in (None, k)]}
         print(json.dumps({"only": args.only, **{k: v for k, v in r.items() if not hasattr(v, "shape")}}),
               flush=True)
         return
@@ -706,7 +725,7 @@ def main():
         del v
         torch.cuda.empty_cache()
     kinds = ("f16_single2048",) + (() if args.skip_variant else
-                                    ("tq4_32x8192", "g32_4bit_32x8192", "q8_0_batch16"))
+                                    ("tq4_32x8192", "g32_4bit_32x8192", "q8_0_batch16", "tq4_d256_32x32768"))
     others = [bench_decode_cfg(args, torch, capi, dev, k) for k in kinds]
     pre = None if args.skip_prefill else bench_prefill(args, torch, capi, dev)
     paged = None if args.skip_prefill else bench_paged_prefill(args, torch, capi, dev)

@@ -400,11 +400,11 @@ inline int tq_stream_ranges(int B, int Hkv, int max_blocks, int max_splits, int 
 }
 
 // Page ranges of the head_dim-256 TurboQuant decode (tq_decode_d256.hip):
-// workgroups of 4 / Hkv ranges (one per group of Hkv waves), two resident
-// per CU; fewer for small batches (the last workgroup's surplus streams idle)
+// one workgroup of 8 / Hkv ranges (one per group of Hkv waves) per CU;
+// fewer for small batches (the last workgroup's surplus streams idle)
 inline int d256_ranges(int B, int Hkv, int max_blocks, int max_splits, int cus) {
-    const int ns = std::max(1, 4 / Hkv);
-    int64_t n = (int64_t)cus * 2 * ns;
+    const int ns = std::max(1, 8 / Hkv);
+    int64_t n = (int64_t)cus * ns;
     n = std::min<int64_t>(n, ((int64_t)B * max_blocks + kPpsMin - 1) / kPpsMin);
     if (max_splits > 1) n = std::min<int64_t>(n, (int64_t)B * max_splits);
     return (int)std::max<int64_t>(1, n);

@@ -11,12 +11,13 @@
 // merged in a second pass (stage 2, :508-547).
 //
 // Organisation:
-//  * a workgroup of 4 waves = Hkv heads x S page streams (S = 4 / Hkv); each
-//    stream is a page range of its own (its own plan, pieces and partial
-//    slots), and each wave (head, stream) runs one page of its stream per
-//    step;
+//  * a workgroup of 8 waves = Hkv heads x S page streams (S = 8 / Hkv), one
+//    per CU; each stream is a page range of its own (its own plan, pieces
+//    and partial slots), and each wave (head, stream) runs one page of its
+//    stream per step;
 //  * per step the workgroup fetches the S pages (every KV head of each, a
-//    contiguous block) by load-to-LDS transfers into one of two buffers;
+//    contiguous block) by load-to-LDS transfers into one of three buffers,
+//    two steps in flight;
 //  * per wave and page (16 tokens x G <= 8 query heads): S^T = K . Q^T on
 //    v_mfma_f32_16x16x32_f16 over 8 steps of 32 dims (lane (r16, grp) holds
 //    dims 64 grp .. + 63 of token r16; Q^T columns c and c + 8 both hold head
@@ -25,8 +26,8 @@
 //    tokens, 16 output tiles of 16 dims (lane r16 owns dims 16 r16 .. + 15),
 //    V codes as exact fp16 subnormals and sum(P * zero) kept apart;
 //  * key codes go through an LDS table of packed fp16 centroid pairs (code
-//    pair -> two fp16), replicated so that few lanes of a half wave share a
-//    bank; P enters the PV product as fp16(P * scale), with the exact running
+//    pair -> two fp16) in 32 copies, lane l reading copy l % 32 (no two
+//    lanes of a half wave share a bank); P enters the PV product as fp16(P * scale), with the exact running
 //    max for a page whose largest value scale exceeds 65504 / 2^8.
 #include "decode_plan.hpp"
 
@@ -42,12 +43,15 @@ struct D2Geo {
     static constexpr int slot = (kp + vd + 4 + 1) / 2 * 2;  // 262 (4-bit), 198 (3-bit)
     static constexpr int row = HK * slot;                   // one token row, every KV head
     static constexpr int page = kBs * row;                  // a multiple of 16 bytes
-    static constexpr int ns = 4 / HK;                       // page streams per workgroup
-    static constexpr int chunks = page / 16;                // 16-byte chunks of a page
-    static constexpr int cw = (chunks + 3) / 4;             // chunks per wave and page
-    static constexpr int tr = (cw + 63) / 64;               // transfers per wave and page
-    // key table: entry e (codes c0 | c1 << KB) at words (e << log2c) + copy
-    static constexpr int log2c = KB == 3 ? 5 : 2;
+    static constexpr int ns = 8 / HK;                       // page streams per workgroup (HK waves each)
+    static constexpr int nb = 3;                            // page buffers per stream
+    // a page is HK * slot 16-byte chunks: wave h of a stream fetches chunks
+    // h * slot .. + slot - 1, in ni transfers (the last of `last` lanes)
+    static constexpr int ni = (slot + 63) / 64;
+    static constexpr int last = slot - 64 * (ni - 1);
+    // key table: entry e (codes c0 | c1 << KB) at words (e << log2c) + copy,
+    // 32 copies: lane l reads copy l % 32, its own bank
+    static constexpr int log2c = 5;
     static constexpr int lut_words = (KB == 3 ? 64 : 256) << log2c;
     static constexpr int kw = KB == 3 ? 7 : 9;  // key words of a lane (its 64 dims, from the 4-byte floor)
 };
@@ -56,9 +60,9 @@ template <int KB, int HK>
 struct alignas(16) D2Lds {
     using DG = D2Geo<KB, HK>;
     uint32_t lut[DG::lut_words];
-    uint8_t ring[2][DG::ns][DG::page];
-    uint16_t qsc[4][8 * 256];  // per-wave rotated q (fp16, [head][dim])
-    float wscr[4][80];         // per-wave exchange
+    uint8_t ring[DG::ns][DG::nb][DG::page];  // [stream][buffer]: a buffer within 64 KB of its stream's
+    float wscr[8][80];                       // per-wave exchange
+    uint32_t ctab[16];                       // fp16 centroids (table build)
     int32_t bt[DG::ns][kPages2];
     int32_t info[DG::ns][kPages2];  // b << 6 | valid tokens << 1 | piece ends
     int32_t seg_b[DG::ns][kPages2], seg_ps[DG::ns][kPages2], seg_L[DG::ns][kPages2];
@@ -98,7 +102,7 @@ __device__ __forceinline__ uint32_t v_field(const uint32_t (&wv)[4], int c) {
 }
 
 template <int KB, int HK, bool BF>
-__global__ void __launch_bounds__(256, 2) tq_decode_d256_kernel(DecodeParams p) {
+__global__ void __launch_bounds__(512, 1) tq_decode_d256_kernel(DecodeParams p) {
     using DG = D2Geo<KB, HK>;
     using AT = f16x8;
     __shared__ D2Lds<KB, HK> lds;
@@ -134,16 +138,14 @@ __global__ void __launch_bounds__(256, 2) tq_decode_d256_kernel(DecodeParams p) 
         }
         if (lane == 0) lds.plan[stream] = wp;
     }
-    // key table
-    for (int i = tid; i < DG::lut_words; i += 256) {
-        const int e = i >> DG::log2c, c0 = e & ((1 << KB) - 1), c1 = e >> KB;
-        float a = 0.0f, b = 0.0f;
-#pragma unroll
-        for (int c = 0; c < (1 << KB); ++c) {
-            a = c == c0 ? p.tab.centroids[c] : a;
-            b = c == c1 ? p.tab.centroids[c] : b;
-        }
-        lds.lut[i] = (uint32_t)f32_to_f16_bits(a) | ((uint32_t)f32_to_f16_bits(b) << 16);
+    // key table: the fp16 centroids, then each entry's 32 copies (four per
+    // 16-byte store)
+    if (tid < (1 << KB)) lds.ctab[tid] = f32_to_f16_bits(p.tab.centroids[tid]);
+    __syncthreads();
+    for (int i = tid; i < DG::lut_words / 4; i += 512) {
+        const int e = i >> (DG::log2c - 2);
+        const uint32_t v = lds.ctab[e & ((1 << KB) - 1)] | (lds.ctab[e >> KB] << 16);
+        reinterpret_cast<u32x4*>(lds.lut)[i] = u32x4{v, v, v, v};
     }
     __syncthreads();
     WGPlan& plan = lds.plan[stream];
@@ -172,28 +174,30 @@ __global__ void __launch_bounds__(256, 2) tq_decode_d256_kernel(DecodeParams p) 
     // ---- Q operand: lane (r16, grp) holds dims 64 grp + 8 j + e of head
     // r16 % 8 for MFMA j, rotated (H q / sqrt(256)).  The rotation runs with
     // lane (h, t) = (lane / 8, lane % 8) holding dims 32 t .. + 31 of head h
-    // (three cross-lane stages by DPP), and the wave's LDS block turns its
-    // fp16 result into the operand layout.
+    // (three cross-lane stages by DPP); lane permutes then gather the
+    // operand: dims 64 grp .. + 31 from lane 8 h + 2 grp, the next 32 from
+    // lane 8 h + 2 grp + 1.
     AT qb[8];
-    uint16_t* const qsc = lds.qsc[wave];
-    auto load_q = [&](int b) __attribute__((always_inline)) {
-        const int h = lane >> 3, t = lane & 7;
-        float y[32];
-        if (h < G) {
-            const u32x4* src = reinterpret_cast<const u32x4*>(p.q + ((int64_t)b * p.Hq + hq0 + h) * kD2 + 32 * t);
+    const int qlh = lane >> 3, qlt = lane & 7;
+    auto fetch_q = [&](int b, u32x4 (&raw)[4]) __attribute__((always_inline)) {
+        if (qlh < G) {
+            const u32x4* src = reinterpret_cast<const u32x4*>(p.q + ((int64_t)b * p.Hq + hq0 + qlh) * kD2 + 32 * qlt);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const u32x4 wv = src[c];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    y[8 * c + 2 * e] = half_to_f32<BF>((uint16_t)(wv[e] & 0xffff));
-                    y[8 * c + 2 * e + 1] = half_to_f32<BF>((uint16_t)(wv[e] >> 16));
-                }
-            }
+            for (int c = 0; c < 4; ++c) raw[c] = src[c];
         } else {
 #pragma unroll
-            for (int e = 0; e < 32; ++e) y[e] = 0.0f;
+            for (int c = 0; c < 4; ++c) raw[c] = u32x4{0u, 0u, 0u, 0u};
         }
+    };
+    auto rotate_q = [&](const u32x4 (&raw)[4]) __attribute__((always_inline)) {
+        float y[32];
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                y[8 * c + 2 * e] = half_to_f32<BF>((uint16_t)(raw[c][e] & 0xffff));
+                y[8 * c + 2 * e + 1] = half_to_f32<BF>((uint16_t)(raw[c][e] >> 16));
+            }
         // Walsh-Hadamard: half-widths 1..16 inside the lane, 32, 64, 128 across
         // lanes (dim bits 5, 6, 7 = lane bits 0, 1, 2)
 #pragma unroll
@@ -221,23 +225,25 @@ __global__ void __launch_bounds__(256, 2) tq_decode_d256_kernel(DecodeParams p) 
             const float o = row_xor<4>(y[e], lane);
             y[e] = (lane & 4) ? o - y[e] : y[e] + o;
         }
-        u32x4* dst = reinterpret_cast<u32x4*>(qsc + h * kD2 + 32 * t);
+        uint32_t wq[16];  // fp16 pairs: dims 32 t + 2 k, + 1
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
+        for (int k = 0; k < 16; ++k)
+            wq[k] = (uint32_t)f32_to_f16_bits(__fmul_rn(y[2 * k], p.tab.rot_c)) |
+                    ((uint32_t)f32_to_f16_bits(__fmul_rn(y[2 * k + 1], p.tab.rot_c)) << 16);
+        const int src0 = (8 * qh + 2 * grp) << 2;  // byte address of the source lane
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
             u32x4 v;
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                v[e] = (uint32_t)f32_to_f16_bits(__fmul_rn(y[8 * c + 2 * e], p.tab.rot_c)) |
-                       ((uint32_t)f32_to_f16_bits(__fmul_rn(y[8 * c + 2 * e + 1], p.tab.rot_c)) << 16);
-            dst[c] = v;
+            for (int d = 0; d < 4; ++d)
+                v[d] = (uint32_t)__builtin_amdgcn_ds_bpermute(src0 + ((j >> 2) << 2), (int)wq[4 * (j & 3) + d]);
+            qb[j] = __builtin_bit_cast(AT, v);
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const uint16_t* srcq = qsc + qh * kD2 + 64 * grp;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) qb[j] = *reinterpret_cast<const AT*>(srcq + 8 * j);
-        __builtin_amdgcn_wave_barrier();
+    };
+    auto load_q = [&](int b) __attribute__((always_inline)) {
+        u32x4 raw[4];
+        fetch_q(b, raw);
+        rotate_q(raw);
     };
 
     // ---- running state of the current piece
@@ -310,12 +316,12 @@ __global__ void __launch_bounds__(256, 2) tq_decode_d256_kernel(DecodeParams p) 
         reset_state();
     };
 
-    // ---- loop-invariant LDS offsets inside a page buffer (a byte copy of the
-    // page; token row r at r * row, this head's run at head * slot of it): the
-    // key words of token r16 (dims 64 grp .. + 63, from the 4-byte floor), its
-    // norm, the value runs of tokens 4 grp + i (dims 16 r16 .. + 15) and their
-    // scale / zero pairs
-    const int run0 = head * DG::slot;
+    // ---- loop-invariant LDS offsets from buffer 0 of this wave's stream (a
+    // byte copy of the page; token row r at r * row, this head's run at
+    // head * slot of it): the key words of token r16 (dims 64 grp .. + 63,
+    // from the 4-byte floor), its norm, the value runs of tokens 4 grp + i
+    // (dims 16 r16 .. + 15) and their scale / zero pairs
+    const int run0 = stream * DG::nb * DG::page + head * DG::slot;
     const int kq = r16 * DG::row + run0 + (KB == 3 ? 24 : 32) * grp;
     const int kfl = kq & ~3;
     const uint32_t ksh = (uint32_t)(kq & 3);
@@ -435,6 +441,12 @@ __global__ void __launch_bounds__(256, 2) tq_decode_d256_kernel(DecodeParams p) 
         }
         l_part += psum;
         z_part += zsum;
+        uint32_t vw[2][4];  // half h, token 4 grp + i: the run's words from its floor, aligned
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                vw[h][i] = __builtin_amdgcn_alignbyte(lds32(pg + vfl[h][i] + 4), lds32(pg + vfl[h][i]), vsh[h][i]);
         // value operands: tile c = dim 16 r16 + c; tokens 4 grp + 0, 1 in dword
         // 0 and + 2, 3 in dword 1; the run's first 8 codes from its bytes
         // 0 .. 3, the last 8 from the bytes after (3-bit: bytes 3 .. 6, 4-bit:
@@ -444,11 +456,7 @@ __global__ void __launch_bounds__(256, 2) tq_decode_d256_kernel(DecodeParams p) 
             uint32_t wv[2][4];
 #pragma unroll
             for (int tp = 0; tp < 2; ++tp) {
-                const int i0 = 2 * tp, i1 = 2 * tp + 1;
-                const uint32_t A = __builtin_amdgcn_alignbyte(lds32(pg + vfl[half][i0] + 4), lds32(pg + vfl[half][i0]),
-                                                              vsh[half][i0]);
-                const uint32_t B = __builtin_amdgcn_alignbyte(lds32(pg + vfl[half][i1] + 4), lds32(pg + vfl[half][i1]),
-                                                              vsh[half][i1]);
+                const uint32_t A = vw[half][2 * tp], B = vw[half][2 * tp + 1];
                 wv[tp][0] = __builtin_amdgcn_perm(B, A, vsel0);
                 wv[tp][1] = __builtin_amdgcn_perm(B, A, vsel1);
                 wv[tp][2] = __builtin_amdgcn_perm(B, A, vsel2);
@@ -462,19 +470,22 @@ __global__ void __launch_bounds__(256, 2) tq_decode_d256_kernel(DecodeParams p) 
         }
     };
 
-    // ---- pages of a stream: staged per slice (block and sequence info)
-    const uint32_t ring_lds = lds_addr2(&lds.ring[0][0][0]);
-    auto dma_page = [&](int32_t blk, int buf, int s) __attribute__((always_inline)) {
-        // wave w fetches chunks [cw w, min(cw (w + 1), chunks)) of stream s's page
-        const int c0 = DG::cw * wave, n = min(DG::chunks, c0 + DG::cw) - c0;
-        const uint8_t* src = p.kc + (int64_t)blk * p.page_bytes + 16 * c0;
-        const uint32_t m0 = __builtin_amdgcn_readfirstlane(ring_lds + (buf * DG::ns + s) * DG::page + 16 * c0);
+    // ---- pages of a stream: staged per slice (block and sequence info).
+    // Wave h of a stream fetches chunks h * slot .. + slot - 1 of the stream's
+    // page of a step: always ni transfers (a stream without a page in the
+    // step fetches block 0 unused), so that vmcnt counts steps.
+    const uint32_t ring_lds = lds_addr2(&lds.ring[stream][0][0]) + 16 * head * DG::slot;
+    auto dma_step = [&](int k, int buf) __attribute__((always_inline)) {
+        const int info = __builtin_amdgcn_readfirstlane(lds.info[stream][k]);
+        const int32_t blk = (info & (1 << 30)) ? __builtin_amdgcn_readfirstlane(max(lds.bt[stream][k], 0)) : 0;
+        const uint8_t* src = p.kc + (int64_t)blk * p.page_bytes + 16 * head * DG::slot;
+        const uint32_t m0 = __builtin_amdgcn_readfirstlane(ring_lds + buf * DG::page);
         uint32_t doff;
         asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0\n\tv_lshlrev_b32 %0, 4, %0"
                      : "=v"(doff));
 #pragma unroll
-        for (int i = 0; i < DG::tr; ++i)
-            if (64 * i < n && 64 * i + lane < n) dma16_d2(src + 1024 * i, doff, m0 + 1024 * i);
+        for (int i = 0; i < DG::ni - 1; ++i) dma16_d2(src + 1024 * i, doff, m0 + 1024 * i);
+        if (lane < DG::last) dma16_d2(src + 1024 * (DG::ni - 1), doff, m0 + 1024 * (DG::ni - 1));
     };
 
     for (int c0 = 0; c0 < steps; c0 += kPages2) {
@@ -489,7 +500,7 @@ __global__ void __launch_bounds__(256, 2) tq_decode_d256_kernel(DecodeParams p) 
             if (lane == 0) lds.n_seg[stream] = ns;
         }
         __syncthreads();
-        for (int e = tid; e < DG::ns * cn; e += 256) {
+        for (int e = tid; e < DG::ns * cn; e += 512) {
             const int s = e / cn, i = e - s * cn;
             const int lo_s = lds.plan[s].p_lo, hi_s = lds.plan[s].p_hi;
             const int gp = lo_s + c0 + i;
@@ -514,25 +525,32 @@ __global__ void __launch_bounds__(256, 2) tq_decode_d256_kernel(DecodeParams p) 
         }
         __syncthreads();
 
-        auto issue_step = [&](int k, int buf) __attribute__((always_inline)) {
-#pragma unroll
-            for (int s = 0; s < DG::ns; ++s) {
-                const int info = __builtin_amdgcn_readfirstlane(lds.info[s][k]);
-                if (info & (1 << 30)) dma_page(__builtin_amdgcn_readfirstlane(max(lds.bt[s][k], 0)), buf, s);
-            }
-        };
-        // Step k sits in buffer k % 2: wait for this wave's transfers of step k,
-        // a workgroup barrier (every wave's have landed, and every wave has
-        // finished step k - 1, whose buffer is free), issue step k + 1, compute.
-        issue_step(0, 0);
-        for (int k0 = 0; k0 < cn; k0 += 2) {
-            static_for<2>([&](auto pc) __attribute__((always_inline)) {
+        // Step k sits in buffer k % 3; two steps in flight.  At step k: wait
+        // for this wave's transfers of step k (those of step k + 1 may stay
+        // in flight), a workgroup barrier (every wave's have landed, and
+        // every wave has finished step k - 1, whose buffer is free), issue
+        // step k + 2 there, compute step k.
+        // q of the range's first sequence: its loads in flight with the first
+        // transfers
+        const int info0 = __builtin_amdgcn_readfirstlane(lds.info[stream][0]);
+        const bool pre = c0 == 0 && (info0 & (1 << 30));
+        u32x4 raw[4];
+        if (pre) fetch_q((info0 >> 6) & 0xffffff, raw);
+        dma_step(0, 0);
+        if (cn > 1) dma_step(1, 1);
+        if (pre) {
+            rotate_q(raw);
+            cur_b = (info0 >> 6) & 0xffffff;
+        }
+        for (int k0 = 0; k0 < cn; k0 += 3) {
+            static_for<3>([&](auto pc) __attribute__((always_inline)) {
                 constexpr int P = decltype(pc)::value;
                 const int k = k0 + P;
                 if (k < cn) {
-                    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                    if (k + 1 < cn) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DG::ni) : "memory");
+                    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                     __syncthreads();
-                    if (k + 1 < cn) issue_step(k + 1, P ^ 1);
+                    if (k + 2 < cn) dma_step(k + 2, (P + 2) % 3);
                     const int info = __builtin_amdgcn_readfirstlane(lds.info[stream][k]);
                     if (info & (1 << 30)) {  // uniform over the wave
                         const int b = (info >> 6) & 0xffffff;
@@ -540,7 +558,7 @@ __global__ void __launch_bounds__(256, 2) tq_decode_d256_kernel(DecodeParams p) 
                             load_q(b);
                             cur_b = b;
                         }
-                        compute_page(&lds.ring[P][stream][0], (info >> 1) & 31);
+                        compute_page(&lds.ring[0][P][0], (info >> 1) & 31);
                         if (info & 1) finalize(b);
                     }
                 }
@@ -553,12 +571,13 @@ __global__ void __launch_bounds__(256, 2) tq_decode_d256_kernel(DecodeParams p) 
 
 // Combines the pieces of sequences cut by range boundaries (head_dim 256):
 // decode_merge_kernel's rule over rows of 256 + 2 floats (o unnormalised, m,
-// l).  Grid (B, Hkv), one wave per query head of the KV head; lane l owns
-// dims 4 l .. + 3, eight pieces' rows in flight at a time.
-__global__ void __launch_bounds__(512) decode_merge_d256_kernel(DecodeParams p) {
-    const int b = blockIdx.x, g = blockIdx.y;
+// l).  Grid (B, Hq), 4 waves per (sequence, query head): wave w takes pieces
+// w, w + 4, ... (sixteen rows in flight), lane l dims 4 l .. + 3; the four
+// partial sums are combined through LDS.
+__global__ void __launch_bounds__(256) decode_merge_d256_kernel(DecodeParams p) {
+    __shared__ __attribute__((aligned(16))) float red[4][kD2 + 4];  // rows 16-byte aligned
+    const int b = blockIdx.x, hq = blockIdx.y;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int hq = g * p.G + wave;
     int carry = 0, ps_b = 0, pg_b = 0;
     for (int b0 = 0; b0 < p.B; b0 += 64) {
         int L = 0;
@@ -573,7 +592,7 @@ __global__ void __launch_bounds__(512) decode_merge_d256_kernel(DecodeParams p) 
     const int T = carry;
     uint16_t* orow = reinterpret_cast<uint16_t*>(p.out) + ((int64_t)b * p.Hq + hq) * kD2;
     if (pg_b == 0) {
-        reinterpret_cast<u32x2*>(orow)[lane] = u32x2{0u, 0u};
+        if (wave == 0) reinterpret_cast<u32x2*>(orow)[lane] = u32x2{0u, 0u};
         return;
     }
     const int n = effective_wgs(p, T, p.grid);
@@ -587,50 +606,64 @@ __global__ void __launch_bounds__(512) decode_merge_d256_kernel(DecodeParams p) 
     };
     float M = kNegInf, L = 0.0f;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int s0 = 0; s0 < nseg; s0 += 64) {
-        const int cnt = min(64, nseg - s0);
-        float2 ml = make_float2(kNegInf, 0.0f);
-        if (lane < cnt) ml = *reinterpret_cast<const float2*>(row(s0 + lane) + kD2);
-        const float Mn = fmaxf(M, wave_max(ml.x));
-        if (Mn > M && M != kNegInf) {  // wave-uniform
-            const float f = __builtin_amdgcn_exp2f(M - Mn);
+    for (int s0 = wave; s0 < nseg; s0 += 64) {
+        // (rows are 8-byte aligned: float2 loads)
+        float2 o[16][2], ml[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const float* r = row(min(s0 + 4 * u, nseg - 1));
+            ml[u] = *reinterpret_cast<const float2*>(r + kD2);
+            o[u][0] = *reinterpret_cast<const float2*>(r + 4 * lane);
+            o[u][1] = *reinterpret_cast<const float2*>(r + 4 * lane + 2);
+        }
+        float mx = M;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) mx = s0 + 4 * u < nseg ? fmaxf(mx, ml[u].x) : mx;
+        if (mx > M && M != kNegInf) {  // wave-uniform
+            const float f = __builtin_amdgcn_exp2f(M - mx);
             L *= f;
 #pragma unroll
             for (int e = 0; e < 4; ++e) acc[e] *= f;
         }
-        M = Mn;
+        M = mx;
         const float Mu = M == kNegInf ? 0.0f : M;
-        float wt = 0.0f;
-        if (lane < cnt) {
-            wt = __builtin_amdgcn_exp2f(ml.x - Mu);
-            L = __builtin_fmaf(ml.y, wt, L);
-        }
-        for (int j0 = 0; j0 < cnt; j0 += 8) {
-            // (rows are 8-byte aligned: float2 loads)
-            float2 o[8][2];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const float2* r = reinterpret_cast<const float2*>(row(s0 + min(j0 + u, cnt - 1)) + 4 * lane);
-                o[u][0] = r[0];
-                o[u][1] = r[1];
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const float wu = j0 + u < cnt ? __shfl(wt, min(j0 + u, cnt - 1), 64) : 0.0f;
-                acc[0] = __builtin_fmaf(o[u][0].x, wu, acc[0]);
-                acc[1] = __builtin_fmaf(o[u][0].y, wu, acc[1]);
-                acc[2] = __builtin_fmaf(o[u][1].x, wu, acc[2]);
-                acc[3] = __builtin_fmaf(o[u][1].y, wu, acc[3]);
-            }
+        for (int u = 0; u < 16; ++u) {
+            const float wu = s0 + 4 * u < nseg ? __builtin_amdgcn_exp2f(ml[u].x - Mu) : 0.0f;
+            L = __builtin_fmaf(ml[u].y, wu, L);
+            acc[0] = __builtin_fmaf(o[u][0].x, wu, acc[0]);
+            acc[1] = __builtin_fmaf(o[u][0].y, wu, acc[1]);
+            acc[2] = __builtin_fmaf(o[u][1].x, wu, acc[2]);
+            acc[3] = __builtin_fmaf(o[u][1].y, wu, acc[3]);
         }
     }
-    L = wave_sum(L);
-    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    *reinterpret_cast<f32x4*>(&red[wave][4 * lane]) = f32x4{acc[0], acc[1], acc[2], acc[3]};
+    if (lane == 0) {
+        red[wave][kD2] = M;
+        red[wave][kD2 + 1] = L;
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    float Mg = kNegInf;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) Mg = fmaxf(Mg, red[w][kD2]);
+    const float Mgu = Mg == kNegInf ? 0.0f : Mg;
+    float Lg = 0.0f;
+    f32x4 og = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const float f = red[w][kD2] == kNegInf ? 0.0f : __builtin_amdgcn_exp2f(red[w][kD2] - Mgu);
+        Lg = __builtin_fmaf(red[w][kD2 + 1], f, Lg);
+        const f32x4 v = *reinterpret_cast<const f32x4*>(&red[w][4 * lane]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) og[e] = __builtin_fmaf(v[e], f, og[e]);
+    }
+    const float inv = Lg > 0.0f ? 1.0f / Lg : 0.0f;
     uint32_t w2[2];
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-        const uint16_t x0 = p.q_bf16 ? f32_to_bf16_bits(acc[2 * e] * inv) : f32_to_f16_bits(acc[2 * e] * inv);
-        const uint16_t x1 = p.q_bf16 ? f32_to_bf16_bits(acc[2 * e + 1] * inv) : f32_to_f16_bits(acc[2 * e + 1] * inv);
+        const uint16_t x0 = p.q_bf16 ? f32_to_bf16_bits(og[2 * e] * inv) : f32_to_f16_bits(og[2 * e] * inv);
+        const uint16_t x1 = p.q_bf16 ? f32_to_bf16_bits(og[2 * e + 1] * inv) : f32_to_f16_bits(og[2 * e + 1] * inv);
         w2[e] = (uint32_t)x0 | ((uint32_t)x1 << 16);
     }
     reinterpret_cast<u32x2*>(orow)[lane] = u32x2{w2[0], w2[1]};
@@ -645,10 +678,10 @@ int launch_d256(DecodeParams& prm, hipStream_t stream) {
     // ranges: one per sequence (per-sequence mode), else d256_ranges'
     prm.grid = prm.per_seq ? prm.B : d256_ranges(prm.B, prm.Hkv, prm.max_blocks, prm.max_splits, num_cus());
     const int nwg = (prm.grid + DG::ns - 1) / DG::ns;
-    hipLaunchKernelGGL((tq_decode_d256_kernel<KB, HK, BF>), dim3(nwg), dim3(256), 0, stream, prm);
+    hipLaunchKernelGGL((tq_decode_d256_kernel<KB, HK, BF>), dim3(nwg), dim3(512), 0, stream, prm);
     VMC_LAUNCH_CHECK();
     if (!prm.per_seq) {
-        hipLaunchKernelGGL(decode_merge_d256_kernel, dim3(prm.B, prm.Hkv), dim3(64 * prm.G), 0, stream, prm);
+        hipLaunchKernelGGL(decode_merge_d256_kernel, dim3(prm.B, prm.Hq), dim3(256), 0, stream, prm);
         VMC_LAUNCH_CHECK();
     }
     return VMC_OK;
