@@ -80,14 +80,19 @@ def decode_workload():
 
 
 def time_loop(torch, fn, n, warm, stream):
-    """`warm` untimed calls, then `n` back-to-back timed calls between two HIP
-    events on `stream` (the stream the kernels run on): the mean ms per call
-    over that region; then `n` more calls with an event after each, for the
-    median ms of one call.  (An event between calls is a full release on this
-    runtime: it adds several microseconds to every call it follows, so it
-    stays out of the mean.)  Returns (mean, median)."""
-    for i in range(warm):
+    """Untimed warm-up (at least `warm` calls and at least 0.3 s, so the
+    clocks have settled under the load), then `n` back-to-back timed calls
+    between two HIP events on `stream` (the stream the kernels run on): the
+    mean ms per call, the whole-job rate; then `n` more calls with an event
+    after each, for the median ms of one call.  Returns (mean, median)."""
+    import time
+    t_end = time.perf_counter() + 0.3
+    i = 0
+    while i < warm or (time.perf_counter() < t_end and i < 4000):
         fn(i)
+        i += 1
+        if i % 16 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
