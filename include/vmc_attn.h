@@ -62,6 +62,34 @@ int vmc_reshape_and_cache(const void* key, const void* value, void* key_cache,
                           vmc_stream_t stream);
 
 /*
+ * fp8 pages: reshape_and_cache with kv_cache_dtype "fp8_e4m3" or "fp8_e5m2"
+ * (src/cuda/cache_kernels.cu:101-120, :14-54).  Both strings store OCP FP8
+ * E4M3 bytes (the reference casts to __nv_fp8_e4m3 for either): one byte per
+ * value, x / k_scale for K and x / v_scale for V, rounded to nearest even and
+ * saturated to +-448 (NaN -> 0x7f).  Page addressing and slot_mapping as in
+ * vmc_reshape_and_cache with one-byte entries (head_dim bytes per (token,
+ * head)); cache_stride 0 = block_size * num_kv_heads * head_dim.
+ *   k_scale, v_scale   HOST pointers to one float each, read at the call
+ *                      (cache_kernels.cu:102-104); NULL = 1.0
+ * head_dim % 16 == 0; cache_stride % 16 == 0; key/value/pools 16-byte aligned.
+ */
+int vmc_reshape_and_cache_fp8(const void* key, const void* value, void* key_cache,
+                              void* value_cache, const int64_t* slot_mapping, int num_tokens,
+                              int num_kv_heads, int head_dim, int64_t block_size,
+                              int64_t cache_stride, const float* k_scale, const float* v_scale,
+                              int src_dtype, int layout, vmc_stream_t stream);
+
+/*
+ * Cache conversion to fp8: replaces vm_c::convert_fp8 (src/cuda/
+ * cache_kernels.cu:175-212): dst[i] = fp8(src[i] * (float)scale) for
+ * num_elements values of src_dtype, E5M2 when e5m2 != 0 ("fp8_e5m2"), else
+ * E4M3 ("fp8_e4m3"); OCP FP8, rounded to nearest even, saturated to the
+ * largest finite value (E4M3 448, E5M2 57344), NaN -> 0x7f.
+ */
+int vmc_convert_fp8(void* dst_cache, const void* src_cache, double scale, int64_t num_elements,
+                    int e5m2, int src_dtype, vmc_stream_t stream);
+
+/*
  * Paged decode attention, one query token per sequence, over f16/bf16/q8_0/
  * q4_0 pages read through the block table, split-KV with an fp32 LSE merge.
  * Replaces vm_c::paged_attention_v1 / _v2 (include/vm_c/cuda/

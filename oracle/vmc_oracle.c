@@ -243,6 +243,80 @@ void orc_kv_append(const uint16_t* key, const uint16_t* value, int src_bf16,
     free(tmp);
 }
 
+/* OCP OFP8 v1.0 (E4M3: 3 mantissa bits, bias 7, max 448 = 0x7e; E5M2: 2
+ * mantissa bits, bias 15, max 57344 = 0x7b), round to nearest even with
+ * saturation to the largest finite value; see the header. */
+uint8_t orc_f32_to_ofp8(float x, int e5m2) {
+    const int M = e5m2 ? 2 : 3, B = e5m2 ? 15 : 7;
+    const float maxv = e5m2 ? 57344.0f : 448.0f;
+    const uint8_t maxc = e5m2 ? 0x7b : 0x7e;
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    const uint8_t s = (uint8_t)((u >> 31) << 7);
+    if (isnan(x)) return 0x7f;
+    if (fabsf(x) >= maxv) return (uint8_t)(s | maxc);
+    const uint32_t a = u & 0x7fffffffu;
+    const int E = (int)(a >> 23) - 127;
+    const uint32_t man = a & 0x7fffffu;
+    if (E >= 1 - B) { /* normal: keep M mantissa bits, a carry moves into the exponent */
+        const int sh = 23 - M;
+        const uint32_t q = man >> sh, rem = man & ((1u << sh) - 1u), half = 1u << (sh - 1);
+        const uint32_t up = rem > half || (rem == half && (q & 1u));
+        return (uint8_t)(s | ((((uint32_t)(E + B)) << M) + q + up));
+    }
+    if (a < 0x00800000u) return s; /* zero and fp32 subnormals (far below the fp8 quantum) */
+    /* subnormal: multiples of 2^(1 - B - M) */
+    const uint32_t sig = man | 0x800000u;
+    const int sh = 24 - B - M - E; /* value / quantum = sig >> sh */
+    if (sh >= 32) return s;
+    const uint32_t q = sig >> sh, rem = sig & ((1u << sh) - 1u), half = 1u << (sh - 1);
+    const uint32_t up = rem > half || (rem == half && (q & 1u));
+    return (uint8_t)(s | (q + up));
+}
+
+void orc_f32_to_ofp8_n(const float* x, uint8_t* y, int64_t n, int e5m2) {
+    for (int64_t i = 0; i < n; ++i) y[i] = orc_f32_to_ofp8(x[i], e5m2);
+}
+
+float orc_ofp8_to_f32(uint8_t b, int e5m2) {
+    const int M = e5m2 ? 2 : 3, B = e5m2 ? 15 : 7;
+    const float sg = (b & 0x80) ? -1.0f : 1.0f;
+    const int e = (b & 0x7f) >> M, m = b & ((1 << M) - 1);
+    if (e5m2 && e == 31) return m ? NAN : sg * INFINITY;
+    if (!e5m2 && e == 15 && m == 7) return NAN;
+    if (e == 0) return sg * ldexpf((float)m, 1 - B - M);
+    return sg * ldexpf((float)((1 << M) + m), e - B - M);
+}
+
+void orc_reshape_and_cache_fp8(const uint16_t* key, const uint16_t* value, int src_bf16,
+                               uint8_t* key_cache, uint8_t* value_cache,
+                               const int64_t* slot_mapping, int num_tokens, int num_kv_heads,
+                               int head_dim, int64_t block_size, int64_t stride, float k_scale,
+                               float v_scale, int hnd) {
+    const int64_t E = head_dim;
+    if (stride <= 0) stride = block_size * num_kv_heads * E;
+    for (int t = 0; t < num_tokens; ++t) {
+        const int64_t slot = slot_mapping[t];
+        if (slot < 0) continue; /* cache_kernels.cu:26 */
+        const int64_t blk = slot / block_size, off = slot % block_size;
+        for (int h = 0; h < num_kv_heads; ++h) {
+            const int64_t src = ((int64_t)t * num_kv_heads + h) * head_dim;
+            /* cache_kernels.cu:36-40 */
+            const int64_t dst = hnd ? blk * stride + (int64_t)h * block_size * E + off * E
+                                    : blk * stride + off * num_kv_heads * E + (int64_t)h * E;
+            for (int d = 0; d < head_dim; ++d) { /* cache_kernels.cu:42-46 */
+                key_cache[dst + d] = orc_f32_to_ofp8(half_to_f32(key[src + d], src_bf16) / k_scale, 0);
+                value_cache[dst + d] = orc_f32_to_ofp8(half_to_f32(value[src + d], src_bf16) / v_scale, 0);
+            }
+        }
+    }
+}
+
+void orc_convert_fp8(uint8_t* dst, const uint16_t* src, int src_bf16, float scale, int64_t n, int e5m2) {
+    for (int64_t i = 0; i < n; ++i) /* cache_kernels.cu:181-184 */
+        dst[i] = orc_f32_to_ofp8(half_to_f32(src[i], src_bf16) * scale, e5m2);
+}
+
 void orc_kv_dequant_entry(const uint8_t* e, int fmt, int D, float* out) {
     if (fmt == ORC_KV_F16 || fmt == ORC_KV_BF16) {
         for (int d = 0; d < D; ++d) {

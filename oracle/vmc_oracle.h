@@ -24,6 +24,10 @@
  *     dequantized pages; split-count invariance; permuted block tables.
  *   - ggml CPU flash-attention restatement: against the vendored ggml CPU
  *     flash_attn_ext (oracle/_ref) and fp64 exact attention.
+ *   - OCP fp8 conversion: every fp16 and bf16 value, random fp32 and every
+ *     midpoint between neighbouring codes (and the floats either side of
+ *     it) against a nearest-value search over the 256 codes with ties to
+ *     the even code; the specification's max / min values.
  */
 #ifndef VMC_ORACLE_H
 #define VMC_ORACLE_H
@@ -48,6 +52,31 @@ void orc_quantize_row_q8_0(const float* x, void* y, int64_t k);
 void orc_dequantize_row_q8_0(const void* x, float* y, int64_t k);
 void orc_quantize_row_q4_0(const float* x, void* y, int64_t k);
 void orc_dequantize_row_q4_0(const void* x, float* y, int64_t k);
+
+/* ---- OCP 8-bit floating point (OCP "8-bit Floating Point Specification
+ *      (OFP8)" v1.0, 2023: E4M3 bias 7, max 448, NaN S.1111.111, no inf;
+ *      E5M2 bias 15, max 57344, IEEE inf / NaN) from fp32: round to nearest
+ *      even, |x| >= max (inf included) saturated to +-max, NaN -> 0x7f.
+ *      This is the conversion of vm_c's fp8 KV paths
+ *      (cache_kernels.cu:43-46 and :184 cast to __nv_fp8_e4m3 / _e5m2,
+ *      whose float constructors saturate to finite); NaN's byte is not
+ *      fixed by those call sites (parity unpinned for NaN inputs). ---- */
+uint8_t orc_f32_to_ofp8(float x, int e5m2);
+void    orc_f32_to_ofp8_n(const float* x, uint8_t* y, int64_t n, int e5m2);
+float   orc_ofp8_to_f32(uint8_t b, int e5m2);
+/* reshape_and_cache with kv_cache_dtype "fp8_e4m3" or "fp8_e5m2"
+ * (cache_kernels.cu:101-120, :14-54): both write E4M3 bytes of x / scale
+ * (the reference casts to __nv_fp8_e4m3 for either string); one byte per
+ * value; page addressing as orc_kv_append with E = head_dim and the block
+ * stride `stride` bytes (0 = bs*Hkv*head_dim). */
+void orc_reshape_and_cache_fp8(const uint16_t* key, const uint16_t* value, int src_bf16,
+                               uint8_t* key_cache, uint8_t* value_cache,
+                               const int64_t* slot_mapping, int num_tokens, int num_kv_heads,
+                               int head_dim, int64_t block_size, int64_t stride, float k_scale,
+                               float v_scale, int hnd);
+/* convert_fp8 (cache_kernels.cu:175-212): dst[i] = fp8(src[i] * scale),
+ * E4M3 for "fp8_e4m3", else E5M2. */
+void orc_convert_fp8(uint8_t* dst, const uint16_t* src, int src_bf16, float scale, int64_t n, int e5m2);
 
 /* ---- paged KV formats for the non-TurboQuant path ---- */
 enum { ORC_KV_F16 = 0, ORC_KV_BF16 = 1, ORC_KV_Q8_0 = 2, ORC_KV_Q4_0 = 3 };

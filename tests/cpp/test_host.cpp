@@ -291,7 +291,7 @@ static void test_metadata() {
 static void test_errors() {
     bool threw = false;
     try {
-        reshape_and_cache(nullptr, nullptr, nullptr, nullptr, nullptr, 0, 8, 128, 16, 0, "fp8_e4m3",
+        reshape_and_cache(nullptr, nullptr, nullptr, nullptr, nullptr, 0, 8, 128, 16, 0, "fp4_e2m1",
                           nullptr, nullptr, ScalarType::FLOAT16);
     } catch (const std::runtime_error& e) {
         threw = std::string(e.what()).find("kv_cache_dtype") != std::string::npos;
@@ -321,10 +321,22 @@ static void test_errors() {
     convert_fp8(nullptr, nullptr, 1.0, 0, "fp8_e4m3", ScalarType::FLOAT16);  // nothing to convert
     threw = false;
     try {
-        reshape_and_cache_flash(nullptr, nullptr, nullptr, nullptr, nullptr, 0, 8, 128, 16, 0, "fp8_e5m2",
+        reshape_and_cache_flash(nullptr, nullptr, nullptr, nullptr, nullptr, 0, 8, 128, 16, 0, "int4",
                                 nullptr, nullptr, ScalarType::FLOAT16);
     } catch (const std::runtime_error& e) {
         threw = std::string(e.what()).find("kv_cache_dtype") != std::string::npos;
+    }
+    CHECK(threw);
+    // fp8 pages: no tokens is no work; a head_dim the fp8 append does not
+    // take is an argument error
+    reshape_and_cache(nullptr, nullptr, nullptr, nullptr, nullptr, 0, 8, 128, 16, 0, "fp8_e5m2", nullptr, nullptr,
+                      ScalarType::FLOAT16);
+    threw = false;
+    try {
+        reshape_and_cache(nullptr, nullptr, nullptr, nullptr, nullptr, 4, 8, 100, 16, 0, "fp8_e4m3", nullptr,
+                          nullptr, ScalarType::FLOAT16);
+    } catch (const std::runtime_error& e) {
+        threw = std::string(e.what()).find("vmc_reshape_and_cache_fp8") != std::string::npos;
     }
     CHECK(threw);
     TQWorkspace tw;

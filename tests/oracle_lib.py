@@ -82,6 +82,12 @@ def lib():
         L.orc_g32_decode_exact.argtypes = [_P, _P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int,
                                            C.c_double, C.c_int64, C.c_int64, C.c_int, C.c_uint64,
                                            C.c_int, C.c_int]
+        L.orc_f32_to_ofp8_n.argtypes = [_P, _P, C.c_int64, C.c_int]
+        L.orc_ofp8_to_f32.argtypes = [C.c_uint8, C.c_int]
+        L.orc_ofp8_to_f32.restype = C.c_float
+        L.orc_reshape_and_cache_fp8.argtypes = [_P, _P, C.c_int, _P, _P, _P, C.c_int, C.c_int, C.c_int,
+                                                C.c_int64, C.c_int64, C.c_float, C.c_float, C.c_int]
+        L.orc_convert_fp8.argtypes = [_P, _P, C.c_int, C.c_float, C.c_int64, C.c_int]
         L.orc_f32_to_fp8.argtypes = [C.c_float, C.c_int]
         L.orc_f32_to_fp8.restype = C.c_uint8
         L.orc_fp8_to_f32.argtypes = [C.c_uint8, C.c_int]
@@ -263,6 +269,36 @@ def g32_decode_exact(q_bits, cache, block_tables, seq_lens, Hkv, scale, block_si
                                _ptr(np.ascontiguousarray(seq_lens, dtype=np.int32)), B, Hq, Hkv, D,
                                scale, block_size, bt.shape[1], bits, seed, int(bf16), nthreads)
     return out
+
+
+def ofp8_encode(x, e5m2=False):
+    """OCP E4M3 / E5M2 bytes of fp32 values (round to nearest even, saturated)."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.zeros(x.shape, np.uint8)
+    lib().orc_f32_to_ofp8_n(_ptr(x), _ptr(y), x.size, int(e5m2))
+    return y
+
+
+def ofp8_decode(b, e5m2=False):
+    b = np.asarray(b, np.uint8)
+    return np.array([lib().orc_ofp8_to_f32(int(v), int(e5m2)) for v in b.ravel()],
+                    np.float32).reshape(b.shape)
+
+
+def reshape_and_cache_fp8(key_bits, value_bits, slot_mapping, kcache, vcache, block_size, k_scale=1.0,
+                          v_scale=1.0, hnd=False, src_bf16=False, stride=0):
+    T, H, D = key_bits.shape
+    lib().orc_reshape_and_cache_fp8(_ptr(np.ascontiguousarray(key_bits)), _ptr(np.ascontiguousarray(value_bits)),
+                                    int(src_bf16), _ptr(kcache), _ptr(vcache),
+                                    _ptr(np.ascontiguousarray(slot_mapping, dtype=np.int64)), T, H, D,
+                                    block_size, stride, float(k_scale), float(v_scale), int(hnd))
+
+
+def convert_fp8(src_bits, scale, e5m2=False, src_bf16=False):
+    src = np.ascontiguousarray(src_bits, np.uint16)
+    dst = np.zeros(src.shape, np.uint8)
+    lib().orc_convert_fp8(_ptr(dst), _ptr(src), int(src_bf16), float(scale), src.size, int(e5m2))
+    return dst
 
 
 def fp8_encode(x, e4b15=False):

@@ -56,6 +56,8 @@ def load():
     L.vmc_kv_entry_bytes.argtypes = [_I, _I]
     L.vmc_reshape_and_cache.restype = _I
     L.vmc_reshape_and_cache.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I64, _I64, _I, _I, _I, _P]
+    L.vmc_reshape_and_cache_fp8.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I64, _I64, _P, _P, _I, _I, _P]
+    L.vmc_convert_fp8.argtypes = [_P, _P, C.c_double, _I64, _I, _I, _P]
     L.vmc_paged_decode_workspace_size.restype = _SZ
     L.vmc_paged_decode_workspace_size.argtypes = [_I, _I, _I, _I, _I, _I, _I]
     L.vmc_paged_attention_decode.restype = _I
@@ -183,6 +185,28 @@ def reshape_and_cache(key, value, key_cache, value_cache, slot_mapping, block_si
                                       _ptr(slot_mapping), T, H, D, block_size, cache_stride,
                                       kv_format, _dtype_code(key), layout, _stream(stream))
     _check(rc, "vmc_reshape_and_cache")
+
+
+def reshape_and_cache_fp8(key, value, key_cache, value_cache, slot_mapping, block_size, k_scale=None,
+                          v_scale=None, layout=LAYOUT_NHD, cache_stride=0, stream=None):
+    """vmc_reshape_and_cache_fp8: E4M3 pages of key / k_scale and value / v_scale
+    (scales are host floats, None = 1)."""
+    T, H, D = key.shape
+    ks = C.c_float(k_scale) if k_scale is not None else None
+    vs = C.c_float(v_scale) if v_scale is not None else None
+    rc = load().vmc_reshape_and_cache_fp8(_ptr(key), _ptr(value), _ptr(key_cache), _ptr(value_cache),
+                                          _ptr(slot_mapping), T, H, D, block_size, cache_stride,
+                                          C.byref(ks) if ks is not None else None,
+                                          C.byref(vs) if vs is not None else None,
+                                          _dtype_code(key), layout, _stream(stream))
+    _check(rc, "vmc_reshape_and_cache_fp8")
+
+
+def convert_fp8(dst, src, scale, e5m2=False, stream=None):
+    """vmc_convert_fp8: dst (uint8, src.numel() bytes) = fp8(src * scale)."""
+    rc = load().vmc_convert_fp8(_ptr(dst), _ptr(src), float(scale), src.numel(), int(bool(e5m2)),
+                                _dtype_code(src), _stream(stream))
+    _check(rc, "vmc_convert_fp8")
 
 
 def paged_decode_workspace_size(batch, num_heads, num_kv_heads, head_dim=128, max_blocks=0,

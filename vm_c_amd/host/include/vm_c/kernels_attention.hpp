@@ -57,9 +57,10 @@ void reshape_and_cache_flash(const void* key, const void* value, void* key_cache
                              const void* v_scale, ScalarType dtype, hipStream_t stream = nullptr,
                              const std::string& layout = "nhd");
 
-// kernels_cache.h:41-46 (cache_kernels.cu:160-200): fp8 KV caches are not
-// carried (reshape_and_cache rejects the fp8 dtype strings too); throws
-// std::runtime_error naming the call.
+// kernels_cache.h:41-46 (cache_kernels.cu:175-212): dst = fp8(src * scale),
+// OCP E4M3 for "fp8_e4m3", E5M2 otherwise (vmc_convert_fp8).  reshape_and_cache
+// above writes E4M3 pages for "fp8_e4m3" and "fp8_e5m2" (x / k_scale, x /
+// v_scale; the scales are host float pointers, null = 1).
 void convert_fp8(void* dst_cache, const void* src_cache, double scale, int64_t num_elements,
                  const std::string& kv_cache_dtype, ScalarType dtype, hipStream_t stream = nullptr);
 

@@ -241,7 +241,15 @@ void reshape_and_cache(const void* key, const void* value, void* key_cache, void
                        int64_t block_size, int64_t cache_stride, const std::string& kv_cache_dtype,
                        const void* k_scale, const void* v_scale, ScalarType dtype,
                        hipStream_t stream, const std::string& layout) {
-    if (k_scale || v_scale) throw std::runtime_error("reshape_and_cache: fp8 k/v scales are not supported");
+    if (kv_cache_dtype == "fp8_e4m3" || kv_cache_dtype == "fp8_e5m2") {
+        // both strings store E4M3 bytes of x / scale (cache_kernels.cu:101-120)
+        VMC_CALL(vmc_reshape_and_cache_fp8(key, value, key_cache, value_cache, slot_mapping, num_tokens,
+                                           num_kv_heads, head_dim, block_size, cache_stride,
+                                           static_cast<const float*>(k_scale), static_cast<const float*>(v_scale),
+                                           vmc_dtype_of(dtype), vmc_layout_of(layout), stream));
+        return;
+    }
+    // the scales only apply to fp8 caches (cache_kernels.cu:42-51)
     VMC_CALL(vmc_reshape_and_cache(key, value, key_cache, value_cache, slot_mapping, num_tokens,
                                    num_kv_heads, head_dim, block_size, cache_stride,
                                    vmc_kv_format_of(kv_cache_dtype, dtype), vmc_dtype_of(dtype),
@@ -259,13 +267,10 @@ void reshape_and_cache_flash(const void* key, const void* value, void* key_cache
 
 void convert_fp8(void* dst_cache, const void* src_cache, double scale, int64_t num_elements,
                  const std::string& kv_cache_dtype, ScalarType dtype, hipStream_t stream) {
-    (void)dst_cache;
-    (void)src_cache;
-    (void)scale;
-    (void)dtype;
-    (void)stream;
-    if (num_elements <= 0) return;  // as the reference: nothing to convert
-    throw std::runtime_error("convert_fp8: fp8 KV caches (" + kv_cache_dtype + ") are not supported");
+    if (num_elements <= 0) return;  // cache_kernels.cu:193
+    // "fp8_e4m3" -> E4M3, any other string -> E5M2 (cache_kernels.cu:196-211)
+    VMC_CALL(vmc_convert_fp8(dst_cache, src_cache, scale, num_elements, kv_cache_dtype == "fp8_e4m3" ? 0 : 1,
+                             vmc_dtype_of(dtype), stream));
 }
 
 void paged_attention_prefill(void* out, const void* query, const void* key_cache,
