@@ -54,6 +54,9 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kBs = 16;
+// split partial rows: o[128], m, l, two floats of padding (528 B, so a row
+// starts 16-byte aligned and takes 16-byte stores)
+constexpr int kPartRow = kD + 4;
 constexpr float kNegInf = -__builtin_inff();
 
 // FMT_G4 / FMT_G3: the per-32-group variant (no reference counterpart): one
@@ -227,7 +230,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // Combines the pieces of every sequence that range boundaries cut.  Grid
-// (B, Hkv), one wave per query head of the KV head.  Rows hold D + 2 floats:
+// (B, Hkv), one wave per query head of the KV head.  Rows hold kPartRow floats:
 // o unnormalised, m, l (log2 domain); out = sum_s o_s 2^(m_s - M) /
 // sum_s l_s 2^(m_s - M), M = max_s m_s.  Pieces of sequence b: workgroups
 // w0..w1 (those holding its first and last page); w0 wrote slot 2 w0 + 1,
@@ -267,10 +270,10 @@ __global__ void __launch_bounds__(1024) decode_merge_kernel(DecodeParams p) {
     const int w0 = wg_of_page(ps, n, T), w1 = wg_of_page(ps + pg - 1, n, T);
     if (w0 == w1) return;  // written by its workgroup
     const int nseg = w1 - w0 + 1;
-    const int64_t rs = (int64_t)p.Hq * (kD + 2);
+    const int64_t rs = (int64_t)p.Hq * kPartRow;
     auto row = [&](int s) {  // piece s = workgroup w0 + s
         const int slot = s == 0 ? 2 * w0 + 1 : 2 * (w0 + s);
-        return p.part + slot * rs + (int64_t)hq * (kD + 2);
+        return p.part + slot * rs + (int64_t)hq * kPartRow;
     };
     // one pass over the pieces, 64 at a time, with a running max: the m / l
     // pair of each piece and the first 16 pieces' o rows are loaded together,
@@ -410,11 +413,11 @@ inline int d256_ranges(int B, int Hkv, int max_blocks, int max_splits, int cus) 
     return (int)std::max<int64_t>(1, n);
 }
 
-// split partials of the head_dim-256 TurboQuant decode: two rows of 256 + 2
+// split partials of the head_dim-256 TurboQuant decode: two rows of 256 + 4
 // floats per page range
 inline size_t workspace_bytes_d256(int B, int Hq, int Hkv, int max_blocks, int max_splits, int cus) {
     if (max_splits == 1) return 0;
-    return (size_t)2 * d256_ranges(B, Hkv, max_blocks, max_splits, cus) * Hq * (256 + 2) * sizeof(float);
+    return (size_t)2 * d256_ranges(B, Hkv, max_blocks, max_splits, cus) * Hq * (256 + 4) * sizeof(float);
 }
 
 // split partials: two rows per page range of the largest grid any decode
@@ -423,7 +426,7 @@ inline size_t workspace_bytes_for(int B, int Hq, int Hkv, int max_blocks, int ma
     if (max_splits == 1) return 0;
     const int n = std::max(flat_grid(B, Hkv, max_blocks, max_splits, cus),
                            tq_stream_ranges(B, Hkv, max_blocks, max_splits, cus));
-    return (size_t)2 * n * Hq * (kD + 2) * sizeof(float);
+    return (size_t)2 * n * Hq * kPartRow * sizeof(float);
 }
 
 // The pipelined TurboQuant decode (tq_decode.hip): reference slot layout,

@@ -354,13 +354,15 @@ __global__ void __launch_bounds__(512) tq_decode_kernel(DecodeParams p) {
                 uint16_t* o = reinterpret_cast<uint16_t*>(p.out) + ((int64_t)b * p.Hq + hq) * kD + 8 * r16;
                 *reinterpret_cast<u32x4*>(o) = u32x4{wd[0], wd[1], wd[2], wd[3]};
             } else {
-                float* o = p.part + ((int64_t)slot * p.Hq + hq) * (kD + 2);
+                float* o = p.part + ((int64_t)slot * p.Hq + hq) * kPartRow;
                 float* od = o + 8 * r16;
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    *reinterpret_cast<float2*>(od + 2 * e) =
-                        make_float2(__builtin_fmaf(oacc[2 * e][i], vscale(2 * e), zh),
-                                    __builtin_fmaf(oacc[2 * e + 1][i], vscale(2 * e + 1), zh));
+                for (int h2 = 0; h2 < 2; ++h2) {
+                    f32x4 v;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = __builtin_fmaf(oacc[4 * h2 + e][i], vscale(4 * h2 + e), zh);
+                    *reinterpret_cast<f32x4*>(od + 4 * h2) = v;
+                }
                 if (r16 == 0) *reinterpret_cast<float2*>(o + kD) = make_float2(mh, lh);
             }
         }

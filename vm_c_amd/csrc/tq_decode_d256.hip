@@ -35,7 +35,8 @@ namespace vmc {
 namespace {
 
 constexpr int kD2 = 256;
-constexpr int kPages2 = 64;  // pages per staged slice of a stream's block table
+constexpr int kPages2 = 64;
+constexpr int kPartRow2 = kD2 + 4;  // split partial row: o[256], m, l, padding to 16 bytes  // pages per staged slice of a stream's block table
 
 template <int KB, int HK>
 struct D2Geo {
@@ -276,7 +277,7 @@ __global__ void __launch_bounds__(512, 1) tq_decode_d256_kernel(DecodeParams p) 
         const f32x4 zh4 = gather4_from_row0(z_tot, wscr + 16, r16, grp);
         const f32x4 mh4 = gather4_from_row0(m_run, wscr + 32, r16, grp);
         uint8_t* const obase = reinterpret_cast<uint8_t*>(p.out) + ((int64_t)b * p.Hq + hq0) * (2 * kD2);
-        uint8_t* const pbase = reinterpret_cast<uint8_t*>(p.part) + ((int64_t)slot * p.Hq + hq0) * (4 * (kD2 + 2));
+        uint8_t* const pbase = reinterpret_cast<uint8_t*>(p.part) + ((int64_t)slot * p.Hq + hq0) * (4 * kPartRow2);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int hh = 4 * grp + i;
@@ -298,17 +299,19 @@ __global__ void __launch_bounds__(512, 1) tq_decode_d256_kernel(DecodeParams p) 
                 store_done2(v0);
                 store_done2(v1);
             } else {
-                const uint32_t off = (uint32_t)(hh * (4 * (kD2 + 2)) + 64 * r16);
+                const uint32_t off = (uint32_t)(hh * (4 * kPartRow2) + 64 * r16);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    u32x2 v = {__builtin_bit_cast(uint32_t, __builtin_fmaf(oacc[2 * e][i], kVScale<FMT_TQ, KB>(2 * e & 7), zh)),
-                               __builtin_bit_cast(uint32_t, __builtin_fmaf(oacc[2 * e + 1][i], kVScale<FMT_TQ, KB>((2 * e + 1) & 7), zh))};
-                    *reinterpret_cast<u32x2*>(pbase + off + 8 * e) = v;
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    u32x4 v;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        v[e] = __builtin_bit_cast(uint32_t, __builtin_fmaf(oacc[4 * q4 + e][i], kVScale<FMT_TQ, KB>((4 * q4 + e) & 7), zh));
+                    *reinterpret_cast<u32x4*>(pbase + off + 16 * q4) = v;
                     store_done2(v);
                 }
                 if (r16 == 0) {
                     u32x2 v = {__builtin_bit_cast(uint32_t, mh), __builtin_bit_cast(uint32_t, lh)};
-                    *reinterpret_cast<u32x2*>(pbase + (uint32_t)(hh * (4 * (kD2 + 2)) + 4 * kD2)) = v;
+                    *reinterpret_cast<u32x2*>(pbase + (uint32_t)(hh * (4 * kPartRow2) + 4 * kD2)) = v;
                     store_done2(v);
                 }
             }
@@ -570,7 +573,7 @@ __global__ void __launch_bounds__(512, 1) tq_decode_d256_kernel(DecodeParams p) 
 }
 
 // Combines the pieces of sequences cut by range boundaries (head_dim 256):
-// decode_merge_kernel's rule over rows of 256 + 2 floats (o unnormalised, m,
+// decode_merge_kernel's rule over rows of kPartRow2 floats (o unnormalised, m,
 // l).  Grid (B, Hq), 4 waves per (sequence, query head): wave w takes pieces
 // w, w + 4, ... (sixteen rows in flight), lane l dims 4 l .. + 3; the four
 // partial sums are combined through LDS.
@@ -599,10 +602,10 @@ __global__ void __launch_bounds__(256) decode_merge_d256_kernel(DecodeParams p) 
     const int w0 = wg_of_page(ps_b, n, T), w1 = wg_of_page(ps_b + pg_b - 1, n, T);
     if (w0 == w1) return;  // written by its range
     const int nseg = w1 - w0 + 1;
-    const int64_t rs = (int64_t)p.Hq * (kD2 + 2);
+    const int64_t rs = (int64_t)p.Hq * kPartRow2;
     auto row = [&](int s) {  // piece s = range w0 + s
         const int slot = s == 0 ? 2 * w0 + 1 : 2 * (w0 + s);
-        return p.part + slot * rs + (int64_t)hq * (kD2 + 2);
+        return p.part + slot * rs + (int64_t)hq * kPartRow2;
     };
     float M = kNegInf, L = 0.0f;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};

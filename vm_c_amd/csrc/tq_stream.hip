@@ -285,7 +285,7 @@ __global__ void __launch_bounds__(512, 4) tq_stream_kernel(DecodeParams p) {
         // uniform row bases (scalar) plus 32-bit lane offsets: head hq0 + 4 grp
         // + i, dims 8 r16 .. + 7 (only lane groups 0 and 1 hold heads < 8)
         uint8_t* const obase = reinterpret_cast<uint8_t*>(p.out) + ((int64_t)b * p.Hq + hq0) * (2 * kD);
-        uint8_t* const pbase = reinterpret_cast<uint8_t*>(p.part) + ((int64_t)slot * p.Hq + hq0) * (4 * (kD + 2));
+        uint8_t* const pbase = reinterpret_cast<uint8_t*>(p.part) + ((int64_t)slot * p.Hq + hq0) * (4 * kPartRow);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int hh = 4 * grp + i;
@@ -305,17 +305,19 @@ __global__ void __launch_bounds__(512, 4) tq_stream_kernel(DecodeParams p) {
                 *reinterpret_cast<u32x4*>(obase + off) = v;
                 store_done(v);
             } else {
-                const uint32_t off = (uint32_t)(hh * (4 * (kD + 2)) + 32 * r16);
+                const uint32_t off = (uint32_t)(hh * (4 * kPartRow) + 32 * r16);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    u32x2 v = {__builtin_bit_cast(uint32_t, __builtin_fmaf(oacc[2 * e][i], kVScale<FMT_TQ, VB>(2 * e), zh)),
-                               __builtin_bit_cast(uint32_t, __builtin_fmaf(oacc[2 * e + 1][i], kVScale<FMT_TQ, VB>(2 * e + 1), zh))};
-                    *reinterpret_cast<u32x2*>(pbase + off + 8 * e) = v;
+                for (int h2 = 0; h2 < 2; ++h2) {
+                    u32x4 v;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        v[e] = __builtin_bit_cast(uint32_t, __builtin_fmaf(oacc[4 * h2 + e][i], kVScale<FMT_TQ, VB>(4 * h2 + e), zh));
+                    *reinterpret_cast<u32x4*>(pbase + off + 16 * h2) = v;
                     store_done(v);
                 }
                 if (r16 == 0) {
                     u32x2 v = {__builtin_bit_cast(uint32_t, mh), __builtin_bit_cast(uint32_t, lh)};
-                    *reinterpret_cast<u32x2*>(pbase + (uint32_t)(hh * (4 * (kD + 2)) + 4 * kD)) = v;
+                    *reinterpret_cast<u32x2*>(pbase + (uint32_t)(hh * (4 * kPartRow) + 4 * kD)) = v;
                     store_done(v);
                 }
             }

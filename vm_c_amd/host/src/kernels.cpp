@@ -170,11 +170,11 @@ void TQWorkspace::ensure_decode(int batch_size, int num_heads, int num_kv_heads,
 }
 
 void TQWorkspace::ensure_decode(int bhq, int head_dim, int num_kv_splits, int device) {
-    // the decode's split partials are fp32 rows of head_dim + 2 floats, at
+    // the decode's split partials are fp32 rows of head_dim + 4 floats, at
     // most two per launched workgroup and query head, with at most
     // batch x num_kv_splits workgroups (vmc_turboquant_decode_workspace_size)
     if (bhq <= 0 || num_kv_splits <= 1 || (head_dim != 128 && head_dim != 256)) return;
-    const size_t need = (size_t)2 * (size_t)num_kv_splits * (size_t)bhq * (size_t)(head_dim + 2) * sizeof(float);
+    const size_t need = (size_t)2 * (size_t)num_kv_splits * (size_t)bhq * (size_t)(head_dim + 4) * sizeof(float);
     if (need <= decode_bytes) return;
     HIP_CHECK(hipSetDevice(device));
     if (decode_workspace) HIP_CHECK(hipFree(decode_workspace));
