@@ -63,7 +63,7 @@ int vmc_reshape_and_cache(const void* key, const void* value, void* key_cache,
 
 /*
  * fp8 pages: reshape_and_cache with kv_cache_dtype "fp8_e4m3" or "fp8_e5m2"
- * (src/cuda/cache_kernels.cu:101-120, :14-54).  Both strings store OCP FP8
+ * (src/cuda/cache_kernels.cu:101-131, :14-54).  Both strings store OCP FP8
  * E4M3 bytes (the reference casts to __nv_fp8_e4m3 for either): one byte per
  * value, x / k_scale for K and x / v_scale for V, rounded to nearest even and
  * saturated to +-448 (NaN -> 0x7f).  Page addressing and slot_mapping as in

@@ -65,7 +65,7 @@ uint8_t orc_f32_to_ofp8(float x, int e5m2);
 void    orc_f32_to_ofp8_n(const float* x, uint8_t* y, int64_t n, int e5m2);
 float   orc_ofp8_to_f32(uint8_t b, int e5m2);
 /* reshape_and_cache with kv_cache_dtype "fp8_e4m3" or "fp8_e5m2"
- * (cache_kernels.cu:101-120, :14-54): both write E4M3 bytes of x / scale
+ * (cache_kernels.cu:101-131, :14-54): both write E4M3 bytes of x / scale
  * (the reference casts to __nv_fp8_e4m3 for either string); one byte per
  * value; page addressing as orc_kv_append with E = head_dim and the block
  * stride `stride` bytes (0 = bs*Hkv*head_dim). */

@@ -1,5 +1,5 @@
 """fp8 pages on the GPU: vmc_reshape_and_cache_fp8 (reshape_and_cache with
-kv_cache_dtype "fp8_e4m3" / "fp8_e5m2", cache_kernels.cu:101-120) and
+kv_cache_dtype "fp8_e4m3" / "fp8_e5m2", cache_kernels.cu:101-131) and
 vmc_convert_fp8 (convert_fp8, cache_kernels.cu:175-212), every byte equal
 to the oracle's restatement of the OCP FP8 conversion (which
 tests/test_oracle_ofp8.py pins by exhaustive search).  Inputs hold values

@@ -242,7 +242,7 @@ void reshape_and_cache(const void* key, const void* value, void* key_cache, void
                        const void* k_scale, const void* v_scale, ScalarType dtype,
                        hipStream_t stream, const std::string& layout) {
     if (kv_cache_dtype == "fp8_e4m3" || kv_cache_dtype == "fp8_e5m2") {
-        // both strings store E4M3 bytes of x / scale (cache_kernels.cu:101-120)
+        // both strings store E4M3 bytes of x / scale (cache_kernels.cu:101-131)
         VMC_CALL(vmc_reshape_and_cache_fp8(key, value, key_cache, value_cache, slot_mapping, num_tokens,
                                            num_kv_heads, head_dim, block_size, cache_stride,
                                            static_cast<const float*>(k_scale), static_cast<const float*>(v_scale),
