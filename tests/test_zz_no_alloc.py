@@ -3,8 +3,9 @@ partials live in the library's own device array): through the C ABI, its
 output equals vmc_turboquant_decode_attention's with a caller workspace, bit
 for bit (same kernels, same split), on two calls in a row -- the second with a
 smaller batch and shorter contexts, so stale rows of the first call are in the
-array -- for fp16 and bf16 activations; and a shape whose partials exceed the
-array is rejected with VMC_ENOMEM before any launch."""
+array -- for fp16 and bf16 activations and for the head_dim-256 decode; and
+a shape whose partials exceed the array is rejected with VMC_ENOMEM before
+any launch."""
 import numpy as np
 import pytest
 
@@ -46,11 +47,37 @@ def test_noalloc_decode_matches_workspace_decode(dev, bf16):
             f"noalloc decode differs from the workspace decode (B={w.B})"
 
 
-@pytest.mark.parametrize("D,Hq,Hkv", [(256, 16, 4), (128, 64, 2)])
+@pytest.mark.parametrize("method", ["turboquant_4bit_nc", "turboquant_3bit_nc"])
+def test_noalloc_d256_decode_matches_workspace_decode(dev, method):
+    """head_dim 256 with 1, 2 or 4 KV heads runs the MFMA decode whose split
+    partials are rows of 256 + 4 floats; the array holds them as well: bit for
+    bit against the workspace entry point on two calls in a row, the second
+    with a smaller batch, fewer heads and shorter contexts."""
+    import torch
+    from vm_c_amd import capi
+    cfg = capi.tq_config(256, method)
+    big = make_workload([9000, 300, 4100, 16], Hq=16, Hkv=2, D=256, seed=24)
+    small = make_workload([700, 20], Hq=8, Hkv=1, D=256, seed=25)
+    for w in (big, small):
+        cache, q = _pages(dev, w, cfg, False)
+        bt = torch.from_numpy(w.bt).to(dev)
+        sl = torch.from_numpy(w.seq_lens).to(dev)
+        ref = torch.full_like(q, float("nan"))
+        capi.turboquant_decode_attention(ref, q, cache, bt, sl, w.Hkv, float(w.scale), cfg, BS)
+        got = torch.full_like(q, float("nan"))
+        capi.turboquant_decode_attention_noalloc(got, q, cache, bt, sl, w.Hkv, float(w.scale), cfg, BS)
+        torch.cuda.synchronize()
+        assert torch.isfinite(ref.float()).all()
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), \
+            f"noalloc head_dim-256 decode differs from the workspace decode (B={w.B})"
+
+
+@pytest.mark.parametrize("D,Hq,Hkv", [(256, 16, 8), (128, 64, 2)])
 def test_noalloc_one_wave_per_row_shapes(dev, D, Hq, Hkv):
-    """head_dim 256 and 32 query heads per KV head run the one-wave-per-row
-    kernel, which needs no split partials: the allocation-free entry point
-    takes them at any size and matches the workspace entry point."""
+    """head_dim 256 with 8 KV heads and 32 query heads per KV head run the
+    one-wave-per-row kernel, which needs no split partials: the
+    allocation-free entry point takes them at any size and matches the
+    workspace entry point."""
     import torch
     from vm_c_amd import capi
     cfg = capi.tq_config(D, "turboquant_4bit_nc")
