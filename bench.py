@@ -293,7 +293,8 @@ def bench_decode_cfg(args, torch, capi, dev, kind):
 
 def bench_prefill(args, torch, capi, dev):
     """Causal prefill of 4 x 4096 tokens, 32/8 heads, bf16, the q8_0 pages
-    written in the same launch.  Sets of q/k/v/out/pages (370 MB each) are
+    written in the same launch (vmc_flash_attention_prefill_ws: the V^T
+    tiles built by a first launch into a workspace, both launches timed).  Sets of q/k/v/out/pages (370 MB each) are
     replicated past 1 GiB and rotated, so the 256 MB last-level cache holds
     no set from one call to the next."""
     B, S, Hq, Hkv = 4, 4096, 32, 8
@@ -317,12 +318,14 @@ def bench_prefill(args, torch, capi, dev):
     slots = (perm[t // BS] * BS + t % BS).to(torch.int64)
     scale = 1.0 / math.sqrt(D)
     stream = torch.cuda.current_stream()
+    # the call's V^T tiles (vmc_flash_attention_prefill_ws), allocated once
+    ws = torch.empty(capi.flash_attention_prefill_workspace_size(T, Hkv, D), dtype=torch.uint8, device=dev)
 
     def run(i):
         q, k, v, out, kc, vc = sets[i % nset]
         capi.flash_attention_prefill(out, q, k, v, pos, Hkv, scale, key_cache=kc, value_cache=vc,
                                      slot_mapping=slots, block_size=BS, kv_format=capi.KV_Q8_0,
-                                     stream=stream)
+                                     stream=stream, workspace=ws)
 
     n = max(20, args.steps)
     ms, med = time_loop(torch, run, n, max(2, args.warmup // 2), stream)

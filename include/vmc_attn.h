@@ -382,6 +382,30 @@ int vmc_flash_attention_prefill(void* output, const void* query, const void* key
                                 vmc_stream_t stream);
 
 /*
+ * vmc_flash_attention_prefill with a caller workspace (no counterpart in the
+ * reference, whose prefill takes none): the same arguments and results, plus
+ * workspace / workspace_bytes, at least
+ * vmc_flash_attention_prefill_workspace_size(num_tokens, num_kv_heads,
+ * head_dim) bytes, 16-byte aligned (VMC_ENOMEM when smaller, VMC_EINVAL when
+ * NULL at head_dim 128).  A first launch writes the fp16 V^T tiles of the
+ * step's V (16 KB per 64 keys and KV head) into the workspace once, so the
+ * attention kernel fetches them instead of transposing V in every
+ * workgroup that reads it.  Outputs equal vmc_flash_attention_prefill's bit
+ * for bit, except that bf16 V which that function would run in its exact
+ * mode for some workgroups may run exact in more of them here (a tile's
+ * flag covers all of its rows).  head_dim 64 / 256 ignore the workspace.
+ * Concurrent calls on one workspace race.
+ */
+size_t vmc_flash_attention_prefill_workspace_size(int num_tokens, int num_kv_heads, int head_dim);
+int vmc_flash_attention_prefill_ws(void* output, const void* query, const void* key,
+                                   const void* value, int num_tokens, int num_heads,
+                                   int num_kv_heads, int head_dim, float scale,
+                                   const int32_t* token_positions, int dtype, void* key_cache,
+                                   void* value_cache, const int64_t* slot_mapping,
+                                   int64_t block_size, int kv_format, int layout, void* workspace,
+                                   size_t workspace_bytes, vmc_stream_t stream);
+
+/*
  * Measurement only (no counterpart in the reference): one streaming read of
  * bytes (a multiple of 16) at src (16-byte aligned).  mode 0: 16-byte
  * non-temporal vector loads into registers (sink: 1 KB of device memory the

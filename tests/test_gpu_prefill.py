@@ -1,6 +1,9 @@
 """Causal prefill parity on the GPU: HIP MFMA prefill vs exact fp64 causal
 attention (oracle), tolerance |got - ref| <= 2e-3 + 1e-2 |ref|; the fused
-quantize-on-append must write the same bytes as the standalone append."""
+quantize-on-append must write the same bytes as the standalone append.  Each
+case runs through vmc_flash_attention_prefill and, with a workspace of
+prebuilt V^T tiles, through vmc_flash_attention_prefill_ws, whose outputs
+must equal the first's bit for bit wherever neither runs the exact mode."""
 import os
 
 import numpy as np
@@ -18,7 +21,7 @@ def _inputs(seq_lens, Hq, Hkv, D=128, seed=0, bf16=True):
     return prefill_inputs(seq_lens, Hq, Hkv, D=D, seed=seed, bf16=bf16)
 
 
-def _run(dev, qb, kb, vb, pos, Hkv, scale, bf16=True, append=None):
+def _run(dev, qb, kb, vb, pos, Hkv, scale, bf16=True, append=None, ws=False):
     import torch
     from vm_c_amd import capi
     tdt = torch.bfloat16 if bf16 else torch.float16
@@ -26,11 +29,15 @@ def _run(dev, qb, kb, vb, pos, Hkv, scale, bf16=True, append=None):
     q, k, v = to(qb), to(kb), to(vb)
     out = torch.full_like(q, float("nan"))
     kw = {}
+    if ws:
+        n = capi.flash_attention_prefill_workspace_size(q.shape[0], Hkv, q.shape[2])
+        # stale bytes from an earlier use must not matter
+        kw["workspace"] = torch.full((n,), 0xA5, dtype=torch.uint8, device=dev)
     if append is not None:
         fmt, slots, nbytes = append
         kc = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
         vc = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
-        kw = dict(key_cache=kc, value_cache=vc, slot_mapping=torch.from_numpy(slots).to(dev),
+        kw.update(key_cache=kc, value_cache=vc, slot_mapping=torch.from_numpy(slots).to(dev),
                   block_size=BS, kv_format=fmt)
     capi.flash_attention_prefill(out, q, k, v, torch.from_numpy(pos).to(dev), Hkv, scale, **kw)
     torch.cuda.synchronize()
@@ -40,14 +47,15 @@ def _run(dev, qb, kb, vb, pos, Hkv, scale, bf16=True, append=None):
     return res
 
 
+@pytest.mark.parametrize("ws", [False, True])
 @pytest.mark.parametrize("bf16", [True, False])
 @pytest.mark.parametrize("seq_lens,Hq,Hkv", [([300, 77], 8, 2), ([1, 2, 129, 64, 200], 4, 4),
-                                              ([513], 8, 1)])
-def test_prefill_all_rows_vs_exact(dev, bf16, seq_lens, Hq, Hkv):
+                                              ([513], 8, 1), ([256, 64, 192], 8, 2)])
+def test_prefill_all_rows_vs_exact(dev, bf16, seq_lens, Hq, Hkv, ws):
     qb, kb, vb, pos, cu = _inputs(seq_lens, Hq, Hkv, seed=len(seq_lens), bf16=bf16)
     T = qb.shape[0]
     scale = 1.0 / np.sqrt(128)
-    got = _run(dev, qb, kb, vb, pos, Hkv, scale, bf16=bf16)
+    got = _run(dev, qb, kb, vb, pos, Hkv, scale, bf16=bf16, ws=ws)
     toks = np.repeat(np.arange(T), Hq)
     heads = np.tile(np.arange(Hq), T)
     ex = O.prefill_exact_rows(qb, kb, vb, cu, Hkv, scale, toks, heads, is_bf16=bf16)
@@ -63,8 +71,9 @@ def _slots_for(T, seed):
     return perm[t // BS] * BS + t % BS, nblk
 
 
+@pytest.mark.parametrize("ws", [False, True])
 @pytest.mark.parametrize("fmt", [O.KV_Q8_0, O.KV_Q4_0, O.KV_F16, O.KV_BF16])
-def test_prefill_fused_append_bitexact(dev, fmt):
+def test_prefill_fused_append_bitexact(dev, fmt, ws):
     seq_lens, Hq, Hkv = [333, 190], 8, 2
     qb, kb, vb, pos, cu = _inputs(seq_lens, Hq, Hkv, seed=13)
     T = qb.shape[0]
@@ -72,7 +81,7 @@ def test_prefill_fused_append_bitexact(dev, fmt):
     slots[7] = -1
     E = O.entry_bytes(fmt, 128)
     nbytes = nblk * BS * Hkv * E
-    got, kc, vc = _run(dev, qb, kb, vb, pos, Hkv, 1.0 / np.sqrt(128), append=(fmt, slots, nbytes))
+    got, kc, vc = _run(dev, qb, kb, vb, pos, Hkv, 1.0 / np.sqrt(128), append=(fmt, slots, nbytes), ws=ws)
     kr = np.zeros(nbytes, np.uint8)
     vr = np.zeros(nbytes, np.uint8)
     O.kv_append(kb, vb, slots, kr, vr, BS, fmt, src_bf16=True)
@@ -91,7 +100,11 @@ def test_prefill_config4_full_size(dev):
     E = O.entry_bytes(O.KV_Q8_0, 128)
     nbytes = nblk * BS * Hkv * E
     scale = 1.0 / np.sqrt(128)
-    got, kc, vc = _run(dev, qb, kb, vb, pos, Hkv, scale, append=(O.KV_Q8_0, slots, nbytes))
+    got, kc, vc = _run(dev, qb, kb, vb, pos, Hkv, scale, append=(O.KV_Q8_0, slots, nbytes), ws=True)
+    # the workspace path (prebuilt V^T tiles, the benchmark's) equals the
+    # in-kernel one bit for bit on this input
+    got0 = _run(dev, qb, kb, vb, pos, Hkv, scale)
+    assert np.array_equal(got.view(np.uint32), got0.view(np.uint32))
     # 8,256 rows against fp64 attention: every head of 256 random tokens and
     # of the first and last token of each sequence
     rng = np.random.default_rng(0)
@@ -113,7 +126,8 @@ def test_prefill_config4_full_size(dev):
     assert np.array_equal(kc, kr) and np.array_equal(vc, vr)
 
 
-def test_prefill_bf16_v_outside_fp16_range(dev):
+@pytest.mark.parametrize("ws", [False, True])
+def test_prefill_bf16_v_outside_fp16_range(dev, ws):
     """bf16 V that fp16 cannot hold: one sequence at 2^100 scale (fp16
     overflows), one at 2^-20 (fp16 subnormals keep 4 bits) with bf16
     subnormals mixed in, one N(0,1) with sparse +-1e30 and +-1e-38 spikes
@@ -141,7 +155,7 @@ def test_prefill_bf16_v_outside_fp16_range(dev):
         v[cu[b]:cu[b + 1]] = seg.reshape(v[cu[b]:cu[b + 1]].shape)
     vb = f32_to_bf16_bits(v.astype(np.float32))
     scale = 1.0 / np.sqrt(128)
-    got = _run(dev, qb, kb, vb, pos, Hkv, scale).reshape(T * Hq, 128)
+    got = _run(dev, qb, kb, vb, pos, Hkv, scale, ws=ws).reshape(T * Hq, 128)
     assert np.isfinite(got).all()
     toks = np.repeat(np.arange(T), Hq)
     heads = np.tile(np.arange(Hq), T)
@@ -151,3 +165,36 @@ def test_prefill_bf16_v_outside_fp16_range(dev):
         sel = (toks >= cu[b]) & (toks < cu[b + 1])
         ok, err = close_report(got[sel] / rs[sel], ex[sel] / rs[sel], ATOL, RTOL)
         assert ok, f"sequence {b}: max scaled err {err}"
+
+
+@pytest.mark.parametrize("bf16", [True, False])
+@pytest.mark.parametrize("seq_lens,Hq,Hkv", [([256, 512, 64, 128], 8, 2), ([300, 77, 129], 4, 1),
+                                              ([1000, 24], 32, 8)])
+def test_prefill_ws_equals_in_kernel_transpose(dev, bf16, seq_lens, Hq, Hkv):
+    """Prebuilt V^T tiles (sequences starting on 64-key boundaries) and the
+    in-kernel pass (the others) give the same bits."""
+    qb, kb, vb, pos, cu = _inputs(seq_lens, Hq, Hkv, seed=31, bf16=bf16)
+    scale = 1.0 / np.sqrt(128)
+    a = _run(dev, qb, kb, vb, pos, Hkv, scale, bf16=bf16)
+    b = _run(dev, qb, kb, vb, pos, Hkv, scale, bf16=bf16, ws=True)
+    assert np.isfinite(a).all()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_prefill_ws_fp16_inf_in_a_shared_tile(dev):
+    """fp16 V with an inf in the second sequence, which shares a 64-key tile
+    with the first: the tile's flag sends the workgroups that read it to
+    the in-kernel pass, so the two paths agree bit for bit; the first
+    sequence's rows of other tiles and the third sequence (no shared tile)
+    stay finite.  (Rows whose tile holds the inf, masked or not, are not
+    finite on either path: 0 * inf in the P . V product.)"""
+    seq_lens, Hq, Hkv = [100, 28, 64], 8, 2
+    qb, kb, vb, pos, cu = _inputs(seq_lens, Hq, Hkv, seed=33, bf16=False)
+    vb = vb.copy()
+    vb[cu[1] + 3, 1, 17] = 0x7C00  # +inf, second sequence, KV head 1
+    scale = 1.0 / np.sqrt(128)
+    a = _run(dev, qb, kb, vb, pos, Hkv, scale, bf16=False)
+    b = _run(dev, qb, kb, vb, pos, Hkv, scale, bf16=False, ws=True)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.isfinite(b[:64]).all() and np.isfinite(b[cu[2]:cu[3]]).all()
+    assert np.isfinite(b[cu[0]:cu[1], :4]).all()  # query heads of KV head 0

@@ -97,6 +97,11 @@ def load():
     L.vmc_flash_attention_prefill.restype = _I
     L.vmc_flash_attention_prefill.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P, _P,
                                               _P, _I64, _I, _I, _P]
+    L.vmc_flash_attention_prefill_workspace_size.restype = _SZ
+    L.vmc_flash_attention_prefill_workspace_size.argtypes = [_I, _I, _I]
+    L.vmc_flash_attention_prefill_ws.restype = _I
+    L.vmc_flash_attention_prefill_ws.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _I, _P, _P,
+                                                 _P, _I64, _I, _I, _P, _SZ, _P]
     L.vmc_hbm_read_probe.restype = _I
     L.vmc_hbm_read_probe.argtypes = [_P, _SZ, _I, _P, _P]
     L.vmc_selftest.restype = _I
@@ -278,15 +283,27 @@ def turboquant_decode_attention_noalloc(out, query, kv_cache, block_tables, seq_
     return out
 
 
+def flash_attention_prefill_workspace_size(num_tokens, num_kv_heads, head_dim=128):
+    return load().vmc_flash_attention_prefill_workspace_size(num_tokens, num_kv_heads, head_dim)
+
+
 def flash_attention_prefill(out, query, key, value, token_positions, num_kv_heads, scale,
                             key_cache=None, value_cache=None, slot_mapping=None, block_size=16,
-                            kv_format=KV_Q8_0, layout=LAYOUT_NHD, stream=None):
+                            kv_format=KV_Q8_0, layout=LAYOUT_NHD, stream=None, workspace=None):
+    """vmc_flash_attention_prefill; with a workspace (a uint8 device tensor of
+    at least flash_attention_prefill_workspace_size bytes),
+    vmc_flash_attention_prefill_ws (V^T tiles built once per call)."""
     T, Hq, D = query.shape
-    rc = load().vmc_flash_attention_prefill(
-        _ptr(out), _ptr(query), _ptr(key), _ptr(value), T, Hq, num_kv_heads, D, scale,
-        _ptr(token_positions), _dtype_code(query), _ptr(key_cache), _ptr(value_cache),
-        _ptr(slot_mapping), block_size, kv_format, layout, _stream(stream))
-    _check(rc, "vmc_flash_attention_prefill")
+    args = (_ptr(out), _ptr(query), _ptr(key), _ptr(value), T, Hq, num_kv_heads, D, scale,
+            _ptr(token_positions), _dtype_code(query), _ptr(key_cache), _ptr(value_cache),
+            _ptr(slot_mapping), block_size, kv_format, layout)
+    if workspace is None:
+        rc = load().vmc_flash_attention_prefill(*args, _stream(stream))
+        _check(rc, "vmc_flash_attention_prefill")
+    else:
+        rc = load().vmc_flash_attention_prefill_ws(*args, _ptr(workspace), workspace.numel() * workspace.element_size(),
+                                                   _stream(stream))
+        _check(rc, "vmc_flash_attention_prefill_ws")
     return out
 
 

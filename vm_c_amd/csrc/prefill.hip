@@ -86,6 +86,11 @@ struct PrefillParams {
     const int64_t* slots;
     int64_t bs, E, stride;
     int hnd;
+    // local K/V with a workspace: the V^T tiles of every 64-key tile of the
+    // step (vt_prep_kernel) and their exact-mode flags, vt_tiles per KV head
+    const uint8_t* vt;
+    const uint8_t* vt_flag;
+    int vt_tiles;
 };
 
 template <bool BF16>
@@ -159,7 +164,7 @@ __device__ __forceinline__ int wave_max_int(int v) {
 // workgroups.  Grid: query block (largest first) x KV head x head group.
 // BF16 is the type of the S MFMA and of V (paged: the page type; q8_0 /
 // q4_0 pages dequantize to fp16).
-template <bool BF16, int APPEND_FMT, int SRC>
+template <bool BF16, int APPEND_FMT, int SRC, bool VT>
 __global__ void __launch_bounds__(512, 1)
 prefill_kernel(PrefillParams p) {
     using M = MT<BF16>;
@@ -332,9 +337,21 @@ prefill_kernel(PrefillParams p) {
     const uint32_t lds_w = __builtin_amdgcn_readfirstlane(
         (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)&lds.tile[0][0][1024 * w]);
     constexpr uint32_t kSlotB = 2 * BN * 256, kPartB = BN * 256;
-    auto load_tile = [&](int t, auto slot_c) __attribute__((always_inline)) {
+    // prebuilt V^T tiles: wave w fetches bytes 2048 w .. + 2047 of the tile
+    // into the same bytes of the slot's V^T tile
+    const uint32_t vt_w = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)&lds.vtr[0][2048 * w]);
+    const uint32_t lane16 = 16u * (uint32_t)lane;
+    auto load_tile = [&](int t, auto slot_c, auto vt_c) __attribute__((always_inline)) {
         constexpr int SL = decltype(slot_c)::value;
+        constexpr bool FROM_VT = decltype(vt_c)::value;
         const int k0 = kv_lo + t * BN;
+        if constexpr (FROM_VT) {
+            // kv_lo is a multiple of BN here, so the tile is prebuilt tile k0 / BN
+            const uint8_t* src = p.vt + (((int64_t)g * p.vt_tiles + (k0 / BN)) << 14) + 2048 * wu;
+            dma16s(src, lane16, vt_w + SL * (uint32_t)(kD * BN * 2));
+            dma16s(src + 1024, lane16, vt_w + SL * (uint32_t)(kD * BN * 2) + 1024u);
+        }
         if constexpr (SRC == SRC_LOCAL) {
             if (k0 + BN <= kv_end) {  // uniform: every row of the tile in range
                 const int64_t toff = (int64_t)k0 * row_stride;
@@ -342,7 +359,7 @@ prefill_kernel(PrefillParams p) {
                 for (int i = 0; i < 2; ++i) {
                     const int64_t off = toff + (int64_t)(32 * i) * row_stride;
                     dma16s(kgu + off, ld_off, lds_w + SL * kSlotB + 8192u * i);
-                    dma16s(vgu + off, ld_off, lds_w + SL * kSlotB + kPartB + 8192u * i);
+                    if constexpr (!FROM_VT) dma16s(vgu + off, ld_off, lds_w + SL * kSlotB + kPartB + 8192u * i);
                 }
                 return;
             }
@@ -354,7 +371,7 @@ prefill_kernel(PrefillParams p) {
             if constexpr (SRC == SRC_LOCAL) {
                 const int64_t off = (int64_t)kk * row_stride;
                 dma16m(kg + off, lds_w + SL * kSlotB + 8192u * i);
-                dma16m(vg + off, lds_w + SL * kSlotB + kPartB + 8192u * i);
+                if constexpr (!FROM_VT) dma16m(vg + off, lds_w + SL * kSlotB + kPartB + 8192u * i);
             } else {
                 const int64_t off = (int64_t)page_at(min(k0 + 32 * i + 4 * wu, kv_end - 1)) * p.page_bytes +
                                     row_in_page(kk) + ld_col;
@@ -817,14 +834,18 @@ prefill_kernel(PrefillParams p) {
     // exit costs the common case registers.
     // q8_0 / q4_0 pages instead hold the next tile in registers while a
     // tile runs and dequantize it into its slot before that tile's barrier.
+    // With prebuilt V^T tiles (FROM_VT) the transfers bring the V^T tile
+    // instead of the raw V rows and there is no V^T pass; the exact mode was
+    // decided before the pass from the tiles' flags.
     static_assert(NSLOT == 3, "wait counts below assume three slots");
     constexpr bool kDma = SRC == SRC_LOCAL || SRC == SRC_PAGED;
-    auto run = [&](auto exact_c) __attribute__((always_inline)) {
+    auto run = [&](auto exact_c, auto vt_c) __attribute__((always_inline)) {
         constexpr bool EXACT = decltype(exact_c)::value;
+        constexpr bool FROM_VT = decltype(vt_c)::value;
         bool redo = false;
         if constexpr (kDma) {
-            load_tile(0, std::integral_constant<int, 0>{});
-            if (1 < ntile) load_tile(1, std::integral_constant<int, 1>{});
+            load_tile(0, std::integral_constant<int, 0>{}, vt_c);
+            if (1 < ntile) load_tile(1, std::integral_constant<int, 1>{}, vt_c);
         } else {
             issue_q(0);
         }
@@ -839,15 +860,15 @@ prefill_kernel(PrefillParams p) {
                     } else {
                         store_q(sc);
                     }
-                    if constexpr (!EXACT) v_transpose(sc);
+                    if constexpr (!EXACT && !FROM_VT) v_transpose(sc);
                     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-                    if constexpr (BF16 && !EXACT) {
+                    if constexpr (BF16 && !EXACT && !FROM_VT) {
                         const uint64_t wf = *reinterpret_cast<const uint64_t*>(lds.wide[S]);
                         redo |= (__builtin_amdgcn_readfirstlane((uint32_t)wf) |
                                  __builtin_amdgcn_readfirstlane((uint32_t)(wf >> 32))) != 0;
                     }
                     if constexpr (kDma) {
-                        if (t + 2 < ntile) load_tile(t + 2, std::integral_constant<int, (S + 2) % NSLOT>{});
+                        if (t + 2 < ntile) load_tile(t + 2, std::integral_constant<int, (S + 2) % NSLOT>{}, vt_c);
                     } else {
                         if (t + 1 < ntile) issue_q(t + 1);
                     }
@@ -859,7 +880,7 @@ prefill_kernel(PrefillParams p) {
         return redo;
     };
     auto run_pass = [&]() __attribute__((always_inline)) {
-        if (run(std::false_type{})) {
+        if (run(std::false_type{}, std::false_type{})) {
             if constexpr (BF16) {
                 __syncthreads();  // every wave is past its last read of the ring
                 // the pass's rows start over: O rows 8b + 4h + i, this lane's row
@@ -878,7 +899,7 @@ prefill_kernel(PrefillParams p) {
                     m_thr = kNegInf;
                     l_part = 0.0f;
                 }
-                run(std::true_type{});
+                run(std::true_type{}, std::false_type{});
             }
         }
     };
@@ -896,7 +917,29 @@ prefill_kernel(PrefillParams p) {
             wlo_min = wrow0 - p.pos[wrow0];
             wlo_max = wrow1 - p.pos[wrow1];
         }
-        run_pass();
+        // prebuilt V^T tiles serve a workgroup whose tiles start on a 64-key
+        // boundary; a workgroup whose sequence starts elsewhere transposes
+        // its own tiles
+        bool prebuilt = false;
+        if constexpr (VT) {
+            if ((kv_lo % BN) == 0) {
+                bool flagged = false;
+                const uint8_t* fl = p.vt_flag + (int64_t)g * p.vt_tiles + kv_lo / BN;
+                for (int t0 = 0; t0 < ntile; t0 += 64)
+                    flagged |= __ballot(t0 + lane < ntile && fl[t0 + lane] != 0) != 0;
+                // a flagged tile: bf16 runs the exact mode; fp16 (whose flag
+                // marks an inf or NaN, possibly in another sequence's rows of
+                // the tile) transposes its own rows, which stop at kv_end
+                if (!flagged) {
+                    run(std::false_type{}, std::true_type{});
+                    prebuilt = true;
+                } else if constexpr (BF16) {
+                    run(std::true_type{}, std::false_type{});
+                    prebuilt = true;
+                }
+            }
+        }
+        if (!prebuilt) run_pass();
     } else {
         // runs of rows of one sequence: every wave scans the workgroup's rows
         // and finds the same runs
@@ -978,25 +1021,100 @@ prefill_kernel(PrefillParams p) {
     }
 }
 
-template <bool BF16, int FMT, int SRC = SRC_LOCAL>
+// ---- V^T tiles of the local prefill, built once per (64-key tile, KV head)
+// rather than by every workgroup that reads the tile.  Tile tau of head g is
+// the byte image of prefill_kernel's LDS V^T tile: fp16 V[64 tau + 16c + 8a
+// + 4h + e][d] at byte d * 128 + 16 * ((2c + h) ^ ((d >> 1) & 7)) + 8a + 2e
+// (keys past the step: zero).  flag[g][tau] = 1 when some row of the tile
+// holds, for bf16 V, |v| >= 65536 or a NaN, or a value below 2^-17 and none
+// of 2^-8 or more (per row: every case the kernel's own pass flags for its
+// rows' groups is flagged); for fp16 V, an inf or NaN.
+template <bool BF16>
+__global__ void __launch_bounds__(256) vt_prep_kernel(const uint16_t* __restrict__ v, uint8_t* __restrict__ vt,
+                                                      uint8_t* __restrict__ flag, int T, int Hkv, int ntT) {
+    __shared__ alignas(16) uint16_t tl[BN][kD];
+    const int tau = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+    bool fl = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = tid + 256 * i;
+        const int r = c >> 4, cc = c & 15;  // row of the tile, 16-byte chunk of the row
+        const int k = BN * tau + r;
+        u32x4 w = {0u, 0u, 0u, 0u};
+        if (k < T) w = *reinterpret_cast<const u32x4*>(v + ((int64_t)k * Hkv + g) * kD + 8 * cc);
+        uint32_t mx = 0, mn1 = 0xffffu;
+        u16x2 amax = {0, 0}, amin1 = {0xffff, 0xffff};  // |bits|, |bits| - 1 (0 wraps)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const u16x2 a = __builtin_bit_cast(u16x2, w[e] & 0x7fff7fffu);
+            amax = __builtin_elementwise_max(amax, a);
+            amin1 = __builtin_elementwise_min(amin1, a - u16x2{1, 1});
+            if constexpr (BF16) {
+                const f16x2 hh = {(_Float16)__builtin_bit_cast(float, w[e] << 16),
+                                  (_Float16)__builtin_bit_cast(float, w[e] & 0xffff0000u)};
+                w[e] = __builtin_bit_cast(uint32_t, hh);
+            }
+        }
+        mx = max((uint32_t)amax[0], (uint32_t)amax[1]);
+        mn1 = min((uint32_t)amin1[0], (uint32_t)amin1[1]);
+        // a row's 16 chunks sit in lanes 16j .. 16j + 15
+#pragma unroll
+        for (int m = 1; m < 16; m <<= 1) {
+            mx = max(mx, (uint32_t)__shfl_xor((int)mx, m, kWave));
+            mn1 = min(mn1, (uint32_t)__shfl_xor((int)mn1, m, kWave));
+        }
+        // bf16 bit patterns: 0x477f = 65280 (largest below 2^16), 0x3700 =
+        // 2^-17, 0x3b80 = 2^-8; fp16: 0x7c00 = inf
+        if constexpr (BF16)
+            fl |= mx > 0x477fu || (mn1 < 0x36ffu && mx < 0x3b80u);
+        else
+            fl |= mx >= 0x7c00u;
+        *reinterpret_cast<u32x4*>(&tl[r][8 * cc]) = w;
+    }
+    const int any = __syncthreads_or(fl ? 1 : 0);
+    if (tid == 0) flag[(int64_t)g * ntT + tau] = any ? 1 : 0;
+    // the tile's 16 KB as 1024 chunks, chunk q = tid + 256 i (consecutive
+    // lanes, consecutive bytes): dim row d = q >> 3 at position q & 7, which
+    // holds logical chunk ci = (q & 7) ^ ((d >> 1) & 7)
+    uint8_t* out = vt + (((int64_t)g * ntT + tau) << 14);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int q = tid + 256 * i, d = q >> 3;
+        const int ci = (q & 7) ^ ((d >> 1) & 7), c = ci >> 1, h = ci & 1;
+        uint32_t x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = tl[16 * c + 8 * (u >> 2) + 4 * h + (u & 3)][d];
+        const u32x4 o = {x[0] | (x[1] << 16), x[2] | (x[3] << 16), x[4] | (x[5] << 16), x[6] | (x[7] << 16)};
+        *reinterpret_cast<u32x4*>(out + 16 * q) = o;
+    }
+}
+
+template <bool BF16, int FMT, int SRC = SRC_LOCAL, bool VT = false>
 int launch_prefill(PrefillParams& prm, hipStream_t stream) {
-    auto kern = prefill_kernel<BF16, FMT, SRC>;
+    auto kern = prefill_kernel<BF16, FMT, SRC, VT>;
     const int64_t grid = (int64_t)prm.ntiles * prm.Hkv * prm.hgroups;
     hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * NW), 0, stream, prm);
     VMC_LAUNCH_CHECK();
     return VMC_OK;
 }
 
-template <bool BF16>
+template <bool BF16, bool VT>
 int dispatch_fmt(PrefillParams& prm, int fmt, hipStream_t s) {
     switch (fmt) {
-        case -1: return launch_prefill<BF16, -1>(prm, s);
-        case VMC_KV_F16: return launch_prefill<BF16, VMC_KV_F16>(prm, s);
-        case VMC_KV_BF16: return launch_prefill<BF16, VMC_KV_BF16>(prm, s);
-        case VMC_KV_Q8_0: return launch_prefill<BF16, VMC_KV_Q8_0>(prm, s);
-        case VMC_KV_Q4_0: return launch_prefill<BF16, VMC_KV_Q4_0>(prm, s);
+        case -1: return launch_prefill<BF16, -1, SRC_LOCAL, VT>(prm, s);
+        case VMC_KV_F16: return launch_prefill<BF16, VMC_KV_F16, SRC_LOCAL, VT>(prm, s);
+        case VMC_KV_BF16: return launch_prefill<BF16, VMC_KV_BF16, SRC_LOCAL, VT>(prm, s);
+        case VMC_KV_Q8_0: return launch_prefill<BF16, VMC_KV_Q8_0, SRC_LOCAL, VT>(prm, s);
+        case VMC_KV_Q4_0: return launch_prefill<BF16, VMC_KV_Q4_0, SRC_LOCAL, VT>(prm, s);
         default: return VMC_EINVAL;
     }
+}
+
+// workspace of the local prefill's prebuilt V^T tiles: 16 KB per (64-key
+// tile, KV head), then one flag byte each
+size_t vt_workspace_bytes(int64_t num_tokens, int64_t num_kv_heads) {
+    const int64_t n = (num_tokens + BN - 1) / BN * num_kv_heads;
+    return (size_t)(n * (kD * BN * 2) + ((n + 255) & ~(int64_t)255));
 }
 
 // workgroup shape shared by the local and paged entry points
@@ -1149,13 +1267,13 @@ extern "C" int vmc_flash_attention_prefill_v2(void* output, const void* query, c
     }
 }
 
-extern "C" int vmc_flash_attention_prefill(void* output, const void* query, const void* key,
-                                           const void* value, int num_tokens, int num_heads,
-                                           int num_kv_heads, int head_dim, float scale,
-                                           const int32_t* token_positions, int dtype,
-                                           void* key_cache, void* value_cache,
-                                           const int64_t* slot_mapping, int64_t block_size,
-                                           int kv_format, int layout, vmc_stream_t stream) {
+namespace {
+// the local prefill; with a workspace (ws != NULL) the V^T tiles are built
+// once by vt_prep_kernel and the attention kernel fetches them
+int local_prefill(void* output, const void* query, const void* key, const void* value, int num_tokens,
+                  int num_heads, int num_kv_heads, int head_dim, float scale, const int32_t* token_positions,
+                  int dtype, void* key_cache, void* value_cache, const int64_t* slot_mapping, int64_t block_size,
+                  int kv_format, int layout, void* ws, size_t ws_bytes, vmc_stream_t stream) {
     if (generic_head_dim(head_dim)) {
         // head_dim 64 / 256: the append by vmc_reshape_and_cache, then one
         // wave per (token, query head) over this step's K/V
@@ -1218,5 +1336,54 @@ extern "C" int vmc_flash_attention_prefill(void* output, const void* query, cons
     }
     if ((int64_t)prm.ntiles * prm.Hkv * prm.hgroups > 0x7fffffffLL) return VMC_EINVAL;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    return dtype == VMC_DTYPE_BF16 ? dispatch_fmt<true>(prm, fmt, s) : dispatch_fmt<false>(prm, fmt, s);
+    const bool bf = dtype == VMC_DTYPE_BF16;
+    if (!ws) return bf ? dispatch_fmt<true, false>(prm, fmt, s) : dispatch_fmt<false, false>(prm, fmt, s);
+    if (ws_bytes < vt_workspace_bytes(num_tokens, num_kv_heads)) return VMC_ENOMEM;
+    if (((uintptr_t)ws & 15) != 0) return VMC_EINVAL;
+    const int ntT = (num_tokens + BN - 1) / BN;
+    prm.vt = reinterpret_cast<const uint8_t*>(ws);
+    prm.vt_flag = prm.vt + (int64_t)ntT * num_kv_heads * (kD * BN * 2);
+    prm.vt_tiles = ntT;
+    uint8_t* vt = reinterpret_cast<uint8_t*>(ws);
+    uint8_t* flag = vt + (int64_t)ntT * num_kv_heads * (kD * BN * 2);
+    const dim3 vgrid((unsigned)ntT, (unsigned)num_kv_heads);
+    if (bf)
+        hipLaunchKernelGGL(vt_prep_kernel<true>, vgrid, dim3(256), 0, s, prm.v, vt, flag, num_tokens, num_kv_heads, ntT);
+    else
+        hipLaunchKernelGGL(vt_prep_kernel<false>, vgrid, dim3(256), 0, s, prm.v, vt, flag, num_tokens, num_kv_heads,
+                           ntT);
+    VMC_LAUNCH_CHECK();
+    return bf ? dispatch_fmt<true, true>(prm, fmt, s) : dispatch_fmt<false, true>(prm, fmt, s);
+}
+}  // namespace
+
+extern "C" int vmc_flash_attention_prefill(void* output, const void* query, const void* key,
+                                           const void* value, int num_tokens, int num_heads,
+                                           int num_kv_heads, int head_dim, float scale,
+                                           const int32_t* token_positions, int dtype,
+                                           void* key_cache, void* value_cache,
+                                           const int64_t* slot_mapping, int64_t block_size,
+                                           int kv_format, int layout, vmc_stream_t stream) {
+    return local_prefill(output, query, key, value, num_tokens, num_heads, num_kv_heads, head_dim, scale,
+                         token_positions, dtype, key_cache, value_cache, slot_mapping, block_size, kv_format,
+                         layout, nullptr, 0, stream);
+}
+
+extern "C" size_t vmc_flash_attention_prefill_workspace_size(int num_tokens, int num_kv_heads, int head_dim) {
+    if (head_dim != kD || num_tokens <= 0 || num_kv_heads <= 0) return 0;
+    return vt_workspace_bytes(num_tokens, num_kv_heads);
+}
+
+extern "C" int vmc_flash_attention_prefill_ws(void* output, const void* query, const void* key,
+                                              const void* value, int num_tokens, int num_heads,
+                                              int num_kv_heads, int head_dim, float scale,
+                                              const int32_t* token_positions, int dtype, void* key_cache,
+                                              void* value_cache, const int64_t* slot_mapping,
+                                              int64_t block_size, int kv_format, int layout,
+                                              void* workspace, size_t workspace_bytes, vmc_stream_t stream) {
+    // head_dim 64 / 256 take no workspace (their kernel has no tiles)
+    if (head_dim == kD && num_tokens > 0 && !workspace) return VMC_EINVAL;
+    return local_prefill(output, query, key, value, num_tokens, num_heads, num_kv_heads, head_dim, scale,
+                         token_positions, dtype, key_cache, value_cache, slot_mapping, block_size, kv_format,
+                         layout, head_dim == kD ? workspace : nullptr, workspace_bytes, stream);
 }
