@@ -1032,7 +1032,9 @@ prefill_kernel(PrefillParams p) {
 template <bool BF16>
 __global__ void __launch_bounds__(256) vt_prep_kernel(const uint16_t* __restrict__ v, uint8_t* __restrict__ vt,
                                                       uint8_t* __restrict__ flag, int T, int Hkv, int ntT) {
-    __shared__ alignas(16) uint16_t tl[BN][kD];
+    // rows padded to 65 dwords: the 8 lanes that gather one dim from 8 rows
+    // of the tile hit 8 banks in pairs, not one bank
+    __shared__ alignas(16) uint16_t tl[BN][kD + 2];
     const int tau = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
     bool fl = false;
 #pragma unroll
@@ -1069,7 +1071,8 @@ __global__ void __launch_bounds__(256) vt_prep_kernel(const uint16_t* __restrict
             fl |= mx > 0x477fu || (mn1 < 0x36ffu && mx < 0x3b80u);
         else
             fl |= mx >= 0x7c00u;
-        *reinterpret_cast<u32x4*>(&tl[r][8 * cc]) = w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) *reinterpret_cast<uint32_t*>(&tl[r][8 * cc + 2 * e]) = w[e];
     }
     const int any = __syncthreads_or(fl ? 1 : 0);
     if (tid == 0) flag[(int64_t)g * ntT + tau] = any ? 1 : 0;
