@@ -773,7 +773,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(gbs_attn, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs_attn / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(),
-                     "kernel": "turboquant_decode_attention: tq_decode_kernel + "
+                     "kernel": "turboquant_decode_attention: tq_stream_kernel + "
                                "decode_merge_kernel (one operator, two launches)",
                      "ms": round(dec["ms_attn"], 4), "ms_median": round(dec["med_attn"], 4),
                      "launches_timed": dec["n_attn"], "bytes": dec["attn_bytes"],
@@ -787,7 +787,8 @@ def main():
     if others:
         line["decode_other_configs"] = others
     if pre is not None:
-        line["prefill"] = {"workload": "causal prefill B=4 S=4096 Hq=32 Hkv=8 bf16, fused q8_0 append",
+        line["prefill"] = {"workload": "causal prefill B=4 S=4096 Hq=32 Hkv=8 bf16, fused q8_0 append "
+                                       "(vmc_flash_attention_prefill_ws: vt_prep_kernel + prefill_kernel)",
                            "ms": round(pre["ms"], 4), "ms_median": round(pre["med"], 4),
                            "launches_timed": pre["n"], "tflops": round(pre["tflops"], 1),
                            "pct_peak_mfma_bf16": round(100 * pre["tflops"] / MFMA_BF16_PEAK_TFLOPS, 2)}
