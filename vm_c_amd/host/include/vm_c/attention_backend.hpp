@@ -71,7 +71,8 @@ public:
                         int num_kv_heads, int head_dim, float scale, int64_t block_size,
                         ScalarType dtype, hipStream_t stream) override;
 
-    // split-KV decode workspace (0 until ensure_workspace)
+    // split-KV decode workspace, also the local prefill's V^T tiles (0 until
+    // ensure_workspace)
     size_t workspace_size() const override { return ws_bytes_; }
     void ensure_workspace(int max_num_batched_tokens, int max_num_seqs, int num_attention_heads,
                           int num_kv_heads, int head_dim, int gpu_device) override;
@@ -120,6 +121,8 @@ private:
     TQBuffers buffers_;
     TQConfig config_;
     TQWorkspace workspace_;
+    void* prefill_ws_ = nullptr;  // the local prefill's V^T tiles (ensure_workspace)
+    size_t prefill_ws_bytes_ = 0;
     int gpu_device_;
     ScalarType activation_dtype_;
     int max_num_batched_tokens_ = 0;

@@ -60,6 +60,14 @@ void PagedAttentionBackend::forward_prefill(void* output, const void* query, con
     }
     require_no_cached_prefix(meta, "PagedAttentionBackend::forward_prefill");
     if (!key || !value) throw std::runtime_error("PagedAttentionBackend::forward_prefill: needs the step's K/V");
+    if (ws_ && vmc_flash_attention_prefill_workspace_size(meta.num_tokens, num_kv_heads, head_dim) <= ws_bytes_) {
+        // the step's V^T tiles built once in the workspace
+        VMC_CALL(vmc_flash_attention_prefill_ws(output, query, key, value, meta.num_tokens, num_heads, num_kv_heads,
+                                                head_dim, scale, meta.token_positions, vmc_dtype_of(dtype), nullptr,
+                                                nullptr, nullptr, 16, VMC_KV_F16, VMC_LAYOUT_NHD, ws_, ws_bytes_,
+                                                reinterpret_cast<vmc_stream_t>(stream)));
+        return;
+    }
     flash_attention_prefill_local(output, query, key, value, meta.num_tokens, num_heads, num_kv_heads,
                                   head_dim, scale, meta.token_to_seq, meta.token_positions, dtype, stream);
 }
@@ -92,13 +100,16 @@ void PagedAttentionBackend::forward_decode(void* output, const void* query, cons
 }
 
 // pre-sizes the split workspace for max_num_seqs requests of up to 32768
-// tokens (a batch that needs more runs one pass per request, without it)
+// tokens (a batch that needs more runs one pass per request, without it),
+// and the local prefill's V^T tiles for max_num_batched_tokens tokens (the
+// same buffer: prefill and decode calls are ordered on the stream)
 void PagedAttentionBackend::ensure_workspace(int max_num_batched_tokens, int max_num_seqs,
                                              int num_attention_heads, int num_kv_heads,
                                              int head_dim, int gpu_device) {
-    (void)max_num_batched_tokens;
-    const size_t need = vmc_paged_decode_workspace_size(max_num_seqs, num_attention_heads, num_kv_heads,
-                                                        head_dim, 32768 / 16, 16, 0);
+    const size_t need = std::max(vmc_paged_decode_workspace_size(max_num_seqs, num_attention_heads, num_kv_heads,
+                                                                 head_dim, 32768 / 16, 16, 0),
+                                 vmc_flash_attention_prefill_workspace_size(max_num_batched_tokens, num_kv_heads,
+                                                                            head_dim));
     if (need <= ws_bytes_) return;
     HIP_CHECK(hipSetDevice(gpu_device));
     if (ws_) HIP_CHECK(hipFree(ws_));
@@ -129,6 +140,7 @@ TurboQuantBackend::TurboQuantBackend(int head_dim, const std::string& quant_meth
 TurboQuantBackend::~TurboQuantBackend() {
     buffers_.free_buf();
     workspace_.free_buf();
+    if (prefill_ws_) (void)hipFree(prefill_ws_);
 }
 
 // attention_backend.cpp:120-136: the decode workspace for max_num_seqs
@@ -145,6 +157,16 @@ void TurboQuantBackend::ensure_workspace(int max_num_batched_tokens, int max_num
     head_dim_ = head_dim;
     workspace_.ensure_decode(max_num_seqs, num_attention_heads, num_kv_heads, head_dim,
                              int64_t{1} << 26, 16, config_.max_num_kv_splits, gpu_device);
+    // the local prefill's V^T tiles for max_num_batched_tokens tokens
+    const size_t pneed = vmc_flash_attention_prefill_workspace_size(max_num_batched_tokens, num_kv_heads, head_dim);
+    if (pneed > prefill_ws_bytes_) {
+        HIP_CHECK(hipSetDevice(gpu_device));
+        if (prefill_ws_) HIP_CHECK(hipFree(prefill_ws_));
+        prefill_ws_ = nullptr;
+        prefill_ws_bytes_ = 0;
+        HIP_CHECK(hipMalloc(&prefill_ws_, pneed));
+        prefill_ws_bytes_ = pneed;
+    }
 }
 
 void TurboQuantBackend::store_kv(const void* key, const void* value, void* key_cache,
@@ -176,6 +198,14 @@ void TurboQuantBackend::forward_prefill(void* output, const void* query, const v
         return;
     }
     require_no_cached_prefix(meta, "TurboQuantBackend::forward_prefill");
+    if (prefill_ws_ &&
+        vmc_flash_attention_prefill_workspace_size(meta.num_tokens, num_kv_heads, head_dim) <= prefill_ws_bytes_) {
+        VMC_CALL(vmc_flash_attention_prefill_ws(output, query, key, value, meta.num_tokens, num_heads, num_kv_heads,
+                                                head_dim, scale, meta.token_positions, vmc_dtype_of(dtype), nullptr,
+                                                nullptr, nullptr, 16, VMC_KV_F16, VMC_LAYOUT_NHD, prefill_ws_,
+                                                prefill_ws_bytes_, reinterpret_cast<vmc_stream_t>(stream)));
+        return;
+    }
     flash_attention_prefill_local(output, query, key, value, meta.num_tokens, num_heads, num_kv_heads,
                                   head_dim, scale, meta.token_to_seq, meta.token_positions, dtype, stream);
 }
@@ -195,6 +225,6 @@ void TurboQuantBackend::forward_decode(void* output, const void* query, const vo
                                 config_.max_num_kv_splits, stream, dtype);
 }
 
-size_t TurboQuantBackend::workspace_size() const { return workspace_.decode_bytes; }
+size_t TurboQuantBackend::workspace_size() const { return workspace_.decode_bytes + prefill_ws_bytes_; }
 
 }  // namespace vm_c
