@@ -29,6 +29,10 @@ struct DecodeParams {
     int per_seq;         // 1: one workgroup per sequence
     int pps_min, max_splits;
     int grid;            // page ranges (flat) or sequences (per-sequence mode)
+    // weighted split (flat mode with all grid ranges in use): ranges below
+    // split_h take split_wa parts of the pages each, the others split_wb
+    // (split_h 0: even ranges)
+    int split_h, split_wa, split_wb;
     int hgroups, hpw;    // KV-head groups per page (one workgroup each), heads per group
     int row_bytes;       // TurboQuant: one token's entries, all KV heads (Hkv * slot)
     int lds_pad;         // staged NHD pages: token rows padded in LDS (row a whole number of chunks)
@@ -144,6 +148,28 @@ __device__ __forceinline__ int effective_wgs(const DecodeParams& p, int T, int g
 // workgroup whose range holds global page g: floor(((g + 1) n - 1) / T)
 __device__ __forceinline__ int wg_of_page(int64_t g, int n, int T) {
     return (int)(((g + 1) * n - 1) / T);
+}
+
+// first page of range w of n: T w / n, or with the weighted split
+// T C(w) / C(n), C(x) = wa min(x, h) + wb max(0, x - h)
+__device__ __forceinline__ int range_lo(const DecodeParams& p, int w, int n, int T) {
+    if (p.split_h <= 0 || n != p.grid) return (int)((int64_t)w * T / n);
+    const int64_t h = p.split_h;
+    const int64_t cw = (int64_t)p.split_wa * min((int64_t)w, h) + (int64_t)p.split_wb * max((int64_t)0, (int64_t)w - h);
+    const int64_t cn = (int64_t)p.split_wa * min((int64_t)n, h) + (int64_t)p.split_wb * max((int64_t)0, (int64_t)n - h);
+    return (int)((int64_t)T * cw / cn);
+}
+
+// range holding global page g under range_lo's split
+__device__ __forceinline__ int range_of_page(const DecodeParams& p, int64_t g, int n, int T) {
+    if (p.split_h <= 0 || n != p.grid) return wg_of_page(g, n, T);
+    int a = 0, z = n - 1;  // the last range starting at or before g
+    while (a < z) {
+        const int mid = (a + z + 1) >> 1;
+        if (range_lo(p, mid, n, T) <= g) a = mid;
+        else z = mid - 1;
+    }
+    return a;
 }
 
 struct WGPlan {
@@ -267,7 +293,7 @@ __global__ void __launch_bounds__(1024) decode_merge_kernel(DecodeParams p) {
         return;
     }
     const int n = effective_wgs(p, T, p.grid);
-    const int w0 = wg_of_page(ps, n, T), w1 = wg_of_page(ps + pg - 1, n, T);
+    const int w0 = range_of_page(p, ps, n, T), w1 = range_of_page(p, ps + pg - 1, n, T);
     if (w0 == w1) return;  // written by its workgroup
     const int nseg = w1 - w0 + 1;
     const int64_t rs = (int64_t)p.Hq * kPartRow;

@@ -150,8 +150,8 @@ __global__ void __launch_bounds__(512, 4) tq_stream_kernel(DecodeParams p) {
         } else {
             const int T = total_pages(p, lane);
             const int n = effective_wgs(p, T, nranges);
-            wp.p_lo = w < n ? (int)((int64_t)w * T / n) : 0;
-            wp.p_hi = w < n ? (int)((int64_t)(w + 1) * T / n) : 0;
+            wp.p_lo = w < n ? range_lo(p, w, n, T) : 0;
+            wp.p_hi = w < n ? range_lo(p, w + 1, n, T) : 0;
             wp.first_b = wp.last_b = -1;
             wp.first_cut = wp.last_cut = 0;
         }
@@ -662,6 +662,15 @@ int launch_tq_stream(DecodeParams& prm, hipStream_t stream) {
     prm.hpw = SG::hpg;
     prm.hgroups = 1;
     prm.grid = prm.per_seq ? prm.B : tq_stream_ranges(prm.B, prm.Hkv, prm.max_blocks, prm.max_splits, num_cus());
+    // With two workgroups on every CU, workgroups w and w + CUs share one,
+    // and the first, dispatched ahead, wins the instruction issue: on the
+    // ragged 32k batch it ended at 111-121 us median against 147-158 us for
+    // its partner, which then ran alone.  It takes 5 of 8 parts of the pair's
+    // pages (both then end together: 164.9 against 167.7 us per call).
+    const int cus = num_cus();
+    prm.split_h = !prm.per_seq && prm.grid == 2 * cus ? cus : 0;
+    prm.split_wa = 5;
+    prm.split_wb = 3;
     hipLaunchKernelGGL((tq_stream_kernel<KB, VB, BF>), dim3(prm.grid), dim3(64 * SG::hpg), 0, stream, prm);
     VMC_LAUNCH_CHECK();
     if (!prm.per_seq) {
