@@ -160,16 +160,15 @@ __device__ __forceinline__ int range_lo(const DecodeParams& p, int w, int n, int
     return (int)((int64_t)T * cw / cn);
 }
 
-// range holding global page g under range_lo's split
+// range holding global page g under range_lo's split: the last w with
+// floor(T C(w) / C(n)) <= g, i.e. with C(w) <= K = floor(((g + 1) C(n) - 1) / T)
 __device__ __forceinline__ int range_of_page(const DecodeParams& p, int64_t g, int n, int T) {
     if (p.split_h <= 0 || n != p.grid) return wg_of_page(g, n, T);
-    int a = 0, z = n - 1;  // the last range starting at or before g
-    while (a < z) {
-        const int mid = (a + z + 1) >> 1;
-        if (range_lo(p, mid, n, T) <= g) a = mid;
-        else z = mid - 1;
-    }
-    return a;
+    const int64_t h = min((int64_t)p.split_h, (int64_t)n), wa = p.split_wa, wb = p.split_wb;
+    const int64_t cn = wa * h + wb * ((int64_t)n - h);
+    const int64_t K = ((g + 1) * cn - 1) / T;
+    const int64_t w = K < wa * h ? K / wa : h + (K - wa * h) / wb;
+    return (int)min(w, (int64_t)n - 1);
 }
 
 struct WGPlan {

@@ -666,7 +666,8 @@ int launch_tq_stream(DecodeParams& prm, hipStream_t stream) {
     // and the first, dispatched ahead, wins the instruction issue: on the
     // ragged 32k batch it ended at 111-121 us median against 147-158 us for
     // its partner, which then ran alone.  It takes 5 of 8 parts of the pair's
-    // pages (both then end together: 164.9 against 167.7 us per call).
+    // pages: both then end together, and the kernel took 155.0 against
+    // 160.2 us (162.4-164.7 against 169.4-170.9 us per call, one box).
     const int cus = num_cus();
     prm.split_h = !prm.per_seq && prm.grid == 2 * cus ? cus : 0;
     prm.split_wa = 5;
