@@ -624,7 +624,16 @@ __global__ void __launch_bounds__(512, 4) tq_stream_kernel(DecodeParams p) {
             dma_page(blk_of(2 * k), buf, 0);
             if (2 * k + 1 < npc) dma_page(blk_of(2 * k + 1), buf, 1);
         };
-        if (npairs > 0) issue_pair(0, 0);
+        // q of the slice's first sequence before any transfer is in flight:
+        // its loads' wait (vmcnt) would otherwise also wait for them
+        if (npairs > 0) {
+            const int b0 = __builtin_amdgcn_readfirstlane(lds.info[0]) >> 6;
+            if (b0 != cur_b) {
+                load_q(b0);
+                cur_b = b0;
+            }
+            issue_pair(0, 0);
+        }
         for (int k0 = 0; k0 < npairs; k0 += 2) {
             static_for<2>([&](auto pc) __attribute__((always_inline)) {
                 constexpr int P = decltype(pc)::value;
