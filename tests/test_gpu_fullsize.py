@@ -102,3 +102,31 @@ def test_tq3_ragged_32k(dev):
     ex = O.tq_decode_exact(qb, cache, bt, lens, 8, 1 / np.sqrt(D), BS, L, c)
     ok, err = close_report(got, ex, ATOL, RTOL)
     assert ok, f"vs exact: max err {err}"
+
+
+def test_tq3_many_sequence_switches(dev):
+    """3-bit slots, 160 sequences whose page ranges cross many sequence
+    starts: a tenth empty, a seventh shorter than a page pair, the rest
+    log-uniform in [1024, 16384] tokens, four of 32768 (seed 5; ~48k pages,
+    so the range split also counts every sequence switch as pages).  Every
+    row against the two-stage restatement, the non-empty ones against fp64
+    exact attention; empty sequences give zero rows."""
+    rng = np.random.default_rng(5)
+    B = 160
+    lens = np.exp(rng.uniform(np.log(1024), np.log(16384), B)).astype(np.int64)
+    kind = rng.random(B)
+    lens[kind < 0.1] = 0
+    short = (kind >= 0.1) & (kind < 0.25)
+    lens[short] = rng.integers(1, 40, int(short.sum()))
+    lens[:4] = 32768
+    lens = lens.astype(np.int32)
+    got, qb, cache, bt, L, c = _run(dev, "turboquant_3bit_nc", lens, 64, 8, 5)
+    print(f"turboquant_3bit_nc: {int(((lens + BS - 1) // BS).sum())} pages, oracle decode of {B} rows", flush=True)
+    ref = O.f16_to_f32(O.tq_decode(qb, cache, bt, lens, 8, np.float32(1 / np.sqrt(D)), BS, L, c))
+    ok, err = close_report(got, ref, ATOL, RTOL)
+    assert ok, f"vs restatement: max err {err}"
+    assert np.all(got[lens == 0] == 0.0)
+    nz = lens > 0
+    ex = O.tq_decode_exact(qb[nz], cache, bt[nz], lens[nz], 8, 1 / np.sqrt(D), BS, L, c)
+    ok, err = close_report(got[nz], ex, ATOL, RTOL)
+    assert ok, f"vs exact: max err {err}"

@@ -31,8 +31,11 @@ struct DecodeParams {
     int grid;            // page ranges (flat) or sequences (per-sequence mode)
     // weighted split (flat mode with all grid ranges in use): ranges below
     // split_h take split_wa parts of the pages each, the others split_wb
-    // (split_h 0: even ranges)
-    int split_h, split_wa, split_wb;
+    // (split_h 0: even ranges).  With the weighted split, each sequence
+    // start after the first also counts as split_v pages (what a workgroup
+    // spends switching sequences: the last piece's rows, the next q, a pair
+    // computed twice), so that ranges holding a switch get fewer pages
+    int split_h, split_wa, split_wb, split_v;
     int hgroups, hpw;    // KV-head groups per page (one workgroup each), heads per group
     int row_bytes;       // TurboQuant: one token's entries, all KV heads (Hkv * slot)
     int lds_pad;         // staged NHD pages: token rows padded in LDS (row a whole number of chunks)
@@ -171,6 +174,63 @@ __device__ __forceinline__ int range_of_page(const DecodeParams& p, int64_t g, i
     return (int)min(w, (int64_t)n - 1);
 }
 
+__device__ __forceinline__ int plan_wave_sum(int v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+__device__ __forceinline__ int plan_wave_max(int v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = max(v, __shfl_xor(v, m, 64));
+    return v;
+}
+
+// pages and non-empty sequences of the batch (one wave, results in every lane)
+__device__ __forceinline__ void batch_pages(const DecodeParams& p, int lane, int* T_out, int* nz_out) {
+    int total = 0, nz = 0;
+    for (int b0 = 0; b0 < p.B; b0 += 64) {
+        int L = 0;
+        int pg = b0 + lane < p.B ? seq_pages(p, b0 + lane, &L) : 0;
+        total += plan_wave_sum(pg);
+        nz += __popcll(__ballot(pg > 0));
+    }
+    *T_out = total;
+    *nz_out = nz;
+}
+
+// pages a sequence switch counts as under range_lo's split (0: none).  Only
+// with the weighted split, and only when the ranges are long against it (an
+// empty range then never falls inside a sequence's pieces).
+__device__ __forceinline__ int switch_pages(const DecodeParams& p, int n, int T) {
+    return p.split_h > 0 && n == p.grid && p.split_v > 0 && (int64_t)T >= (int64_t)8 * p.split_v * n ? p.split_v : 0;
+}
+
+// The page axis with V pages inserted before every non-empty sequence but
+// the first: sequence b of rank r (non-empty sequences before it) starting
+// at page ps holds virtual pages ps + V r ..; range boundaries are placed on
+// this axis (range_lo over T + V (nz - 1)), and a boundary inside an
+// inserted gap moves to the start of the sequence after it.  Real pages of
+// the virtual boundaries v0 and v1 (one wave, results in every lane).
+__device__ __forceinline__ void real_pages(const DecodeParams& p, int lane, int V, int v0, int v1, int* r0,
+                                           int* r1) {
+    int carry = 0, carry_nz = 0, best0 = 0, best1 = 0;
+    for (int b0 = 0; b0 < p.B; b0 += 64) {
+        const int b = b0 + lane;
+        int L = 0;
+        const int pg = b < p.B ? seq_pages(p, b, &L) : 0;
+        const int nzf = pg > 0 ? 1 : 0;
+        const int incl = wave_incl_scan(pg, lane), incl_nz = wave_incl_scan(nzf, lane);
+        const int ps = carry + incl - pg, rank = carry_nz + incl_nz - nzf;
+        const int vs = ps + V * rank, gs = vs - (rank > 0 ? V : 0);
+        if (pg > 0 && gs <= v0) best0 = max(best0, v0 < vs ? ps : min(ps + (v0 - vs), ps + pg));
+        if (pg > 0 && gs <= v1) best1 = max(best1, v1 < vs ? ps : min(ps + (v1 - vs), ps + pg));
+        carry += __shfl(incl, 63, 64);
+        carry_nz += __shfl(incl_nz, 63, 64);
+    }
+    *r0 = plan_wave_max(best0);
+    *r1 = plan_wave_max(best1);
+}
+
 struct WGPlan {
     int p_lo, p_hi;        // global page range
     int first_b, last_b;   // sequences holding p_lo and p_hi - 1
@@ -264,35 +324,44 @@ __global__ void __launch_bounds__(1024) decode_merge_kernel(DecodeParams p) {
     const int b = blockIdx.x, g = blockIdx.y;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int hq = g * p.G + wave;
-    __shared__ int sh[3];
+    __shared__ int sh[5];
     if (wave == 0) {
-        int carry = 0, ps_b = 0, pg_b = 0;
+        int carry = 0, carry_nz = 0, ps_b = 0, pg_b = 0, rank_b = 0;
         for (int b0 = 0; b0 < p.B; b0 += 64) {
             int L = 0;
             const int pg = b0 + lane < p.B ? seq_pages(p, b0 + lane, &L) : 0;
-            const int incl = wave_incl_scan(pg, lane);
+            const int nzf = pg > 0 ? 1 : 0;
+            const int incl = wave_incl_scan(pg, lane), incl_nz = wave_incl_scan(nzf, lane);
             if (b0 + lane == b) {
                 ps_b = carry + incl - pg;
                 pg_b = pg;
+                rank_b = carry_nz + incl_nz - nzf;
             }
             carry += __shfl(incl, 63, 64);
+            carry_nz += __shfl(incl_nz, 63, 64);
         }
         // the lane that held b publishes it
         if (lane == (b & 63)) {
             sh[0] = ps_b;
             sh[1] = pg_b;
             sh[2] = carry;
+            sh[3] = rank_b;
+            sh[4] = carry_nz;
         }
     }
     __syncthreads();
-    const int ps = sh[0], pg = sh[1], T = sh[2];
+    const int ps = sh[0], pg = sh[1], T = sh[2], rank = sh[3], nz = sh[4];
     uint16_t* orow = reinterpret_cast<uint16_t*>(p.out) + ((int64_t)b * p.Hq + hq) * kD;
     if (pg == 0) {
         reinterpret_cast<uint32_t*>(orow)[lane] = 0u;
         return;
     }
     const int n = effective_wgs(p, T, p.grid);
-    const int w0 = range_of_page(p, ps, n, T), w1 = range_of_page(p, ps + pg - 1, n, T);
+    // pages on range_lo's axis (switch_pages: V pages before each sequence
+    // after the first)
+    const int V = switch_pages(p, n, T);
+    const int Tv = T + V * max(nz - 1, 0), vs = ps + V * rank;
+    const int w0 = range_of_page(p, vs, n, Tv), w1 = range_of_page(p, vs + pg - 1, n, Tv);
     if (w0 == w1) return;  // written by its workgroup
     const int nseg = w1 - w0 + 1;
     const int64_t rs = (int64_t)p.Hq * kPartRow;

@@ -148,10 +148,20 @@ __global__ void __launch_bounds__(512, 4) tq_stream_kernel(DecodeParams p) {
             const int pg = seq_pages(p, w, &L);
             wp = {ps, ps + pg, w, w, 0, 0};
         } else {
-            const int T = total_pages(p, lane);
+            int T = 0, nz = 0;
+            batch_pages(p, lane, &T, &nz);
             const int n = effective_wgs(p, T, nranges);
-            wp.p_lo = w < n ? range_lo(p, w, n, T) : 0;
-            wp.p_hi = w < n ? range_lo(p, w + 1, n, T) : 0;
+            // boundaries on the axis where a sequence switch counts as V pages
+            const int V = switch_pages(p, n, T);
+            const int Tv = T + V * max(nz - 1, 0);
+            const int v_lo = w < n ? range_lo(p, w, n, Tv) : 0;
+            const int v_hi = w < n ? range_lo(p, w + 1, n, Tv) : 0;
+            if (V > 0) {
+                real_pages(p, lane, V, v_lo, v_hi, &wp.p_lo, &wp.p_hi);
+            } else {
+                wp.p_lo = v_lo;
+                wp.p_hi = v_hi;
+            }
             wp.first_b = wp.last_b = -1;
             wp.first_cut = wp.last_cut = 0;
         }
@@ -681,6 +691,12 @@ int launch_tq_stream(DecodeParams& prm, hipStream_t stream) {
     prm.split_h = !prm.per_seq && prm.grid == 2 * cus ? cus : 0;
     prm.split_wa = 5;
     prm.split_wb = 3;
+    // A range that holds a sequence switch (the last piece's rows, the next
+    // sequence's q loaded and rotated, the pair across the boundary computed
+    // twice) took ~7 us longer on the ragged 32k batch, and the 20 slowest of
+    // 256 CUs all held one.  Counting each switch as 8 pages evens that out:
+    // 166.0 against 167.9 us per call (one box, three alternations).
+    prm.split_v = 8;
     hipLaunchKernelGGL((tq_stream_kernel<KB, VB, BF>), dim3(prm.grid), dim3(64 * SG::hpg), 0, stream, prm);
     VMC_LAUNCH_CHECK();
     if (!prm.per_seq) {
