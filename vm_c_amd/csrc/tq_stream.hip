@@ -133,6 +133,25 @@ __global__ void __launch_bounds__(512, 4) tq_stream_kernel(DecodeParams p) {
     const int nranges = p.grid;
     const int w = (int)blockIdx.x;
 
+    // key table: entry e (codes c0 | c1 << KB) = fp16(C[c0]) | fp16(C[c1]) << 16
+    // at LDS words (e << lut_log2c) + copy.  Built by waves 1.. while wave 0
+    // plans, four words (copies of one entry) per 16-byte write.
+    static_assert(SG::lut_log2c >= 2, "a 16-byte group holds copies of one entry");
+    if (wave != 0) {
+        for (int i = tid - 64; i < SG::lut_words / 4; i += 64 * (hpg - 1)) {
+            const int e = (4 * i) >> SG::lut_log2c;
+            const int c0 = e & ((1 << KB) - 1), c1 = e >> KB;
+            float a = 0.0f, b = 0.0f;
+#pragma unroll
+            for (int c = 0; c < (1 << KB); ++c) {
+                a = c == c0 ? p.tab.centroids[c] : a;
+                b = c == c1 ? p.tab.centroids[c] : b;
+            }
+            const uint32_t v = (uint32_t)f32_to_f16_bits(a) | ((uint32_t)f32_to_f16_bits(b) << 16);
+            reinterpret_cast<u32x4*>(lds.lut)[i] = u32x4{v, v, v, v};
+        }
+    }
+
     // ---- this workgroup's page range (paged_decode.hip's plan)
     if (wave == 0) {
         WGPlan wp;
@@ -187,32 +206,22 @@ __global__ void __launch_bounds__(512, 4) tq_stream_kernel(DecodeParams p) {
         return;
     }
 
-    // key table: entry e (codes c0 | c1 << KB) = fp16(C[c0]) | fp16(C[c1]) << 16
-    // at LDS words (e << lut_log2c) + copy
-    auto lut_entry = [&](int e) -> uint32_t {
-        const int c0 = e & ((1 << KB) - 1), c1 = e >> KB;
-        float a = 0.0f, b = 0.0f;
-#pragma unroll
-        for (int c = 0; c < (1 << KB); ++c) {
-            a = c == c0 ? p.tab.centroids[c] : a;
-            b = c == c1 ? p.tab.centroids[c] : b;
-        }
-        return (uint32_t)f32_to_f16_bits(a) | ((uint32_t)f32_to_f16_bits(b) << 16);
-    };
-    for (int i = tid; i < SG::lut_words; i += 64 * hpg) lds.lut[i] = lut_entry(i >> SG::lut_log2c);
-
     // ---- Q operand: lane (r16, grp) reads dims 32 grp + 8 j + e of head qh
     // (columns c and c + 8 both hold head c), rotated (H q / sqrt(d)), from
     // the wave's LDS copy, one j at a time (no registers held across pairs)
     u32x4 (&qop)[4][4][8] = lds.qop[wave];
     auto q_at = [&](int j) -> AT { return __builtin_bit_cast(AT, qop[j][grp][qh]); };
     auto load_q = [&](int b) __attribute__((always_inline)) {
+        // lane (r16, grp) rotates dims 32 grp + 16 hf .. + 15 of head qh
+        // (hf = r16 / 8: the two lanes of a head's column pair split the
+        // lane group's 32 dims) and writes their two 8-dim operand words
+        const int hf = r16 >> 3;
         const int64_t qrow = ((int64_t)b * p.Hq + hq0 + qh) * kD;
-        float y[32];
+        float y[16];
         if (q_ok) {
-            const u32x4* src = reinterpret_cast<const u32x4*>(p.q + qrow + 32 * grp);
+            const u32x4* src = reinterpret_cast<const u32x4*>(p.q + qrow + 32 * grp + 16 * hf);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
+            for (int c = 0; c < 2; ++c) {
                 const u32x4 wv = src[c];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -222,38 +231,40 @@ __global__ void __launch_bounds__(512, 4) tq_stream_kernel(DecodeParams p) {
             }
         } else {
 #pragma unroll
-            for (int e = 0; e < 32; ++e) y[e] = 0.0f;
+            for (int e = 0; e < 16; ++e) y[e] = 0.0f;
         }
-        // Walsh-Hadamard: half-widths 1..16 inside the lane, 32 and 64 across
-        // the lane groups (dim bit 32 = grp bit 0, dim bit 64 = grp bit 1)
+        // Walsh-Hadamard: half-widths 1..8 inside the lane, 16 across the
+        // column pair (dim bit 16 = r16 bit 3: a row rotation by 8 lanes), 32
+        // and 64 across the lane groups (grp bits 0 and 1).  The upper element
+        // of a butterfly becomes partner - own: fma(-1, own, partner), exact.
 #pragma unroll
-        for (int hw = 1; hw < 32; hw <<= 1)
+        for (int hw = 1; hw < 16; hw <<= 1)
 #pragma unroll
-            for (int i = 0; i < 32; i += 2 * hw)
+            for (int i = 0; i < 16; i += 2 * hw)
 #pragma unroll
                 for (int j = i; j < i + hw; ++j) {
                     const float a = y[j], c = y[j + hw];
                     y[j] = a + c;
                     y[j + hw] = a - c;
                 }
+        const float s8 = hf ? -1.0f : 1.0f, s16 = (grp & 1) ? -1.0f : 1.0f, s32 = (grp & 2) ? -1.0f : 1.0f;
 #pragma unroll
-        for (int e = 0; e < 32; ++e) {
-            const float o = shfl_xor(y[e], 16);
-            y[e] = (grp & 1) ? o - y[e] : y[e] + o;
+        for (int e = 0; e < 16; ++e) {
+            const float o = __builtin_bit_cast(
+                float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, y[e]), 0x128, 0xf, 0xf, false));
+            y[e] = __builtin_fmaf(s8, y[e], o);
         }
 #pragma unroll
-        for (int e = 0; e < 32; ++e) {
-            const float o = shfl_xor(y[e], 32);
-            y[e] = (grp & 2) ? o - y[e] : y[e] + o;
-        }
-        // (lanes r16 and r16 + 8 write the same head's words)
+        for (int e = 0; e < 16; ++e) y[e] = __builtin_fmaf(s16, y[e], shfl_xor(y[e], 16));
+#pragma unroll
+        for (int e = 0; e < 16; ++e) y[e] = __builtin_fmaf(s32, y[e], shfl_xor(y[e], 32));
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int jj = 0; jj < 2; ++jj) {
             AT v;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = (_Float16)__fmul_rn(y[8 * j + e], p.tab.rot_c);
-            qop[j][grp][qh] = __builtin_bit_cast(u32x4, v);
+            for (int e = 0; e < 8; ++e) v[e] = (_Float16)__fmul_rn(y[8 * jj + e], p.tab.rot_c);
+            qop[2 * hf + jj][grp][qh] = __builtin_bit_cast(u32x4, v);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
