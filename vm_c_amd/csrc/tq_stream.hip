@@ -527,15 +527,17 @@ __global__ void __launch_bounds__(512, 4) tq_stream_kernel(DecodeParams p) {
         z_part += zsum;
         // O += P . V: row h < 8 takes k = 8 grp + i from column h (first page,
         // token 4 grp + i) and k = 8 grp + 4 + i from column h + 8 (second
-        // page; a row rotation by 8 lanes brings it over), rows 8-15 are zero,
-        // so O rows 0-7 sum both pages; the V operand of output chunk c is its
+        // page; a row rotation by 8 lanes brings it over), so O rows 0-7 sum
+        // both pages.  Rows 8-15 take the same columns the other way round:
+        // their O rows are never read, and the rows of a product do not mix,
+        // so they need no zeroing.  The V operand of output chunk c is its
         // code field masked where it lies (an fp16 subnormal
         // code * 2^(shift - 24), kVShift)
         const u32x2 pw2 = __builtin_bit_cast(u32x2, pw);
-        const uint32_t pb0 = dpp_u32<0x128>(pw2[0]), pb1 = dpp_u32<0x128>(pw2[1]);  // row_ror:8
-        const bool lo_row = r16 < 8;
-        const AT pa = __builtin_bit_cast(AT, u32x4{lo_row ? pw2[0] : 0u, lo_row ? pw2[1] : 0u, lo_row ? pb0 : 0u,
-                                                   lo_row ? pb1 : 0u});
+        // row_ror:8 (every lane has a source, so no old value is kept)
+        const uint32_t pb0 = (uint32_t)__builtin_amdgcn_mov_dpp((int)pw2[0], 0x128, 0xf, 0xf, false);
+        const uint32_t pb1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)pw2[1], 0x128, 0xf, 0xf, false);
+        const AT pa = __builtin_bit_cast(AT, u32x4{pw2[0], pw2[1], pb0, pb1});
         // value code words of tokens 4 grp + i (both pages), dims 8 r16 .. + 7
         uint32_t cw2[2][4][2];
 #pragma unroll
