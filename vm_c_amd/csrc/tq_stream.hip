@@ -699,7 +699,7 @@ int launch_tq_stream(DecodeParams& prm, hipStream_t stream) {
     // ragged 32k batch it ended at 111-121 us median against 147-158 us for
     // its partner, which then ran alone.  It takes 5 of 8 parts of the pair's
     // pages: both then end together, and the kernel took 155.0 against
-    // 160.2 us (162.4-164.7 against 169.4-170.9 us per call, one box).
+    // 160.2 us (162.4-164.7 against 169.4-170.9 us per call, the same GPU).
     const int cus = num_cus();
     prm.split_h = !prm.per_seq && prm.grid == 2 * cus ? cus : 0;
     prm.split_wa = 5;
@@ -708,7 +708,7 @@ int launch_tq_stream(DecodeParams& prm, hipStream_t stream) {
     // sequence's q loaded and rotated, the pair across the boundary computed
     // twice) took ~7 us longer on the ragged 32k batch, and the 20 slowest of
     // 256 CUs all held one.  Counting each switch as 8 pages evens that out:
-    // 166.0 against 167.9 us per call (one box, three alternations).
+    // 166.0 against 167.9 us per call (the same GPU, three alternations).
     prm.split_v = 8;
     hipLaunchKernelGGL((tq_stream_kernel<KB, VB, BF>), dim3(prm.grid), dim3(64 * SG::hpg), 0, stream, prm);
     VMC_LAUNCH_CHECK();
